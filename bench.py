@@ -1,0 +1,255 @@
+#!/usr/bin/env python3
+"""Benchmark: blockwise-sparse NF4 MLP decode, one 405B-shaped layer per step.
+
+A step is one decode token through one layer's hot path: the learned-basis
+router (exact fp16 dots + top-k with lowest-index ties) and the fused NF4
+sparse MLP over the selected blocks, read straight from the HBM slot table.
+Steps rotate over --layers distinct seeded layers (default 8, ~12 GB) so that
+the 256 MB Infinity Cache cannot serve a layer's 191 MB of selected blocks.
+
+Reported (one JSON line):
+  value         decode_tok_s = 1e6 / (126 * us_per_layer), MLP-only (router +
+                sparse MLP per layer, 126 layers per token)
+  ms_per_step   wall time per layer (router + MLP), inputs resident in HBM
+  roofline      the sparse-MLP decode kernels (gate/up + down) timed with HIP
+                events on the launch stream: algorithmic bytes per launch
+                (selected packed NF4 + fp32 absmax + x + out) / duration
+  cpu_baseline  the oracle's restatement of the reference PyTorch path
+                (router + dequant fallback with fp16 rounding points) on the
+                host cores, on the same layer shape
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+METRIC = "sparse-MLP µs/layer + HBM GB/s vs peak, 405B shape top-k 208; decode_tok_s"
+PEAK_GBS = 8000.0
+MODEL_LAYERS = 126
+# config id -> (hidden, intermediate, basis rank, top-k)
+CONFIGS = {1: (4096, 14336, 64, 64), 2: (16384, 53248, 64, 208)}
+WORKLOADS = {
+    1: "8B-shaped MLP layer decode: hidden 4096, intermediate 14336, block 32 (448 blocks), top-k 64",
+    2: "405B-shaped MLP layer decode: hidden 16384, intermediate 53248, block 32 (1664 blocks), top-k 208",
+}
+
+
+def algorithmic_bytes(H: int, k: int, qbs: int) -> int:
+    """Bytes the sparse MLP must move once per layer: the selected blocks'
+    packed NF4 (gate, up: 32 x H/2; down: H x 16) and fp32 absmax
+    (gate, up: 32 x H/qbs; down: H, one per row and block), plus x and out."""
+    per_block = 2 * (32 * H // 2 + 4 * 32 * H // qbs) + (16 * H + 4 * H)
+    return k * per_block + 2 * H * 2
+
+
+def router_bytes(H: int, R: int, NB: int) -> int:
+    return 2 * (R * H + R + NB * R + NB + H)
+
+
+def host_threads() -> int:
+    try:
+        n = len(os.sched_getaffinity(0))
+    except AttributeError:
+        n = os.cpu_count() or 1
+    return max(1, min(16, n))
+
+
+def cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def cpu_baseline(layer, sel, runs: int, H: int, I: int, k: int, qbs: int) -> dict:
+    """Time the oracle's restatement of the reference PyTorch path (router +
+    dequant fallback over the gathered blocks) on the host cores."""
+    import numpy as np
+    import torch
+
+    from oracle import oracle as orc
+
+    threads = host_threads()
+    orc.set_num_threads(threads)
+
+    def u16(t):
+        return t.detach().cpu().contiguous().view(torch.int16).numpy().view(np.uint16)
+
+    def npy(t):
+        return t.detach().cpu().contiguous().numpy()
+
+    sel_np = npy(sel).astype(np.int64)
+    gp, ga = orc.gather_rows_blocks(npy(layer.gate_packed), npy(layer.gate_absmax), sel_np, H, qbs)
+    upk, ua = orc.gather_rows_blocks(npy(layer.up_packed), npy(layer.up_absmax), sel_np, H, qbs)
+    t = layer.table
+    dp = npy(t.down_packed)[sel_np].transpose(1, 0, 2).copy()  # block-major -> the reference's [H, k, 16]
+    da = npy(t.down_absmax)[sel_np].T.copy()
+    x16, ew, eb, sw, sb = (u16(v) for v in (layer.x, layer.enc_w, layer.enc_b, layer.score_w, layer.score_b))
+    al = np.arange(k, dtype=np.int32).reshape(1, k)
+
+    def one():
+        orc.route(x16, ew, eb, sw, sb, k)
+        orc.sparse_mlp(x16.reshape(1, H), al, gp, ga, upk, ua, dp, da, qbs=qbs, want_exact=False, want_fallback=True)
+
+    one()  # warm-up
+    times = []
+    for _ in range(max(1, runs)):
+        t0 = time.perf_counter()
+        one()
+        times.append(time.perf_counter() - t0)
+    us = statistics.median(times) * 1e6
+    return {
+        "value": round(1e6 / (MODEL_LAYERS * us), 6),
+        "unit": "tok/s",
+        "us_per_layer": round(us, 1),
+        "gbs": round(algorithmic_bytes(H, k, qbs) / (us * 1e-6) / 1e9, 3),
+        "cores": threads,
+        "kind": "port",
+        "cpu": cpu_model(),
+        "sample": f"1 layer (router + dequant-fallback MLP over {k} pre-gathered blocks, fp16 rounding points, "
+                  f"fp64 accumulation), median of {len(times)} runs after 1 warm-up, {threads} OpenMP threads",
+    }
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--config", type=int, default=2, choices=sorted(CONFIGS))
+    ap.add_argument("--layers", type=int, default=8, help="distinct layers rotated over the steps")
+    ap.add_argument("--cpu-runs", type=int, default=5)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py runs on one GPU only; --gpus {args.gpus} is not supported (this path has no "
+              "multi-GPU mode: see the sharding note in DESIGN.md)", file=sys.stderr)
+        return 2
+
+    import torch
+
+    from next_step_ai_amd.synth import make_synthetic_layer
+
+    device = torch.device("cuda", 0)
+    torch.cuda.set_device(device)
+    H, I, R, k = CONFIGS[args.config]
+    qbs = 64
+    t_gen = time.perf_counter()
+    layers = []
+    for l in range(args.layers):
+        L = make_synthetic_layer(H=H, I=I, R=R, seed=1000 * args.config + l, device=device)
+        L.table = L.slot_table(drop_reference_down=True)
+        from next_step_ai_amd.slot_table import SparseMlpLayer
+
+        L.mlp = SparseMlpLayer(L.router(), L.table, k)
+        layers.append(L)
+    torch.cuda.synchronize()
+    t_gen = time.perf_counter() - t_gen
+    print(f"[bench] generated {args.layers} layers H={H} I={I} k={k} in {t_gen:.1f}s", file=sys.stderr, flush=True)
+
+    outs = [torch.empty(H, dtype=torch.float16, device=device) for _ in layers]
+    sels = [torch.empty(k, dtype=torch.int32, device=device) for _ in layers]
+    ws = None
+    from next_step_ai_amd._runtime import workspace
+
+    ws = workspace(layers[0].mlp.workspace_bytes(), device)
+    n = len(layers)
+    for i in range(args.warmup):
+        j = i % n
+        layers[j].mlp.forward(layers[j].x, out=outs[j], sel_out=sels[j], ws=ws)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        j = i % n
+        layers[j].mlp.forward(layers[j].x, out=outs[j], sel_out=sels[j], ws=ws)
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    us_per_layer = (t1 - t0) / args.steps * 1e6
+    print(f"[bench] {args.steps} steps: {us_per_layer:.2f} us/layer (router + MLP)", file=sys.stderr, flush=True)
+
+    # Sparse-MLP kernels alone, timed with HIP events on the launch stream.
+    for j in range(n):
+        layers[j].table.decode(layers[j].x, sels[j], out=outs[j])
+    torch.cuda.synchronize()
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(args.steps)]
+    for i in range(args.steps):
+        j = i % n
+        ev[i][0].record()
+        layers[j].table.decode(layers[j].x, sels[j], out=outs[j])
+        ev[i][1].record()
+    torch.cuda.synchronize()
+    mlp_ms = [a.elapsed_time(b) for a, b in ev]
+    mlp_us = statistics.mean(mlp_ms) * 1e3
+    # Router alone (route kernels), same method.
+    from next_step_ai_amd.router import route_tokens
+
+    rdicts = [L.routing_dict(k) for L in layers]
+    for j in range(n):
+        route_tokens(layers[j].x.reshape(1, H), rdicts[j], k, sorted_by_score=False)
+    torch.cuda.synchronize()
+    rev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(args.steps)]
+    for i in range(args.steps):
+        j = i % n
+        rev[i][0].record()
+        route_tokens(layers[j].x.reshape(1, H), rdicts[j], k, sorted_by_score=False)
+        rev[i][1].record()
+    torch.cuda.synchronize()
+    route_us = statistics.mean(a.elapsed_time(b) for a, b in rev) * 1e3
+
+    abytes = algorithmic_bytes(H, k, qbs)
+    achieved = abytes / (mlp_us * 1e-6) / 1e9
+    result = {
+        "metric": METRIC,
+        "value": round(1e6 / (MODEL_LAYERS * us_per_layer), 3),
+        "unit": "tok/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(us_per_layer / 1e3, 6),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic",
+        "config": {
+            "workload": WORKLOADS[args.config] + f"; NF4 qbs {qbs} with fp32 absmax; all blocks HBM-resident; "
+                        f"{args.layers} rotating seeded layers; batch 1 fp16 token",
+            "hidden": H, "intermediate": I, "basis_rank": R, "top_k": k, "block": 32, "quant_block": qbs,
+            "rotating_layers": args.layers,
+        },
+        "us_per_layer": round(us_per_layer, 3),
+        "sparse_mlp_us": round(mlp_us, 3),
+        "router_us": round(route_us, 3),
+        "decode_tok_s_126_layers": round(1e6 / (MODEL_LAYERS * us_per_layer), 3),
+        "algorithmic_bytes_per_layer": abytes,
+        "router_bytes_per_layer": router_bytes(H, R, I // 32),
+        "roofline": {
+            "bound": "hbm",
+            "achieved": round(achieved, 2),
+            "peak": PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(achieved / PEAK_GBS, 4),
+            "traffic": None,
+            "kernels": "k_gate_up + k_down (one sparse-MLP decode launch pair)",
+        },
+    }
+    if not args.no_cpu_baseline:
+        result["cpu_baseline"] = cpu_baseline(layers[0], sels[0], args.cpu_runs, H, I, k, qbs)
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,247 @@
+/*
+ * nsmlp.h -- C ABI of the MI355X-native blockwise-sparse NF4 MLP decode path.
+ *
+ * Plain C: device pointers, sizes and an opaque HIP stream (void*).  Every
+ * function returns 0 on success or a negative status (NSMLP_E*); the message
+ * of the last failure on the calling thread is returned by nsmlp_last_error().
+ * No function synchronises the stream, allocates device memory behind the
+ * caller's back, or copies its inputs: the caller provides every buffer,
+ * including the workspace (sized by the *_workspace_bytes functions and
+ * zero-initialised once with nsmlp_workspace_init).  One workspace serves one
+ * stream at a time; calls that share a workspace on different streams race.
+ *
+ * Reference interfaces replaced (paths relative to the reference repository;
+ * TSM = llama3_neuroplastic/triton_sparse_mlp.py,
+ * RT  = llama3_neuroplastic/experiments/streaming_llama_runtime.py).
+ *
+ * Layout conventions (the reference's bitsandbytes NF4 format):
+ *   an [out, in] weight is flattened row-major; byte e/2 holds elements
+ *   (e, e+1) with the even element in the HIGH nibble; one fp32 absmax per
+ *   qbs consecutive elements; code[16] maps a nibble to its NF4 value.
+ *   Sparse block b of the intermediate dimension is rows [32b, 32b+32) of
+ *   gate/up and columns [32b, 32b+32) of down.
+ *   "Slot" storage (the HBM hot-block table) is block-major:
+ *     gate/up packed [slots][32][H/2] u8,  absmax [slots][32][H/qbs] f32
+ *     down    packed [slots][H][16]  u8,   absmax [slots][H] f32
+ */
+#ifndef NSMLP_H
+#define NSMLP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define NSMLP_OK 0
+#define NSMLP_EINVAL (-22)   /* bad shape / argument                    */
+#define NSMLP_ENOSPC (-28)   /* workspace too small                     */
+#define NSMLP_EHIP (-5)      /* HIP runtime or launch error             */
+#define NSMLP_ENODEV (-19)   /* no usable gfx950 device                 */
+
+#define NSMLP_ROUTE_SORTED 1     /* sel in (score desc, index asc) order (torch.topk order) */
+#define NSMLP_ROUTE_LEGACY_ABS 2 /* scores = |latent| . score_w, no bias, no clamp (RT:4332-4334) */
+
+#define NSMLP_DOWN_BLOCK_MAJOR 0 /* down blocks as [n][H][16], absmax [n][H]          */
+#define NSMLP_DOWN_GATHERED 1    /* down blocks as [H][n][16], absmax [H][n] (RT:4491) */
+
+/* Message of the last failing call on this thread ("" if none). */
+const char* nsmlp_last_error(void);
+
+/* ABI version (major*100 + minor). */
+int nsmlp_version(void);
+
+/* 1 if device `device` is a gfx950 GPU usable by this library, else 0. */
+int nsmlp_device_supported(int device);
+
+/* Zero the counter region of a workspace; call once after allocating it. */
+int nsmlp_workspace_init(void* ws, size_t ws_bytes, void* stream);
+
+/* ------------------------------------------------------------------ router
+ * Replaces RT:4311-4352 (_route_sparse_mlp) together with RT:4209-4238
+ * (_compute_sparse_basis_latent), for `rows` tokens:
+ *   latent = fp16(x . enc_w[r] + enc_b[r]); if basis_top_k < R keep the
+ *   basis_top_k largest |latent| (ties: lowest index), zero the rest;
+ *   score  = max(fp16(latent . score_w[j] + score_b[j]), 0)
+ *            (NSMLP_ROUTE_LEGACY_ABS: fp16(|latent| . score_w[j]));
+ *   if down_block_norm: score = fp16(score * down_block_norm[j]);
+ *   sel[t] = the k largest scores, ties broken by the lowest block index,
+ *   in ascending block order (the order of the reference's ordered_blocks,
+ *   RT:4873) or, with NSMLP_ROUTE_SORTED, in (score desc, index asc) order.
+ * Every dot product is computed exactly and rounded once to fp16 (RNE), so
+ * the selection does not depend on summation order.
+ * x [rows][H], enc_w [R][H], enc_b [R] (nullable), score_w [NB][R],
+ * score_b [NB] (nullable), down_block_norm [NB] fp16 (nullable): fp16.
+ * latent_out [rows][R] / scores_out [rows][NB] fp16, nullable.
+ * Limits: H <= 65535, R <= 1024, NB <= 65535, 1 <= k <= NB.
+ */
+size_t nsmlp_route_workspace_bytes(int rows, int H, int R, int NB, int k);
+int nsmlp_route_f16(const void* x, int rows, int H, const void* enc_w, const void* enc_b, int R, int basis_top_k,
+                    const void* score_w, const void* score_b, const void* down_block_norm, int NB, int flags, int k,
+                    int32_t* sel, void* latent_out, void* scores_out, void* ws, size_t ws_bytes, void* stream);
+
+/* ------------------------------------------------- fused decode (M = 1)
+ * One token through the blockwise-sparse MLP over the selected blocks:
+ *   y = sum_{b in sel} Wd[:, b] (silu(Wg_b x) * (Wu_b x))   (fp32 inside, one fp16 rounding)
+ * Replaces the gather + dispatch of RT:5104-5524 (_sparse_mlp_forward_fast)
+ * for a decode token: block b is read from its HBM slot lookup[b] when
+ * lookup[b] >= 0 and from the host-resident copy (block-major, indexed by b)
+ * otherwise, with no host round trip (RT:4867) and no gathered copy
+ * (RT:3644-3702).
+ */
+typedef struct nsmlp_slot_table {
+  int H;            /* hidden size (gate/up in, down out)              */
+  int I;            /* intermediate size (NB * 32)                     */
+  int qbs;          /* NF4 quant block size (multiple of 32, divides H) */
+  int n_slots;      /* HBM slots                                        */
+  const int32_t* lookup;             /* [NB] slot of block b, -1 = not resident; NULL = identity */
+  const uint8_t* gate_packed;        /* [n_slots][32][H/2] */
+  const float* gate_absmax;          /* [n_slots][32][H/qbs] */
+  const uint8_t* up_packed;
+  const float* up_absmax;
+  const uint8_t* down_packed;        /* [n_slots][H][16] */
+  const float* down_absmax;          /* [n_slots][H] */
+  /* Host-resident copy of every block (pinned, device-accessible pointers),
+   * same block-major layout indexed by block id; NULL when all selected
+   * blocks are resident. */
+  const uint8_t* host_gate_packed;
+  const float* host_gate_absmax;
+  const uint8_t* host_up_packed;
+  const float* host_up_absmax;
+  const uint8_t* host_down_packed;
+  const float* host_down_absmax;
+  const float* code;                 /* [16] NF4 code book (device) */
+  const void* down_bias;             /* [H] fp16 or NULL */
+} nsmlp_slot_table;
+
+size_t nsmlp_decode_workspace_bytes(int H, int k);
+int nsmlp_decode_slots_f16(const nsmlp_slot_table* table, const void* x, const int32_t* sel, int k, void* out,
+                           void* ws, size_t ws_bytes, void* stream);
+
+/* Router + fused decode for one decode token (the decode branch of
+ * RT:5833-5923 _mlp_forward_dispatch: route, then sparse MLP), entirely on
+ * the device.  sel_out [k] receives the selected blocks in ascending order. */
+typedef struct nsmlp_router {
+  int R;
+  int basis_top_k;
+  int NB;
+  int flags;                 /* NSMLP_ROUTE_LEGACY_ABS or 0 */
+  const void* enc_w;         /* [R][H] fp16 */
+  const void* enc_b;         /* [R] fp16 or NULL */
+  const void* score_w;       /* [NB][R] fp16 */
+  const void* score_b;       /* [NB] fp16 or NULL */
+  const void* down_block_norm; /* [NB] fp16 or NULL */
+} nsmlp_router;
+
+size_t nsmlp_layer_workspace_bytes(int H, int R, int NB, int k);
+int nsmlp_decode_layer_f16(const nsmlp_router* router, const nsmlp_slot_table* table, const void* x, int k,
+                           int32_t* sel_out, void* out, void* ws, size_t ws_bytes, void* stream);
+
+/* --------------------------------------- reference-signature entry points
+ * Replaces TSM:1378-1509 (triton_sparse_mlp_decode_4bit_single_kernel_sm75):
+ * x [H] fp16; gathered gate/up packed [top_k][32][H/2] u8 with absmax
+ * [top_k][32][H/qbs] f32; down packed [H][top_k][16] u8 with absmax
+ * [H][top_k] f32; code tables [16] f32 (one per projection); out [H] fp16.
+ * out_accum [>= H] f32 receives the fp32 result before rounding (the
+ * reference's scratch, TSM:1476-1508).  block_size must be 32.
+ */
+size_t nsmlp_single_kernel_workspace_bytes(int H, int top_k);
+int nsmlp_single_kernel_decode_f16(const void* x, const uint8_t* gate_packed, const float* gate_absmax,
+                                   const float* gate_code, const uint8_t* up_packed, const float* up_absmax,
+                                   const float* up_code, const uint8_t* down_packed, const float* down_absmax,
+                                   const float* down_code, void* out, float* out_accum, int H, int block_size,
+                                   int qbs, int top_k, void* ws, size_t ws_bytes, void* stream);
+
+/* Replaces TSM:1519-1585 (triton_fused_sparse_mlp_decode_4bit) for one row,
+ * as RT:5651-5675 calls it: the two gate/up output linears, silu * up and the
+ * down input linear fused into the two decode kernels (fp32 inside, one fp16
+ * rounding).  x [H] fp16; active_idx [kk] int32 slots in 0..A-1 (< 0 are
+ * skipped; a slot listed twice is counted twice by the down projection, as
+ * in the reference's input linear); flat_mask [A*32] fp16 (nullable = 1);
+ * gate/up packed [A*32][H] NF4 (absmax per qbs elements) with biases [A*32]
+ * fp16 (nullable); down packed [H][A*32] NF4 with quant block 32 (absmax
+ * [H][A]) and down_bias [H] fp16 (nullable); out [H] fp16.
+ */
+size_t nsmlp_fused_decode_workspace_bytes(int H, int kk);
+int nsmlp_fused_decode_gathered_f16(const void* x, int H, const int32_t* active_idx, int kk, int A,
+                                    const void* flat_mask, const uint8_t* gate_packed, const float* gate_absmax,
+                                    const float* gate_code, const void* gate_bias, const uint8_t* up_packed,
+                                    const float* up_absmax, const float* up_code, const void* up_bias,
+                                    const uint8_t* down_packed, const float* down_absmax, const float* down_code,
+                                    const void* down_bias, int qbs, void* out, void* ws, size_t ws_bytes,
+                                    void* stream);
+
+/* Replaces TSM:1340-1375 (triton_sparse_output_linear_4bit) with row-major
+ * NF4 semantics (the reference's Triton kernel indexes a transposed payload,
+ * TSM:634-635; this computes what its callers pass, RT:4630-4660):
+ *   out[t][s*32 + j] = (sum_c W[s*32 + j][c] x[t][c] + bias[s*32 + j]) * flat_mask[t][s*32 + j]
+ * for every slot s listed in active_idx[t] (entries < 0 are skipped), and
+ * 0 elsewhere.  W [A*32][in_dim] NF4 (absmax per qbs elements), x [rows][in_dim],
+ * flat_mask [rows][A*32] fp16 (nullable = 1), bias [A*32] fp16 (nullable),
+ * active_idx [rows][kk] int32, out [rows][A*32] fp16.
+ */
+size_t nsmlp_output_linear_workspace_bytes(int rows, int kk, int in_dim);
+int nsmlp_output_linear_nf4_f16(const void* x, int rows, int in_dim, const int32_t* active_idx, int kk, int A,
+                                const void* flat_mask, const uint8_t* packed, const float* absmax, const float* code,
+                                int qbs, const void* bias, int block_size, void* out, void* ws, size_t ws_bytes,
+                                void* stream);
+
+/* Replaces TSM:1303-1337 (triton_sparse_input_linear_4bit) with row-major
+ * NF4 semantics (RT:5651-5675 passes the gathered down weight [H][A*32] with
+ * quant block 32, i.e. absmax [H][A]):
+ *   out[t][o] = sum_{s in active_idx[t]} sum_j W[o][s*32 + j] x[t][s*32 + j] + bias[o]
+ * W [out_features][in_features] NF4 (absmax per qbs elements),
+ * x [rows][in_features], out [rows][out_features] fp16.
+ */
+int nsmlp_input_linear_nf4_f16(const void* x, int rows, int in_features, const int32_t* active_idx, int kk,
+                               const uint8_t* packed, const float* absmax, const float* code, int qbs,
+                               int out_features, const void* bias, int block_size, void* out, void* stream);
+
+/* silu(gate) * up elementwise in fp32, rounded to fp16 (TSM:1577-1578). */
+int nsmlp_silu_mul_f16(const void* gate, const void* up, void* out, long long n, void* stream);
+
+/* ----------------------------------------------------- slot-table helpers
+ * Row-block gather (gate/up): dst block i = src block blocks[i], i.e. the
+ * byte range [b*32*in/2, (b+1)*32*in/2) and absmax range [b*32*in/qbs, ...)
+ * of the row-major weight (RT:4530-4578, RT:2722-2786).  src_blocks is the
+ * number of blocks in the source; ids outside [0, src_blocks) leave their
+ * destination block untouched (likewise ids >= in/32 for the down gather).
+ */
+int nsmlp_gather_row_blocks(const uint8_t* src_packed, const float* src_absmax, int src_blocks,
+                            const int32_t* blocks, int n, int in_features, int qbs, uint8_t* dst_packed,
+                            float* dst_absmax, void* stream);
+
+/* Down-proj column gather (RT:4455-4528 _load_down_proj_cold_cols,
+ * RT:2619-2720): for block b, bytes src[o][16b .. 16b+16) and absmax
+ * src_absmax[o][(32b)/qbs] of the row-major [out][in] weight, written
+ * block-major ([n][out][16], [n][out]) or gathered ([out][n][16], [out][n]). */
+int nsmlp_gather_down_columns(const uint8_t* src_packed, const float* src_absmax, const int32_t* blocks, int n,
+                              int out_features, int in_features, int qbs, int dst_layout, uint8_t* dst_packed,
+                              float* dst_absmax, void* stream);
+
+/* Device-side address of pinned host memory (hipHostMalloc'd, e.g. a torch
+ * pinned tensor) for the slot table's host_* pointers: misses are read by the
+ * kernels directly over the host link (the reference stages them through
+ * pinned buffers and H2D copies, RT:3437-3493, safetensor_loader.py:172-201). */
+int nsmlp_host_device_pointer(const void* host, void** device_ptr);
+
+/* -------------------------------------------------------- synthetic data
+ * Seeded synthetic weights for benchmarks (counter-based; the value of
+ * element i depends only on (seed, i)):
+ *   nsmlp_synth_normal_f16: out[i] = fp16(std * N(0,1)).
+ *   nsmlp_synth_nf4:        w[i] = std * N(0,1) quantised to NF4 (absmax per qbs).
+ *   nsmlp_nf4_quantize_f32: NF4 quantisation of given fp32 values (the
+ *   restated bitsandbytes nf4 algorithm: nearest code by midpoint thresholds,
+ *   even element in the high nibble; an all-zero block stores code 7).
+ */
+int nsmlp_synth_normal_f16(uint64_t seed, long long n, float std, void* out, void* stream);
+int nsmlp_synth_nf4(uint64_t seed, long long n, int qbs, float std, uint8_t* packed, float* absmax, void* stream);
+int nsmlp_nf4_quantize_f32(const float* w, long long n, int qbs, uint8_t* packed, float* absmax, void* stream);
+int nsmlp_synth_normal_f32(uint64_t seed, long long n, float std, float* out, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* NSMLP_H */

@@ -1,0 +1,123 @@
+"""ctypes binding of ``libnsmlp.so`` (declared in include/nsmlp.h).
+
+The library is built in-tree by ``python -m next_step_ai_amd.build_lib``.
+There is no fallback: if the library is missing or fails to load, every
+entry point raises ``RuntimeError``.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import threading
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "libnsmlp.so")
+
+_lock = threading.Lock()
+_lib: ctypes.CDLL | None = None
+
+P = ctypes.c_void_p
+I32 = ctypes.c_int
+I64 = ctypes.c_longlong
+U64 = ctypes.c_uint64
+F32 = ctypes.c_float
+SZ = ctypes.c_size_t
+
+NSMLP_ROUTE_SORTED = 1
+NSMLP_ROUTE_LEGACY_ABS = 2
+NSMLP_DOWN_BLOCK_MAJOR = 0
+NSMLP_DOWN_GATHERED = 1
+
+
+class SlotTable(ctypes.Structure):
+    """Mirror of ``nsmlp_slot_table``."""
+
+    _fields_ = [
+        ("H", I32), ("I", I32), ("qbs", I32), ("n_slots", I32),
+        ("lookup", P),
+        ("gate_packed", P), ("gate_absmax", P),
+        ("up_packed", P), ("up_absmax", P),
+        ("down_packed", P), ("down_absmax", P),
+        ("host_gate_packed", P), ("host_gate_absmax", P),
+        ("host_up_packed", P), ("host_up_absmax", P),
+        ("host_down_packed", P), ("host_down_absmax", P),
+        ("code", P),
+        ("down_bias", P),
+    ]
+
+
+class Router(ctypes.Structure):
+    """Mirror of ``nsmlp_router``."""
+
+    _fields_ = [
+        ("R", I32), ("basis_top_k", I32), ("NB", I32), ("flags", I32),
+        ("enc_w", P), ("enc_b", P), ("score_w", P), ("score_b", P), ("down_block_norm", P),
+    ]
+
+
+# name -> (restype, argtypes)
+SIGNATURES: dict[str, tuple] = {
+    "nsmlp_last_error": (ctypes.c_char_p, []),
+    "nsmlp_version": (I32, []),
+    "nsmlp_device_supported": (I32, [I32]),
+    "nsmlp_workspace_init": (I32, [P, SZ, P]),
+    "nsmlp_route_workspace_bytes": (SZ, [I32, I32, I32, I32, I32]),
+    "nsmlp_route_f16": (I32, [P, I32, I32, P, P, I32, I32, P, P, P, I32, I32, I32, P, P, P, P, SZ, P]),
+    "nsmlp_decode_workspace_bytes": (SZ, [I32, I32]),
+    "nsmlp_decode_slots_f16": (I32, [ctypes.POINTER(SlotTable), P, P, I32, P, P, SZ, P]),
+    "nsmlp_layer_workspace_bytes": (SZ, [I32, I32, I32, I32]),
+    "nsmlp_decode_layer_f16": (I32, [ctypes.POINTER(Router), ctypes.POINTER(SlotTable), P, I32, P, P, P, SZ, P]),
+    "nsmlp_single_kernel_workspace_bytes": (SZ, [I32, I32]),
+    "nsmlp_single_kernel_decode_f16": (I32, [P, P, P, P, P, P, P, P, P, P, P, P, I32, I32, I32, I32, P, SZ, P]),
+    "nsmlp_fused_decode_workspace_bytes": (SZ, [I32, I32]),
+    "nsmlp_fused_decode_gathered_f16": (I32, [P, I32, P, I32, I32, P, P, P, P, P, P, P, P, P, P, P, P, P, I32, P, P, SZ, P]),
+    "nsmlp_output_linear_workspace_bytes": (SZ, [I32, I32, I32]),
+    "nsmlp_output_linear_nf4_f16": (I32, [P, I32, I32, P, I32, I32, P, P, P, P, I32, P, I32, P, P, SZ, P]),
+    "nsmlp_input_linear_nf4_f16": (I32, [P, I32, I32, P, I32, P, P, P, I32, I32, P, I32, P, P]),
+    "nsmlp_silu_mul_f16": (I32, [P, P, P, I64, P]),
+    "nsmlp_gather_row_blocks": (I32, [P, P, I32, P, I32, I32, I32, P, P, P]),
+    "nsmlp_gather_down_columns": (I32, [P, P, P, I32, I32, I32, I32, I32, P, P, P]),
+    "nsmlp_host_device_pointer": (I32, [P, ctypes.POINTER(P)]),
+    "nsmlp_synth_normal_f16": (I32, [U64, I64, F32, P, P]),
+    "nsmlp_synth_normal_f32": (I32, [U64, I64, F32, P, P]),
+    "nsmlp_synth_nf4": (I32, [U64, I64, I32, F32, P, P, P]),
+    "nsmlp_nf4_quantize_f32": (I32, [P, I64, I32, P, P, P]),
+}
+
+
+def lib() -> ctypes.CDLL:
+    """Load the library once; raise RuntimeError when it is not built."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is not None:
+            return _lib
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(
+                f"{LIB_PATH} is missing: build it with `python -m next_step_ai_amd.build_lib` "
+                "(there is no CPU fallback)"
+            )
+        handle = ctypes.CDLL(LIB_PATH)
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(handle, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = handle
+    return _lib
+
+
+def last_error() -> str:
+    msg = lib().nsmlp_last_error()
+    return msg.decode("utf-8", "replace") if msg else ""
+
+
+def check(rc: int, what: str) -> None:
+    if rc != 0:
+        raise RuntimeError(f"{what} failed (status {rc}): {last_error()}")
+
+
+def call(name: str, *args) -> None:
+    """Call a status-returning entry point; raise RuntimeError on failure."""
+    rc = getattr(lib(), name)(*args)
+    check(int(rc), name)

@@ -1,0 +1,630 @@
+// C ABI of the nsmlp library: argument validation, workspace carving and
+// kernel launches.  Declarations and the reference interfaces each entry
+// point replaces are in include/nsmlp.h.
+#include <stdarg.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+
+#include <mutex>
+
+#include "nsmlp_internal.h"
+
+namespace nsmlp {
+
+namespace {
+
+thread_local char g_err[512] = "";
+
+constexpr size_t kAlign = 256;
+// Fixed counter region at the start of every workspace (zeroed once by
+// nsmlp_workspace_init, restored to zero by the kernels that use it).
+constexpr size_t kStatusOff = 0;
+constexpr size_t kBlkCountOff = 256;
+constexpr int kMaxK = 32768;
+constexpr size_t kRowCountOff = kBlkCountOff + (size_t)kMaxK * sizeof(int);
+constexpr int kMaxRowChunks = 1024;
+constexpr size_t kCounterBytes = kRowCountOff + (size_t)kMaxRowChunks * sizeof(int) + 256;
+
+constexpr int kRowsPerChunk = 256;
+constexpr int kLatCols = 2048;
+constexpr int kMaxGroups = 64;
+
+size_t align_up(size_t v) { return (v + kAlign - 1) / kAlign * kAlign; }
+
+bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+
+int env_int(const char* name, int dflt) {
+  const char* v = getenv(name);
+  if (v == nullptr || *v == 0) return dflt;
+  return atoi(v);
+}
+
+// NF4 code values (QLoRA normal-float 4-bit table).
+const float kNF4[16] = {
+    -1.0f, -0.6961928009986877f, -0.5250730514526367f, -0.39491748809814453f, -0.28444138169288635f,
+    -0.18477343022823334f, -0.09105003625154495f, 0.0f, 0.07958029955625534f, 0.16093020141124725f,
+    0.24611230194568634f, 0.33791524171829224f, 0.44070982933044434f, 0.5626170039176941f, 0.7229568362236023f,
+    1.0f};
+
+std::mutex g_mid_mu;
+bool g_mid_ready[256] = {false};
+
+int ensure_midpoints() {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 256) return set_error(NSMLP_ENODEV, "no HIP device");
+  std::lock_guard<std::mutex> lk(g_mid_mu);
+  if (g_mid_ready[dev]) return NSMLP_OK;
+  float mid[15];
+  for (int i = 0; i < 15; ++i) mid[i] = (float)(((double)kNF4[i] + (double)kNF4[i + 1]) * 0.5);
+  set_nf4_midpoints(mid);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return set_error(NSMLP_EHIP, "NF4 midpoint upload: %s", hipGetErrorString(e));
+  g_mid_ready[dev] = true;
+  return NSMLP_OK;
+}
+
+// Columns per gate/up split: the largest of {2048, 1024, 512, 256} dividing
+// H that still gives >= 1024 workgroups (k * H / cs), else 256.
+int choose_cs(int H, int k) {
+  int forced = env_int("NSMLP_GU_COLS", 0);
+  if (forced == 256 || forced == 512 || forced == 1024 || forced == 2048)
+    if (H % forced == 0) return forced;
+  const int cands[4] = {2048, 1024, 512, 256};
+  for (int c : cands)
+    if (H % c == 0 && (long long)k * (H / c) >= 1024) return c;
+  for (int c = 256; c <= 2048; c *= 2)
+    if (H % c == 0 && (long long)k * (H / c) >= 1024) return c;
+  return 256;
+}
+
+int choose_groups(int H, int k) {
+  int chunks = (H + kRowsPerChunk - 1) / kRowsPerChunk;
+  int g = (1024 + chunks - 1) / chunks;
+  int forced = env_int("NSMLP_DOWN_GROUPS", 0);
+  if (forced > 0) g = forced;
+  int cap = k < kMaxGroups ? k : kMaxGroups;
+  if (g < 1) g = 1;
+  if (g > cap) g = cap;
+  return g;
+}
+
+struct DecodeWs {
+  size_t part, act, outpart, total;
+};
+
+DecodeWs decode_ws_layout(int H, int k) {
+  DecodeWs w;
+  size_t off = align_up(kCounterBytes);
+  w.part = off;
+  off += align_up((size_t)k * (size_t)(H / 256) * 64 * sizeof(float));
+  w.act = off;
+  off += align_up((size_t)k * 32 * sizeof(float));
+  w.outpart = off;
+  off += align_up((size_t)kMaxGroups * (size_t)H * sizeof(float));
+  w.total = off;
+  return w;
+}
+
+struct RouteWs {
+  size_t lat_part, scores, total;
+};
+
+RouteWs route_ws_layout(size_t base, int rows, int H, int R, int NB) {
+  RouteWs w;
+  int splits = (H + kLatCols - 1) / kLatCols;
+  size_t off = align_up(base);
+  w.lat_part = off;
+  off += align_up((size_t)rows * R * splits * 3 * sizeof(double));
+  w.scores = off;
+  off += align_up((size_t)rows * NB * sizeof(uint16_t));
+  w.total = off;
+  return w;
+}
+
+ProjView row_block_view(const uint8_t* packed, const float* absmax, int H, int qbs) {
+  ProjView v;
+  v.packed = packed;
+  v.absmax = absmax;
+  v.row_stride = H / 2;
+  v.blk_stride = 32LL * (H / 2);
+  v.abs_row_stride = H / qbs;
+  v.abs_blk_stride = 32LL * (H / qbs);
+  return v;
+}
+
+ProjView down_block_major_view(const uint8_t* packed, const float* absmax, int H) {
+  ProjView v;
+  v.packed = packed;
+  v.absmax = absmax;
+  v.row_stride = 16;
+  v.blk_stride = 16LL * H;
+  v.abs_row_stride = 1;
+  v.abs_blk_stride = H;
+  return v;
+}
+
+int validate_decode_shape(int H, int qbs, int k) {
+  if (H <= 0 || H % 256 != 0 || H > (1 << 18))
+    return set_error(NSMLP_EINVAL, "hidden size %d must be a positive multiple of 256", H);
+  if (qbs <= 0 || qbs % 32 != 0 || H % qbs != 0)
+    return set_error(NSMLP_EINVAL, "quant block size %d must be a multiple of 32 dividing hidden size %d", qbs, H);
+  if (k <= 0 || k > kMaxK) return set_error(NSMLP_EINVAL, "k=%d out of range [1, %d]", k, kMaxK);
+  if (H / kRowsPerChunk > kMaxRowChunks) return set_error(NSMLP_EINVAL, "hidden size %d too large", H);
+  return NSMLP_OK;
+}
+
+int fill_decode_ws(DecodeArgs& a, void* ws, size_t ws_bytes) {
+  DecodeWs L = decode_ws_layout(a.H, a.k);
+  if (ws == nullptr || ws_bytes < L.total)
+    return set_error(NSMLP_ENOSPC, "decode workspace needs %zu bytes, got %zu", L.total, ws_bytes);
+  if (((uintptr_t)ws & (kAlign - 1)) != 0) return set_error(NSMLP_EINVAL, "workspace must be 256-byte aligned");
+  char* base = (char*)ws;
+  a.status = (int*)(base + kStatusOff);
+  a.blk_count = (int*)(base + kBlkCountOff);
+  a.row_count = (int*)(base + kRowCountOff);
+  a.part = (float*)(base + L.part);
+  a.act = (float*)(base + L.act);
+  a.outpart = (float*)(base + L.outpart);
+  return NSMLP_OK;
+}
+
+void fill_decode_tiling(DecodeArgs& a) {
+  a.cs = choose_cs(a.H, a.k);
+  a.splits = a.H / a.cs;
+  a.groups = choose_groups(a.H, a.k);
+  a.rows_per_chunk = kRowsPerChunk;
+}
+
+int run_decode(const DecodeArgs& a, hipStream_t s) {
+  launch_decode_gate_up(a, s);
+  int rc = check_launch("decode gate/up");
+  if (rc) return rc;
+  launch_decode_down(a, s);
+  return check_launch("decode down");
+}
+
+int validate_route(int rows, int H, int R, int NB, int k, int flags) {
+  if (rows <= 0) return set_error(NSMLP_EINVAL, "rows=%d must be positive", rows);
+  if (H <= 0 || H > 65535) return set_error(NSMLP_EINVAL, "hidden size %d out of range [1, 65535]", H);
+  if (R <= 0 || R > 1024) return set_error(NSMLP_EINVAL, "basis rank %d out of range [1, 1024]", R);
+  if (NB <= 0 || NB > kMaxSelect) return set_error(NSMLP_EINVAL, "num_blocks %d out of range [1, 65535]", NB);
+  if (k <= 0 || k > NB) return set_error(NSMLP_EINVAL, "k=%d out of range [1, %d]", k, NB);
+  if ((flags & NSMLP_ROUTE_SORTED) && k > 16384) return set_error(NSMLP_EINVAL, "sorted routing limited to k <= 16384");
+  return NSMLP_OK;
+}
+
+int fill_route(RouteArgs& r, const void* x, int rows, int H, const void* enc_w, const void* enc_b, int R,
+               int basis_top_k, const void* score_w, const void* score_b, const void* dbn, int NB, int flags, int k,
+               int32_t* sel, void* latent_out, void* scores_out, char* base, size_t route_base) {
+  RouteWs L = route_ws_layout(route_base, rows, H, R, NB);
+  r.x = (const uint16_t*)x;
+  r.rows = rows;
+  r.H = H;
+  r.enc_w = (const uint16_t*)enc_w;
+  r.enc_b = (const uint16_t*)enc_b;
+  r.R = R;
+  r.basis_top_k = basis_top_k;
+  r.score_w = (const uint16_t*)score_w;
+  r.score_b = (const uint16_t*)score_b;
+  r.dbn = (const uint16_t*)dbn;
+  r.NB = NB;
+  r.legacy_abs = (flags & NSMLP_ROUTE_LEGACY_ABS) ? 1 : 0;
+  r.sorted = (flags & NSMLP_ROUTE_SORTED) ? 1 : 0;
+  r.k = k;
+  r.lat_cols = kLatCols;
+  r.lat_splits = (H + kLatCols - 1) / kLatCols;
+  r.vec = (H % 8 == 0) && aligned16(x) && aligned16(enc_w);
+  r.sel = sel;
+  r.latent_out = (uint16_t*)latent_out;
+  r.scores_out = (uint16_t*)scores_out;
+  r.lat_part = (double*)(base + L.lat_part);
+  r.scores = (uint16_t*)(base + L.scores);
+  r.status = (int*)(base + kStatusOff);
+  return NSMLP_OK;
+}
+
+int table_to_args(const nsmlp_slot_table* t, DecodeArgs& a) {
+  if (t == nullptr) return set_error(NSMLP_EINVAL, "slot table is NULL");
+  if (t->I <= 0 || t->I % 32 != 0) return set_error(NSMLP_EINVAL, "intermediate size %d must be a multiple of 32", t->I);
+  if (!t->gate_packed || !t->gate_absmax || !t->up_packed || !t->up_absmax || !t->down_packed || !t->down_absmax ||
+      !t->code)
+    if (t->n_slots > 0) return set_error(NSMLP_EINVAL, "slot storage pointers must be non-NULL");
+  if (t->n_slots < 0) return set_error(NSMLP_EINVAL, "n_slots must be >= 0");
+  if (t->lookup == nullptr && t->n_slots < t->I / 32)
+    return set_error(NSMLP_EINVAL, "identity lookup needs n_slots >= num_blocks");
+  const void* ptrs[] = {t->gate_packed, t->up_packed, t->down_packed, t->host_gate_packed, t->host_up_packed,
+                        t->host_down_packed};
+  for (const void* p : ptrs)
+    if (p && !aligned16(p)) return set_error(NSMLP_EINVAL, "packed NF4 storage must be 16-byte aligned");
+  memset(&a, 0, sizeof(a));
+  a.H = t->H;
+  a.qbs = t->qbs;
+  a.NB = t->I / 32;
+  a.n_slots = t->n_slots;
+  a.lookup = t->lookup;
+  a.gate = row_block_view(t->gate_packed, t->gate_absmax, t->H, t->qbs);
+  a.up = row_block_view(t->up_packed, t->up_absmax, t->H, t->qbs);
+  a.down = down_block_major_view(t->down_packed, t->down_absmax, t->H);
+  a.host_gate = row_block_view(t->host_gate_packed, t->host_gate_absmax, t->H, t->qbs);
+  a.host_up = row_block_view(t->host_up_packed, t->host_up_absmax, t->H, t->qbs);
+  a.host_down = down_block_major_view(t->host_down_packed, t->host_down_absmax, t->H);
+  a.code = a.code_up = a.code_down = t->code;
+  a.down_bias = (const uint16_t*)t->down_bias;
+  return NSMLP_OK;
+}
+
+}  // namespace
+
+int set_error(int code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof(g_err), fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+int check_launch(const char* what) {
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return set_error(NSMLP_EHIP, "%s launch failed: %s", what, hipGetErrorString(e));
+  return NSMLP_OK;
+}
+
+}  // namespace nsmlp
+
+using namespace nsmlp;
+
+extern "C" {
+
+const char* nsmlp_last_error(void) { return g_err; }
+
+int nsmlp_version(void) { return 100; }
+
+int nsmlp_device_supported(int device) {
+  hipDeviceProp_t prop;
+  if (hipGetDeviceProperties(&prop, device) != hipSuccess) return 0;
+  return strncmp(prop.gcnArchName, "gfx950", 6) == 0 ? 1 : 0;
+}
+
+int nsmlp_workspace_init(void* ws, size_t ws_bytes, void* stream) {
+  if (ws == nullptr || ws_bytes < kCounterBytes)
+    return set_error(NSMLP_ENOSPC, "workspace needs at least %zu bytes", kCounterBytes);
+  launch_zero_u32((uint32_t*)ws, (long long)(kCounterBytes / 4), (hipStream_t)stream);
+  return check_launch("workspace init");
+}
+
+size_t nsmlp_route_workspace_bytes(int rows, int H, int R, int NB, int k) {
+  (void)k;
+  return route_ws_layout(kCounterBytes, rows, H, R, NB).total;
+}
+
+int nsmlp_route_f16(const void* x, int rows, int H, const void* enc_w, const void* enc_b, int R, int basis_top_k,
+                    const void* score_w, const void* score_b, const void* down_block_norm, int NB, int flags, int k,
+                    int32_t* sel, void* latent_out, void* scores_out, void* ws, size_t ws_bytes, void* stream) {
+  int rc = validate_route(rows, H, R, NB, k, flags);
+  if (rc) return rc;
+  if (!x || !enc_w || !score_w || !sel) return set_error(NSMLP_EINVAL, "x, enc_w, score_w and sel must be non-NULL");
+  size_t need = nsmlp_route_workspace_bytes(rows, H, R, NB, k);
+  if (ws == nullptr || ws_bytes < need)
+    return set_error(NSMLP_ENOSPC, "route workspace needs %zu bytes, got %zu", need, ws_bytes);
+  RouteArgs r;
+  fill_route(r, x, rows, H, enc_w, enc_b, R, basis_top_k, score_w, score_b, down_block_norm, NB, flags, k, sel,
+             latent_out, scores_out, (char*)ws, kCounterBytes);
+  launch_route(r, (hipStream_t)stream);
+  return check_launch("route");
+}
+
+size_t nsmlp_decode_workspace_bytes(int H, int k) { return decode_ws_layout(H, k).total; }
+
+int nsmlp_decode_slots_f16(const nsmlp_slot_table* table, const void* x, const int32_t* sel, int k, void* out,
+                           void* ws, size_t ws_bytes, void* stream) {
+  DecodeArgs a;
+  int rc = table_to_args(table, a);
+  if (rc) return rc;
+  rc = validate_decode_shape(a.H, a.qbs, k);
+  if (rc) return rc;
+  if (!x || !sel || !out) return set_error(NSMLP_EINVAL, "x, sel and out must be non-NULL");
+  if (!aligned16(x)) return set_error(NSMLP_EINVAL, "x must be 16-byte aligned");
+  if (k > a.NB) return set_error(NSMLP_EINVAL, "k=%d exceeds num_blocks=%d", k, a.NB);
+  a.x = (const uint16_t*)x;
+  a.k = k;
+  a.sel = sel;
+  a.out = (uint16_t*)out;
+  rc = fill_decode_ws(a, ws, ws_bytes);
+  if (rc) return rc;
+  fill_decode_tiling(a);
+  return run_decode(a, (hipStream_t)stream);
+}
+
+size_t nsmlp_layer_workspace_bytes(int H, int R, int NB, int k) {
+  size_t d = decode_ws_layout(H, k).total;
+  size_t r = route_ws_layout(d, 1, H, R, NB).total;
+  return r + align_up((size_t)k * sizeof(int32_t));
+}
+
+int nsmlp_decode_layer_f16(const nsmlp_router* router, const nsmlp_slot_table* table, const void* x, int k,
+                           int32_t* sel_out, void* out, void* ws, size_t ws_bytes, void* stream) {
+  if (router == nullptr) return set_error(NSMLP_EINVAL, "router is NULL");
+  DecodeArgs a;
+  int rc = table_to_args(table, a);
+  if (rc) return rc;
+  rc = validate_decode_shape(a.H, a.qbs, k);
+  if (rc) return rc;
+  rc = validate_route(1, a.H, router->R, router->NB, k, router->flags);
+  if (rc) return rc;
+  if (router->NB != a.NB)
+    return set_error(NSMLP_EINVAL, "router num_blocks %d != intermediate blocks %d", router->NB, a.NB);
+  if (!x || !out || !router->enc_w || !router->score_w)
+    return set_error(NSMLP_EINVAL, "x, out, enc_w and score_w must be non-NULL");
+  if (!aligned16(x)) return set_error(NSMLP_EINVAL, "x must be 16-byte aligned");
+  size_t need = nsmlp_layer_workspace_bytes(a.H, router->R, router->NB, k);
+  if (ws == nullptr || ws_bytes < need)
+    return set_error(NSMLP_ENOSPC, "layer workspace needs %zu bytes, got %zu", need, ws_bytes);
+  a.x = (const uint16_t*)x;
+  a.k = k;
+  a.out = (uint16_t*)out;
+  rc = fill_decode_ws(a, ws, ws_bytes);
+  if (rc) return rc;
+  fill_decode_tiling(a);
+  size_t dtotal = decode_ws_layout(a.H, k).total;
+  RouteWs RL = route_ws_layout(dtotal, 1, a.H, router->R, router->NB);
+  int32_t* sel = sel_out ? sel_out : (int32_t*)((char*)ws + RL.total);
+  RouteArgs r;
+  fill_route(r, x, 1, a.H, router->enc_w, router->enc_b, router->R, router->basis_top_k, router->score_w,
+             router->score_b, router->down_block_norm, router->NB, router->flags & NSMLP_ROUTE_LEGACY_ABS, k, sel,
+             nullptr, nullptr, (char*)ws, dtotal);
+  hipStream_t s = (hipStream_t)stream;
+  launch_route(r, s);
+  rc = check_launch("route");
+  if (rc) return rc;
+  a.sel = sel;
+  return run_decode(a, s);
+}
+
+size_t nsmlp_single_kernel_workspace_bytes(int H, int top_k) { return decode_ws_layout(H, top_k).total; }
+
+int nsmlp_single_kernel_decode_f16(const void* x, const uint8_t* gate_packed, const float* gate_absmax,
+                                   const float* gate_code, const uint8_t* up_packed, const float* up_absmax,
+                                   const float* up_code, const uint8_t* down_packed, const float* down_absmax,
+                                   const float* down_code, void* out, float* out_accum, int H, int block_size,
+                                   int qbs, int top_k, void* ws, size_t ws_bytes, void* stream) {
+  if (block_size != 32) return set_error(NSMLP_EINVAL, "block_size must be 32 (got %d)", block_size);
+  int rc = validate_decode_shape(H, qbs, top_k);
+  if (rc) return rc;
+  if (!x || !gate_packed || !gate_absmax || !gate_code || !up_packed || !up_absmax || !up_code || !down_packed ||
+      !down_absmax || !down_code || !out)
+    return set_error(NSMLP_EINVAL, "NULL tensor argument");
+  if (!aligned16(x) || !aligned16(gate_packed) || !aligned16(up_packed) || !aligned16(down_packed))
+    return set_error(NSMLP_EINVAL, "x and packed weights must be 16-byte aligned");
+  DecodeArgs a;
+  memset(&a, 0, sizeof(a));
+  a.H = H;
+  a.qbs = qbs;
+  a.k = top_k;
+  a.NB = top_k;
+  a.n_slots = top_k;
+  a.x = (const uint16_t*)x;
+  a.gate = row_block_view(gate_packed, gate_absmax, H, qbs);
+  a.up = row_block_view(up_packed, up_absmax, H, qbs);
+  a.down.packed = down_packed;
+  a.down.absmax = down_absmax;
+  a.down.row_stride = 16LL * top_k;
+  a.down.blk_stride = 16;
+  a.down.abs_row_stride = top_k;
+  a.down.abs_blk_stride = 1;
+  a.code = gate_code;
+  a.code_up = up_code;
+  a.code_down = down_code;
+  a.out = (uint16_t*)out;
+  a.out_f32 = out_accum;
+  rc = fill_decode_ws(a, ws, ws_bytes);
+  if (rc) return rc;
+  fill_decode_tiling(a);
+  return run_decode(a, (hipStream_t)stream);
+}
+
+size_t nsmlp_fused_decode_workspace_bytes(int H, int kk) { return decode_ws_layout(H, kk).total; }
+
+int nsmlp_fused_decode_gathered_f16(const void* x, int H, const int32_t* active_idx, int kk, int A,
+                                    const void* flat_mask, const uint8_t* gate_packed, const float* gate_absmax,
+                                    const float* gate_code, const void* gate_bias, const uint8_t* up_packed,
+                                    const float* up_absmax, const float* up_code, const void* up_bias,
+                                    const uint8_t* down_packed, const float* down_absmax, const float* down_code,
+                                    const void* down_bias, int qbs, void* out, void* ws, size_t ws_bytes,
+                                    void* stream) {
+  int rc = validate_decode_shape(H, qbs, kk);
+  if (rc) return rc;
+  if (A <= 0 || A > kMaxSelect) return set_error(NSMLP_EINVAL, "A=%d out of range", A);
+  if (!x || !active_idx || !gate_packed || !gate_absmax || !gate_code || !up_packed || !up_absmax || !up_code ||
+      !down_packed || !down_absmax || !down_code || !out)
+    return set_error(NSMLP_EINVAL, "NULL tensor argument");
+  if (!aligned16(x) || !aligned16(gate_packed) || !aligned16(up_packed) || !aligned16(down_packed))
+    return set_error(NSMLP_EINVAL, "x and packed weights must be 16-byte aligned");
+  DecodeArgs a;
+  memset(&a, 0, sizeof(a));
+  a.H = H;
+  a.qbs = qbs;
+  a.k = kk;
+  a.NB = A;
+  a.n_slots = A;
+  a.sel = active_idx;
+  a.skip_negative = 1;
+  a.x = (const uint16_t*)x;
+  a.gate = row_block_view(gate_packed, gate_absmax, H, qbs);
+  a.up = row_block_view(up_packed, up_absmax, H, qbs);
+  a.down.packed = down_packed;
+  a.down.absmax = down_absmax;
+  a.down.row_stride = 16LL * A;
+  a.down.blk_stride = 16;
+  a.down.abs_row_stride = A;
+  a.down.abs_blk_stride = 1;
+  a.code = gate_code;
+  a.code_up = up_code;
+  a.code_down = down_code;
+  a.mask = (const uint16_t*)flat_mask;
+  a.gate_bias = (const uint16_t*)gate_bias;
+  a.up_bias = (const uint16_t*)up_bias;
+  a.down_bias = (const uint16_t*)down_bias;
+  a.out = (uint16_t*)out;
+  rc = fill_decode_ws(a, ws, ws_bytes);
+  if (rc) return rc;
+  fill_decode_tiling(a);
+  return run_decode(a, (hipStream_t)stream);
+}
+
+size_t nsmlp_output_linear_workspace_bytes(int rows, int kk, int in_dim) {
+  return align_up(kCounterBytes) + align_up((size_t)rows * kk * (size_t)(in_dim / 256 > 0 ? in_dim / 256 : 1) * 32 *
+                                            sizeof(float));
+}
+
+int nsmlp_output_linear_nf4_f16(const void* x, int rows, int in_dim, const int32_t* active_idx, int kk, int A,
+                                const void* flat_mask, const uint8_t* packed, const float* absmax, const float* code,
+                                int qbs, const void* bias, int block_size, void* out, void* ws, size_t ws_bytes,
+                                void* stream) {
+  if (block_size != 32) return set_error(NSMLP_EINVAL, "block_size must be 32 (got %d)", block_size);
+  if (rows <= 0 || kk <= 0 || A <= 0) return set_error(NSMLP_EINVAL, "rows, kk and A must be positive");
+  if (in_dim <= 0 || in_dim % 256 != 0) return set_error(NSMLP_EINVAL, "input_dim %d must be a multiple of 256", in_dim);
+  if (qbs <= 0 || qbs % 32 != 0 || in_dim % qbs != 0)
+    return set_error(NSMLP_EINVAL, "quant block size %d must be a multiple of 32 dividing %d", qbs, in_dim);
+  if (!x || !active_idx || !packed || !absmax || !code || !out) return set_error(NSMLP_EINVAL, "NULL tensor argument");
+  if (!aligned16(packed)) return set_error(NSMLP_EINVAL, "packed weight must be 16-byte aligned");
+  size_t need = nsmlp_output_linear_workspace_bytes(rows, kk, in_dim);
+  if (ws == nullptr || ws_bytes < need)
+    return set_error(NSMLP_ENOSPC, "output-linear workspace needs %zu bytes, got %zu", need, ws_bytes);
+  LinearArgs l;
+  memset(&l, 0, sizeof(l));
+  l.x = (const uint16_t*)x;
+  l.rows = rows;
+  l.in_dim = in_dim;
+  l.active_idx = active_idx;
+  l.kk = kk;
+  l.A = A;
+  l.packed = packed;
+  l.absmax = absmax;
+  l.code = code;
+  l.qbs = qbs;
+  l.mask = (const uint16_t*)flat_mask;
+  l.bias = (const uint16_t*)bias;
+  l.out = (uint16_t*)out;
+  l.cs = choose_cs(in_dim, rows * kk);
+  l.splits = in_dim / l.cs;
+  l.part = (float*)((char*)ws + align_up(kCounterBytes));
+  launch_output_linear(l, (hipStream_t)stream);
+  return check_launch("output linear");
+}
+
+int nsmlp_input_linear_nf4_f16(const void* x, int rows, int in_features, const int32_t* active_idx, int kk,
+                               const uint8_t* packed, const float* absmax, const float* code, int qbs,
+                               int out_features, const void* bias, int block_size, void* out, void* stream) {
+  if (block_size != 32) return set_error(NSMLP_EINVAL, "block_size must be 32 (got %d)", block_size);
+  if (rows <= 0 || kk <= 0 || out_features <= 0) return set_error(NSMLP_EINVAL, "rows, kk, out_features must be > 0");
+  if (in_features <= 0 || in_features % 32 != 0)
+    return set_error(NSMLP_EINVAL, "in_features %d must be a multiple of 32", in_features);
+  if (qbs <= 0 || qbs % 32 != 0 || in_features % qbs != 0)
+    return set_error(NSMLP_EINVAL, "quant block size %d must be a multiple of 32 dividing %d", qbs, in_features);
+  if (!x || !active_idx || !packed || !absmax || !code || !out) return set_error(NSMLP_EINVAL, "NULL tensor argument");
+  if (!aligned16(packed)) return set_error(NSMLP_EINVAL, "packed weight must be 16-byte aligned");
+  LinearArgs l;
+  memset(&l, 0, sizeof(l));
+  l.x = (const uint16_t*)x;
+  l.rows = rows;
+  l.in_dim = in_features;
+  l.out_dim = out_features;
+  l.active_idx = active_idx;
+  l.kk = kk;
+  l.packed = packed;
+  l.absmax = absmax;
+  l.code = code;
+  l.qbs = qbs;
+  l.bias = (const uint16_t*)bias;
+  l.out = (uint16_t*)out;
+  launch_input_linear(l, (hipStream_t)stream);
+  return check_launch("input linear");
+}
+
+int nsmlp_silu_mul_f16(const void* gate, const void* up, void* out, long long n, void* stream) {
+  if (n < 0 || (n > 0 && (!gate || !up || !out))) return set_error(NSMLP_EINVAL, "bad silu_mul arguments");
+  if (n == 0) return NSMLP_OK;
+  launch_silu_mul((const uint16_t*)gate, (const uint16_t*)up, (uint16_t*)out, n, (hipStream_t)stream);
+  return check_launch("silu_mul");
+}
+
+int nsmlp_gather_row_blocks(const uint8_t* src_packed, const float* src_absmax, int src_blocks,
+                            const int32_t* blocks, int n, int in_features, int qbs, uint8_t* dst_packed,
+                            float* dst_absmax, void* stream) {
+  if (n < 0 || src_blocks < 0 || in_features <= 0 || in_features % 32 != 0 || qbs <= 0 ||
+      (32LL * in_features) % qbs != 0)
+    return set_error(NSMLP_EINVAL, "bad row-block gather geometry");
+  if (n == 0) return NSMLP_OK;
+  if (!src_packed || !src_absmax || !blocks || !dst_packed || !dst_absmax)
+    return set_error(NSMLP_EINVAL, "NULL tensor argument");
+  if (!aligned16(src_packed) || !aligned16(dst_packed)) return set_error(NSMLP_EINVAL, "packed must be 16-byte aligned");
+  launch_gather_rows(src_packed, src_absmax, blocks, src_blocks, n, 16LL * in_features, 32LL * in_features / qbs,
+                     dst_packed,
+                     dst_absmax, (hipStream_t)stream);
+  return check_launch("gather rows");
+}
+
+int nsmlp_gather_down_columns(const uint8_t* src_packed, const float* src_absmax, const int32_t* blocks, int n,
+                              int out_features, int in_features, int qbs, int dst_layout, uint8_t* dst_packed,
+                              float* dst_absmax, void* stream) {
+  if (n < 0 || out_features <= 0 || in_features <= 0 || in_features % 32 != 0 || qbs <= 0 || qbs % 32 != 0 ||
+      in_features % qbs != 0)
+    return set_error(NSMLP_EINVAL, "bad down-column gather geometry");
+  if (dst_layout != NSMLP_DOWN_BLOCK_MAJOR && dst_layout != NSMLP_DOWN_GATHERED)
+    return set_error(NSMLP_EINVAL, "unknown down layout %d", dst_layout);
+  if (n == 0) return NSMLP_OK;
+  if (!src_packed || !src_absmax || !blocks || !dst_packed || !dst_absmax)
+    return set_error(NSMLP_EINVAL, "NULL tensor argument");
+  if (!aligned16(src_packed) || !aligned16(dst_packed)) return set_error(NSMLP_EINVAL, "packed must be 16-byte aligned");
+  launch_gather_down(src_packed, src_absmax, blocks, n, out_features, in_features, qbs, dst_layout, dst_packed,
+                     dst_absmax, (hipStream_t)stream);
+  return check_launch("gather down");
+}
+
+int nsmlp_host_device_pointer(const void* host, void** device_ptr) {
+  if (!host || !device_ptr) return set_error(NSMLP_EINVAL, "NULL pointer");
+  hipError_t e = hipHostGetDevicePointer(device_ptr, const_cast<void*>(host), 0);
+  if (e != hipSuccess) return set_error(NSMLP_EHIP, "hipHostGetDevicePointer: %s", hipGetErrorString(e));
+  return NSMLP_OK;
+}
+
+int nsmlp_synth_normal_f16(uint64_t seed, long long n, float std, void* out, void* stream) {
+  if (n < 0 || (n > 0 && !out)) return set_error(NSMLP_EINVAL, "bad synth arguments");
+  if (n == 0) return NSMLP_OK;
+  launch_synth_normal_f16(seed, n, std, (uint16_t*)out, (hipStream_t)stream);
+  return check_launch("synth normal f16");
+}
+
+int nsmlp_synth_normal_f32(uint64_t seed, long long n, float std, float* out, void* stream) {
+  if (n < 0 || (n > 0 && !out)) return set_error(NSMLP_EINVAL, "bad synth arguments");
+  if (n == 0) return NSMLP_OK;
+  launch_synth_normal_f32(seed, n, std, out, (hipStream_t)stream);
+  return check_launch("synth normal f32");
+}
+
+int nsmlp_synth_nf4(uint64_t seed, long long n, int qbs, float std, uint8_t* packed, float* absmax, void* stream) {
+  if (qbs <= 0 || qbs % 8 != 0 || n < 0 || n % qbs != 0)
+    return set_error(NSMLP_EINVAL, "n=%lld must be a multiple of the quant block size %d (multiple of 8)", n, qbs);
+  if (n == 0) return NSMLP_OK;
+  if (!packed || !absmax) return set_error(NSMLP_EINVAL, "NULL output");
+  if (((uintptr_t)packed & 3u) != 0) return set_error(NSMLP_EINVAL, "packed must be 4-byte aligned");
+  int rc = ensure_midpoints();
+  if (rc) return rc;
+  launch_nf4_quant(nullptr, seed, std, n, qbs, true, packed, absmax, (hipStream_t)stream);
+  return check_launch("synth nf4");
+}
+
+int nsmlp_nf4_quantize_f32(const float* w, long long n, int qbs, uint8_t* packed, float* absmax, void* stream) {
+  if (qbs <= 0 || qbs % 8 != 0 || n < 0 || n % qbs != 0)
+    return set_error(NSMLP_EINVAL, "n=%lld must be a multiple of the quant block size %d (multiple of 8)", n, qbs);
+  if (n == 0) return NSMLP_OK;
+  if (!w || !packed || !absmax) return set_error(NSMLP_EINVAL, "NULL tensor argument");
+  if (((uintptr_t)packed & 3u) != 0) return set_error(NSMLP_EINVAL, "packed must be 4-byte aligned");
+  int rc = ensure_midpoints();
+  if (rc) return rc;
+  launch_nf4_quant(w, 0, 0.0f, n, qbs, false, packed, absmax, (hipStream_t)stream);
+  return check_launch("nf4 quantize");
+}
+
+}  // extern "C"

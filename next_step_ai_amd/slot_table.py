@@ -1,0 +1,289 @@
+"""HBM hot-block slot table and the one-call decode layer.
+
+The reference keeps a per-projection "VRAM hot cache" (RT:2619-2786): a CPU
+``lookup_cpu`` (block -> slot or -1), slot storage for the hot blocks, and a
+host path that gathers, copies and merges the cold ones every token
+(RT:3588-3702, RT:3885-4207, RT:4455-4578).  Here the table lives on the
+device and is read by the decode kernels directly:
+
+* ``lookup`` [NB] int32 on the device (block -> slot, -1 = host-resident);
+* gate/up slots [n_slots, 32, H/2] u8 + absmax [n_slots, 32, H/qbs] f32
+  (the reference's gate/up row blocks are already contiguous: RT:4627-4660);
+* down slots block-major [n_slots, H, 16] u8 + absmax [n_slots, H] f32 (the
+  reference's [H, n, 16] column gather, RT:4491-4511, transposed so that a
+  block's column is one contiguous 256 KB stream at the 405B shape);
+* optional pinned host copy of every block in the same layout; misses are
+  read by the kernels over the host link, without a host round trip.
+
+The fixed-capacity replacement policy keeps the reference's rule
+(``plan_fixed_capacity_bank_update``, RT:2576-2617).
+"""
+from __future__ import annotations
+
+import ctypes
+
+import torch
+
+from . import _lib
+from ._runtime import nf4_code, ptr, require_device, stream_handle, workspace
+
+BLOCK = 32
+
+
+def plan_fixed_capacity_bank_update(*, existing_block_ids_cpu: torch.Tensor, existing_scores_cpu: torch.Tensor,
+                                    active_count: int, capacity: int, novel_blocks_cpu: torch.Tensor):
+    """Slot plan for promoting ``novel_blocks_cpu`` into a fixed-capacity bank
+    (RT:2576-2617): free slots first, then the lowest-score slot; a promoted
+    block scores (max active score + 1) + (i + 1) * 1e-3.
+    Returns (slots, block_ids, scores, active_count)."""
+    cap = max(0, int(capacity))
+    active = max(0, min(int(active_count), int(existing_block_ids_cpu.numel()), cap))
+    if cap <= 0:
+        return torch.empty((0,), dtype=torch.long), existing_block_ids_cpu.clone(), existing_scores_cpu.clone(), active
+    ids = existing_block_ids_cpu.clone()
+    scores = existing_scores_cpu.clone()
+    novel = novel_blocks_cpu.detach().to(device="cpu", dtype=torch.long).reshape(-1)
+    if int(novel.numel()) <= 0:
+        return torch.empty((0,), dtype=torch.long), ids, scores, active
+    novel = novel[:cap]
+    cur = scores.clone()
+    base = float(cur[:active].max().item()) + 1.0 if active > 0 else 1.0
+    nxt = active
+    slots: list[int] = []
+    for i in range(int(novel.numel())):
+        if nxt < cap:
+            s = nxt
+            nxt += 1
+            active = max(active, s + 1)
+        else:
+            s = int(torch.argmin(cur[:cap]).item())
+        ids[s] = int(novel[i].item())
+        cur[s] = base + float(i + 1) * 1e-3
+        slots.append(s)
+    scores.copy_(cur)
+    return torch.tensor(slots, dtype=torch.long), ids, scores, active
+
+
+def partition_cached_block_lookup(lookup: torch.Tensor, *, ordered_blocks: torch.Tensor):
+    """Hot/cold split of ``ordered_blocks`` given their looked-up slots
+    (RT:3588-3604): a block is hot iff its slot is >= 0.
+    Returns (hot_positions or None, hot_slots or None, cold_blocks, cold_mask)."""
+    hot_mask = lookup >= 0
+    if bool(hot_mask.any()):
+        pos = torch.nonzero(hot_mask, as_tuple=False).flatten()
+        slots = lookup.index_select(0, pos).to(torch.long)
+    else:
+        pos, slots = None, None
+    cold_mask = ~hot_mask
+    return pos, slots, ordered_blocks[cold_mask], cold_mask
+
+
+def gather_row_blocks(packed: torch.Tensor, absmax: torch.Tensor, blocks: torch.Tensor, in_features: int,
+                      qbs: int) -> tuple[torch.Tensor, torch.Tensor]:
+    """Device gather of gate/up row blocks (RT:4530-4578 semantics):
+    returns [n, 32*in/2] u8 and [n, 32*in/qbs] f32."""
+    device = require_device(packed, "packed")
+    b = blocks.to(device=device, dtype=torch.int32).contiguous()
+    n = int(b.numel())
+    out_p = torch.empty((n, BLOCK * int(in_features) // 2), dtype=torch.uint8, device=device)
+    out_a = torch.empty((n, BLOCK * int(in_features) // int(qbs)), dtype=torch.float32, device=device)
+    src_blocks = int(packed.numel()) // (BLOCK * int(in_features) // 2)
+    _lib.call("nsmlp_gather_row_blocks", ptr(packed), ptr(absmax), src_blocks, ptr(b), n, int(in_features), int(qbs),
+              ptr(out_p), ptr(out_a), stream_handle(device))
+    return out_p, out_a
+
+
+def gather_down_columns(packed: torch.Tensor, absmax: torch.Tensor, blocks: torch.Tensor, out_features: int,
+                        in_features: int, qbs: int, *, block_major: bool = True):
+    """Device gather of down-proj column blocks (RT:4455-4528 semantics):
+    block b = bytes [o, 16b:16b+16) and absmax [o, (32b)//qbs] of the
+    row-major weight.  block_major -> [n, H, 16] / [n, H]; else the
+    reference's [H, n, 16] / [H, n]."""
+    device = require_device(packed, "packed")
+    b = blocks.to(device=device, dtype=torch.int32).contiguous()
+    n = int(b.numel())
+    H = int(out_features)
+    if block_major:
+        out_p = torch.empty((n, H, 16), dtype=torch.uint8, device=device)
+        out_a = torch.empty((n, H), dtype=torch.float32, device=device)
+        layout = _lib.NSMLP_DOWN_BLOCK_MAJOR
+    else:
+        out_p = torch.empty((H, n, 16), dtype=torch.uint8, device=device)
+        out_a = torch.empty((H, n), dtype=torch.float32, device=device)
+        layout = _lib.NSMLP_DOWN_GATHERED
+    _lib.call("nsmlp_gather_down_columns", ptr(packed), ptr(absmax), ptr(b), n, H, int(in_features), int(qbs),
+              layout, ptr(out_p), ptr(out_a), stream_handle(device))
+    return out_p, out_a
+
+
+def _host_dev_ptr(t: torch.Tensor | None) -> int | None:
+    if t is None:
+        return None
+    out = ctypes.c_void_p()
+    _lib.call("nsmlp_host_device_pointer", ctypes.c_void_p(t.data_ptr()), ctypes.byref(out))
+    return int(out.value) if out.value is not None else None
+
+
+class SparseMlpSlotTable:
+    """Device slot table of one layer's gate/up/down NF4 blocks."""
+
+    def __init__(self, *, H: int, I: int, qbs: int, device: torch.device):
+        if int(I) % BLOCK != 0:
+            raise RuntimeError(f"intermediate_size={int(I)} is not divisible by block_size={BLOCK}")
+        self.H, self.I, self.qbs = int(H), int(I), int(qbs)
+        self.NB = self.I // BLOCK
+        self.device = device
+        self.lookup: torch.Tensor | None = None
+        self.block_ids: torch.Tensor | None = None
+        self.gate_packed = self.gate_absmax = self.up_packed = self.up_absmax = None
+        self.down_packed = self.down_absmax = None
+        self.host: dict[str, torch.Tensor] = {}
+        self.down_bias: torch.Tensor | None = None
+        self.code = nf4_code(device)
+        self._struct: _lib.SlotTable | None = None
+
+    @property
+    def n_slots(self) -> int:
+        return 0 if self.gate_packed is None else int(self.gate_packed.shape[0])
+
+    @classmethod
+    def from_reference(cls, *, gate_packed: torch.Tensor, gate_absmax: torch.Tensor, up_packed: torch.Tensor,
+                       up_absmax: torch.Tensor, down_packed: torch.Tensor, down_absmax: torch.Tensor, H: int, I: int,
+                       qbs: int = 64, resident_blocks: torch.Tensor | None = None,
+                       host_copy: bool = False) -> "SparseMlpSlotTable":
+        """Build from the reference layouts on the device: gate/up ``[I*H/2]``
+        u8 + ``[I*H/qbs]`` f32, down ``[H*I/2]`` u8 + ``[H*I/qbs]`` f32.
+        ``resident_blocks`` (default: all) go to HBM slots in the given
+        order; with ``host_copy`` every block is also kept in pinned host
+        memory and non-resident blocks are served from there."""
+        device = require_device(gate_packed, "gate_packed")
+        t = cls(H=H, I=I, qbs=qbs, device=device)
+        NB = t.NB
+        all_blocks = torch.arange(NB, dtype=torch.int32, device=device)
+        if resident_blocks is None:
+            t.gate_packed = gate_packed.view(NB, BLOCK * H // 2)
+            t.gate_absmax = gate_absmax.view(NB, BLOCK * H // qbs)
+            t.up_packed = up_packed.view(NB, BLOCK * H // 2)
+            t.up_absmax = up_absmax.view(NB, BLOCK * H // qbs)
+            t.down_packed, t.down_absmax = gather_down_columns(down_packed, down_absmax, all_blocks, H, I, qbs)
+            t.lookup = None
+            t.block_ids = all_blocks.to("cpu", torch.long)
+        else:
+            res = resident_blocks.to(device=device, dtype=torch.int32).contiguous()
+            t.gate_packed, t.gate_absmax = gather_row_blocks(gate_packed, gate_absmax, res, H, qbs)
+            t.up_packed, t.up_absmax = gather_row_blocks(up_packed, up_absmax, res, H, qbs)
+            t.down_packed, t.down_absmax = gather_down_columns(down_packed, down_absmax, res, H, I, qbs)
+            lookup = torch.full((NB,), -1, dtype=torch.int32)
+            lookup[res.to("cpu", torch.long)] = torch.arange(int(res.numel()), dtype=torch.int32)
+            t.lookup = lookup.to(device)
+            t.block_ids = res.to("cpu", torch.long)
+        if host_copy:
+            dp, da = gather_down_columns(down_packed, down_absmax, all_blocks, H, I, qbs)
+            srcs = {
+                "gate_packed": gate_packed.view(NB, -1), "gate_absmax": gate_absmax.view(NB, -1),
+                "up_packed": up_packed.view(NB, -1), "up_absmax": up_absmax.view(NB, -1),
+                "down_packed": dp, "down_absmax": da,
+            }
+            for name, src in srcs.items():
+                h = torch.empty(src.shape, dtype=src.dtype, pin_memory=True)
+                h.copy_(src)
+                t.host[name] = h
+            del dp, da
+        return t
+
+    def lookup_cpu(self) -> torch.Tensor:
+        """The reference's ``lookup_cpu`` view (block -> slot or -1)."""
+        if self.lookup is None:
+            return torch.arange(self.NB, dtype=torch.int32)
+        return self.lookup.to("cpu")
+
+    def as_struct(self) -> _lib.SlotTable:
+        h = self.host
+        st = _lib.SlotTable(
+            H=self.H, I=self.I, qbs=self.qbs, n_slots=self.n_slots,
+            lookup=ptr(self.lookup),
+            gate_packed=ptr(self.gate_packed), gate_absmax=ptr(self.gate_absmax),
+            up_packed=ptr(self.up_packed), up_absmax=ptr(self.up_absmax),
+            down_packed=ptr(self.down_packed), down_absmax=ptr(self.down_absmax),
+            host_gate_packed=_host_dev_ptr(h.get("gate_packed")), host_gate_absmax=_host_dev_ptr(h.get("gate_absmax")),
+            host_up_packed=_host_dev_ptr(h.get("up_packed")), host_up_absmax=_host_dev_ptr(h.get("up_absmax")),
+            host_down_packed=_host_dev_ptr(h.get("down_packed")),
+            host_down_absmax=_host_dev_ptr(h.get("down_absmax")),
+            code=ptr(self.code), down_bias=ptr(self.down_bias),
+        )
+        self._struct = st
+        return st
+
+    def decode(self, x: torch.Tensor, sel: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
+        """One decode token over the selected block ids ``sel`` [k]."""
+        x16 = x.reshape(-1).to(device=self.device, dtype=torch.float16).contiguous()
+        s = sel.reshape(-1).to(device=self.device, dtype=torch.int32).contiguous()
+        k = int(s.numel())
+        if out is None:
+            out = torch.empty(self.H, dtype=torch.float16, device=self.device)
+        nbytes = int(_lib.lib().nsmlp_decode_workspace_bytes(self.H, k))
+        ws = workspace(nbytes, self.device)
+        st = self._struct if self._struct is not None else self.as_struct()
+        _lib.call("nsmlp_decode_slots_f16", ctypes.byref(st), ptr(x16), ptr(s), k, ptr(out), ptr(ws), ws.numel(),
+                  stream_handle(self.device))
+        return out
+
+
+class SparseMlpRouter:
+    """Device copy of one layer's router (fp16, as the runtime casts it, RT:850-891)."""
+
+    def __init__(self, *, enc_w: torch.Tensor, enc_b: torch.Tensor | None, score_w: torch.Tensor,
+                 score_b: torch.Tensor | None, basis_top_k: int | None = None,
+                 down_block_norm: torch.Tensor | None = None, legacy_abs: bool = False):
+        device = require_device(enc_w, "enc_w")
+        self.device = device
+        self.enc_w = enc_w.to(device=device, dtype=torch.float16).contiguous()
+        self.enc_b = None if enc_b is None else enc_b.reshape(-1).to(device=device, dtype=torch.float16).contiguous()
+        self.score_w = score_w.to(device=device, dtype=torch.float16).contiguous()
+        self.score_b = None if score_b is None else score_b.reshape(-1).to(device=device, dtype=torch.float16)
+        self.dbn = None if down_block_norm is None else down_block_norm.reshape(-1).to(torch.float16).to(device)
+        self.R = int(self.enc_w.shape[0])
+        self.NB = int(self.score_w.shape[0])
+        self.basis_top_k = self.R if basis_top_k is None else max(1, min(int(basis_top_k), self.R))
+        self.legacy_abs = bool(legacy_abs)
+
+    def as_struct(self) -> _lib.Router:
+        return _lib.Router(
+            R=self.R, basis_top_k=self.basis_top_k, NB=self.NB,
+            flags=_lib.NSMLP_ROUTE_LEGACY_ABS if self.legacy_abs else 0,
+            enc_w=ptr(self.enc_w), enc_b=ptr(self.enc_b), score_w=ptr(self.score_w), score_b=ptr(self.score_b),
+            down_block_norm=ptr(self.dbn),
+        )
+
+
+class SparseMlpLayer:
+    """Router + slot table: one call per decode token and layer, no host
+    round trip (the decode branch of RT:5833-5923)."""
+
+    def __init__(self, router: SparseMlpRouter, table: SparseMlpSlotTable, top_k: int):
+        if router.NB != table.NB:
+            raise RuntimeError(f"router num_blocks {router.NB} != table num_blocks {table.NB}")
+        self.router = router
+        self.table = table
+        self.top_k = max(1, min(int(top_k), table.NB))
+        self._r = router.as_struct()
+        self._t = table.as_struct()
+        self.device = table.device
+
+    def workspace_bytes(self) -> int:
+        return int(_lib.lib().nsmlp_layer_workspace_bytes(self.table.H, self.router.R, self.router.NB, self.top_k))
+
+    def forward(self, x: torch.Tensor, out: torch.Tensor | None = None, sel_out: torch.Tensor | None = None,
+                ws: torch.Tensor | None = None):
+        x16 = x.reshape(-1)
+        if x16.dtype != torch.float16 or x16.device != self.device or x16.data_ptr() % 16:
+            x16 = x16.to(device=self.device, dtype=torch.float16).contiguous().clone()
+        if out is None:
+            out = torch.empty(self.table.H, dtype=torch.float16, device=self.device)
+        if sel_out is None:
+            sel_out = torch.empty(self.top_k, dtype=torch.int32, device=self.device)
+        if ws is None:
+            ws = workspace(self.workspace_bytes(), self.device)
+        _lib.call("nsmlp_decode_layer_f16", ctypes.byref(self._r), ctypes.byref(self._t), ptr(x16), self.top_k,
+                  ptr(sel_out), ptr(out), ptr(ws), ws.numel(), stream_handle(self.device))
+        return out, sel_out

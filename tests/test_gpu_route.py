@@ -1,0 +1,129 @@
+"""GPU router vs the oracle: selected blocks, latent and scores bit-exact."""
+import numpy as np
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+
+
+def _rand16(rng, shape, std):
+    return (rng.standard_normal(shape) * std).astype(np.float16).view(np.uint16)
+
+
+def _dev(a16, device):
+    return torch.from_numpy(a16.view(np.int16).copy()).view(torch.float16).to(device)
+
+
+def _route_gpu(device, x16, enc_w, enc_b, sw, sb, k, *, btk=None, dbn=None, legacy=False, sorted_by_score=True):
+    from next_step_ai_amd import router
+
+    routing = {"enc_w": _dev(enc_w, device), "enc_b": None if enc_b is None else _dev(enc_b, device)}
+    if legacy:
+        routing["dec_norm_t"] = _dev(sw, device).transpose(0, 1).contiguous()
+    else:
+        routing["route_score_weight"] = _dev(sw, device)
+        routing["route_score_bias"] = None if sb is None else _dev(sb, device)
+    if dbn is not None:
+        routing["down_block_norm"] = torch.from_numpy(dbn)
+    x = _dev(x16, device).reshape(-1, enc_w.shape[1])
+    sel, lat, sc = router.route_tokens(x, routing, k, sorted_by_score=sorted_by_score, basis_top_k=btk,
+                                       return_scores=True)
+    torch.cuda.synchronize()
+    return (sel.cpu().numpy(), lat.cpu().view(torch.int16).numpy().view(np.uint16),
+            sc.cpu().view(torch.int16).numpy().view(np.uint16))
+
+
+CASES = [
+    # H, R, NB, k, btk, std_x
+    (256, 8, 40, 5, None, 1.0),
+    (512, 16, 64, 64, None, 1.0),
+    (1000, 12, 97, 13, 5, 3.0),       # H not a multiple of 8 -> scalar path; basis_top_k mask
+    (4096, 64, 448, 64, None, 1.0),   # 8B shape
+    (16384, 64, 1664, 208, None, 1.0),  # 405B shape
+]
+
+
+@pytest.mark.parametrize("H,R,NB,k,btk,sx", CASES)
+def test_route_matches_oracle(gpu, orc, H, R, NB, k, btk, sx):
+    rng = np.random.default_rng(H + NB)
+    x = _rand16(rng, H, sx)
+    enc_w, enc_b = _rand16(rng, (R, H), 0.02), _rand16(rng, R, 0.02)
+    sw, sb = _rand16(rng, (NB, R), 0.02), _rand16(rng, NB, 0.02)
+    lat_o, sc_o, sel_o = orc.route(x, enc_w, enc_b, sw, sb, k, basis_top_k=btk)
+    sel, lat, sc = _route_gpu(gpu, x, enc_w, enc_b, sw, sb, k, btk=btk)
+    assert np.array_equal(lat[0], lat_o)
+    assert np.array_equal(sc[0], sc_o)
+    assert np.array_equal(sel[0], sel_o)
+    sel_asc, _, _ = _route_gpu(gpu, x, enc_w, enc_b, sw, sb, k, btk=btk, sorted_by_score=False)
+    assert np.array_equal(sel_asc[0], np.sort(sel_o))
+
+
+def test_route_ties_lowest_index(gpu, orc):
+    H, R, NB, k = 256, 4, 300, 37
+    rng = np.random.default_rng(7)
+    x = _rand16(rng, H, 1.0)
+    enc_w, enc_b = _rand16(rng, (R, H), 0.02), _rand16(rng, R, 0.02)
+    sw = np.zeros((NB, R), dtype=np.uint16)
+    # three distinct bias levels, many equal scores at each level
+    sb = np.array([0.5, 0.25, 0.5, 0.125] * (NB // 4), dtype=np.float16).view(np.uint16)
+    _, sc_o, sel_o = orc.route(x, enc_w, enc_b, sw, sb, k)
+    sel, _, sc = _route_gpu(gpu, x, enc_w, enc_b, sw, sb, k)
+    assert np.array_equal(sel[0], sel_o)
+    assert np.array_equal(sel[0], np.arange(0, 4 * k, 2)[:k])  # all 0.5's, lowest indices first
+
+
+def test_route_all_blocks_and_one_block(gpu, orc):
+    H, R, NB = 256, 8, 50
+    rng = np.random.default_rng(11)
+    x = _rand16(rng, H, 1.0)
+    enc_w, enc_b = _rand16(rng, (R, H), 0.02), _rand16(rng, R, 0.02)
+    sw, sb = _rand16(rng, (NB, R), 0.5), _rand16(rng, NB, 0.02)
+    for k in (1, NB):
+        _, _, sel_o = orc.route(x, enc_w, enc_b, sw, sb, k)
+        sel, _, _ = _route_gpu(gpu, x, enc_w, enc_b, sw, sb, k)
+        assert np.array_equal(sel[0], sel_o)
+
+
+def test_route_legacy_abs_and_down_block_norm(gpu, orc):
+    H, R, NB, k = 512, 16, 96, 9
+    rng = np.random.default_rng(13)
+    x = _rand16(rng, H, 1.0)
+    enc_w, enc_b = _rand16(rng, (R, H), 0.02), _rand16(rng, R, 0.02)
+    sw = _rand16(rng, (NB, R), 0.02)
+    absw = (sw & 0x7FFF).astype(np.uint16)
+    dbn = (rng.random(NB) * 2).astype(np.float32)
+    lat_o, sc_o, sel_o = orc.route(x, enc_w, enc_b, absw, None, k, legacy_abs=True, down_block_norm=dbn)
+    sel, lat, sc = _route_gpu(gpu, x, enc_w, enc_b, absw, None, k, legacy=True, dbn=dbn)
+    assert np.array_equal(lat[0], lat_o)
+    assert np.array_equal(sc[0], sc_o)
+    assert np.array_equal(sel[0], sel_o)
+
+
+def test_route_multi_row(gpu, orc):
+    H, R, NB, k, N = 2048, 32, 256, 24, 5
+    rng = np.random.default_rng(17)
+    x = _rand16(rng, (N, H), 1.0)
+    enc_w, enc_b = _rand16(rng, (R, H), 0.02), _rand16(rng, R, 0.02)
+    sw, sb = _rand16(rng, (NB, R), 0.02), _rand16(rng, NB, 0.02)
+    sel, _, _ = _route_gpu(gpu, x, enc_w, enc_b, sw, sb, k)
+    for t in range(N):
+        _, _, sel_o = orc.route(x[t], enc_w, enc_b, sw, sb, k)
+        assert np.array_equal(sel[t], sel_o)
+
+
+def test_route_sparse_mlp_dropin(gpu, orc):
+    from next_step_ai_amd.router import route_sparse_mlp
+
+    H, R, NB, k = 1024, 16, 128, 11
+    rng = np.random.default_rng(19)
+    x = _rand16(rng, (1, 3, H), 1.0)
+    enc_w, enc_b = _rand16(rng, (R, H), 0.02), _rand16(rng, R, 0.02)
+    sw, sb = _rand16(rng, (NB, R), 0.02), _rand16(rng, NB, 0.02)
+    routing = {"enc_w": _dev(enc_w, gpu), "enc_b": _dev(enc_b, gpu), "route_score_weight": _dev(sw, gpu),
+               "route_score_bias": _dev(sb, gpu), "down_block_norm": None, "top_k": k, "basis_top_k": R}
+    out = route_sparse_mlp(_dev(x, gpu).reshape(1, 3, H), routing)
+    assert out.dtype == torch.int64 and tuple(out.shape) == (3, k)
+    for t in range(3):
+        _, _, sel_o = orc.route(x[0, t], enc_w, enc_b, sw, sb, k)
+        assert np.array_equal(out[t].cpu().numpy(), sel_o)
+    assert route_sparse_mlp(_dev(x, gpu), None) is None
