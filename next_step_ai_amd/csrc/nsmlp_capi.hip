@@ -90,7 +90,7 @@ int choose_groups(int H, int k) {
 }
 
 struct DecodeWs {
-  size_t part, act, outpart, total;
+  size_t part, act, act_scale, outpart, total;
 };
 
 DecodeWs decode_ws_layout(int H, int k) {
@@ -99,7 +99,9 @@ DecodeWs decode_ws_layout(int H, int k) {
   w.part = off;
   off += align_up((size_t)k * (size_t)(H / 256) * 64 * sizeof(float));
   w.act = off;
-  off += align_up((size_t)k * 32 * sizeof(float));
+  off += align_up((size_t)k * 16 * sizeof(uint32_t));
+  w.act_scale = off;
+  off += align_up((size_t)k * sizeof(float));
   w.outpart = off;
   off += align_up((size_t)kMaxGroups * (size_t)H * sizeof(float));
   w.total = off;
@@ -147,8 +149,8 @@ ProjView down_block_major_view(const uint8_t* packed, const float* absmax, int H
 int validate_decode_shape(int H, int qbs, int k) {
   if (H <= 0 || H % 256 != 0 || H > (1 << 18))
     return set_error(NSMLP_EINVAL, "hidden size %d must be a positive multiple of 256", H);
-  if (qbs <= 0 || qbs % 32 != 0 || H % qbs != 0)
-    return set_error(NSMLP_EINVAL, "quant block size %d must be a multiple of 32 dividing hidden size %d", qbs, H);
+  if (qbs < 32 || (qbs & (qbs - 1)) != 0 || H % qbs != 0)
+    return set_error(NSMLP_EINVAL, "quant block size %d must be a power of two >= 32 dividing hidden size %d", qbs, H);
   if (k <= 0 || k > kMaxK) return set_error(NSMLP_EINVAL, "k=%d out of range [1, %d]", k, kMaxK);
   if (H / kRowsPerChunk > kMaxRowChunks) return set_error(NSMLP_EINVAL, "hidden size %d too large", H);
   return NSMLP_OK;
@@ -164,19 +166,32 @@ int fill_decode_ws(DecodeArgs& a, void* ws, size_t ws_bytes) {
   a.blk_count = (int*)(base + kBlkCountOff);
   a.row_count = (int*)(base + kRowCountOff);
   a.part = (float*)(base + L.part);
-  a.act = (float*)(base + L.act);
+  // streaming path: [k][32] activations and [k] block references fit in the
+  // [k][H/256][64] split partials of the generic path
+  a.st_act = a.part;
+  a.st_enc = (uint32_t*)(a.part + (size_t)a.k * 32);
+  a.act = (uint32_t*)(base + L.act);
+  a.act_scale = (float*)(base + L.act_scale);
   a.outpart = (float*)(base + L.outpart);
   return NSMLP_OK;
 }
 
 void fill_decode_tiling(DecodeArgs& a) {
+  a.qbs_shift = __builtin_ctz((unsigned)a.qbs);
   a.cs = choose_cs(a.H, a.k);
   a.splits = a.H / a.cs;
   a.groups = choose_groups(a.H, a.k);
   a.rows_per_chunk = kRowsPerChunk;
+  a.chunks = (a.H + kRowsPerChunk - 1) / kRowsPerChunk;
+  a.st_gu_wgs = 0;
+  if (env_int("NSMLP_DECODE_SPLIT", 0) == 0) plan_streaming(a, device_cus());
 }
 
 int run_decode(const DecodeArgs& a, hipStream_t s) {
+  if (a.st_gu_wgs > 0) {
+    launch_decode_streaming(a, s);
+    return check_launch("decode");
+  }
   launch_decode_gate_up(a, s);
   int rc = check_launch("decode gate/up");
   if (rc) return rc;

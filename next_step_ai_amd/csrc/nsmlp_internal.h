@@ -125,9 +125,161 @@ __device__ __forceinline__ Exact3 wave_sum_exact(Exact3 e) {
 }
 
 // ------------------------------------------------------------ NF4 decode --
-// 32 NF4 nibbles packed in 16 bytes (element 2i in the high nibble of byte i)
-// dotted with 32 fp32 activations; the code book sits in LDS.
-__device__ __forceinline__ float nf4_dot32(const uint4 w, const float* __restrict__ xf, const float* lut) {
+// A byte holds two NF4 codes: element 2i in the high nibble, 2i+1 in the low
+// nibble.  The code books live in LDS as fp16 values at a 16-byte stride
+// (entry n at byte 16n: the 16 entries sit in 16 distinct banks), so the LDS
+// address of a nibble is the nibble times 16, which one SDWA instruction
+// produces straight from the packed byte:
+//   high nibble: byte & 0xF0                    -> v_and_b32_sdwa  (src1_sel:BYTE_b)
+//   low nibble : (byte << 4) & 0xFF             -> v_lshlrev_b32_sdwa (dst_sel:BYTE_0)
+// The two fp16 codes of a byte form a half2 that v_dot2_f32_f16 multiplies
+// with the matching fp16 activation pair, accumulating in fp32.
+typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
+
+#define NSMLP_NIB_HELPERS(B)                                                                          \
+  __device__ __forceinline__ uint32_t nib_hi16_##B(uint32_t w) {                                      \
+    uint32_t r;                                                                                       \
+    asm("v_and_b32_sdwa %0, %1, %2 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:BYTE_" #B \
+        : "=v"(r) : "v"(0xF0u), "v"(w));                                                              \
+    return r;                                                                                         \
+  }                                                                                                   \
+  __device__ __forceinline__ uint32_t nib_lo16_##B(uint32_t w) {                                      \
+    uint32_t r;                                                                                       \
+    asm("v_lshlrev_b32_sdwa %0, %1, %2 dst_sel:BYTE_0 dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:BYTE_" #B \
+        : "=v"(r) : "v"(4u), "v"(w));                                                                 \
+    return r;                                                                                         \
+  }
+NSMLP_NIB_HELPERS(0)
+NSMLP_NIB_HELPERS(1)
+NSMLP_NIB_HELPERS(2)
+NSMLP_NIB_HELPERS(3)
+#undef NSMLP_NIB_HELPERS
+
+__device__ __forceinline__ half2_t as_half2(uint32_t v) { return __builtin_bit_cast(half2_t, v); }
+
+__device__ __forceinline__ _Float16 lut_at(const char* lut, uint32_t off) {
+  return *reinterpret_cast<const _Float16*>(lut + off);
+}
+
+// Codes of the 8 nibbles of one packed dword, dotted with 4 activation pairs.
+__device__ __forceinline__ float nf4_dot8(uint32_t v, const uint32_t* xp, const char* lut, float acc) {
+  half2_t c0 = {lut_at(lut, nib_hi16_0(v)), lut_at(lut, nib_lo16_0(v))};
+  half2_t c1 = {lut_at(lut, nib_hi16_1(v)), lut_at(lut, nib_lo16_1(v))};
+  half2_t c2 = {lut_at(lut, nib_hi16_2(v)), lut_at(lut, nib_lo16_2(v))};
+  half2_t c3 = {lut_at(lut, nib_hi16_3(v)), lut_at(lut, nib_lo16_3(v))};
+  acc = __builtin_amdgcn_fdot2(c0, as_half2(xp[0]), acc, false);
+  acc = __builtin_amdgcn_fdot2(c1, as_half2(xp[1]), acc, false);
+  acc = __builtin_amdgcn_fdot2(c2, as_half2(xp[2]), acc, false);
+  acc = __builtin_amdgcn_fdot2(c3, as_half2(xp[3]), acc, false);
+  return acc;
+}
+
+// 32 NF4 codes (16 bytes) dotted with 16 activation pairs.
+__device__ __forceinline__ float nf4_dot32(const uint4 w, const uint32_t* xp, const char* lut) {
+  float acc = nf4_dot8(w.x, xp, lut, 0.0f);
+  acc = nf4_dot8(w.y, xp + 4, lut, acc);
+  acc = nf4_dot8(w.z, xp + 8, lut, acc);
+  return nf4_dot8(w.w, xp + 12, lut, acc);
+}
+
+// Byte-indexed code-pair table: entry b (4 bytes at offset 4b) holds the fp16
+// codes of the byte's high nibble (low half) and low nibble (high half), so
+// one LDS read yields the half2 for v_dot2.  The offset 4b comes from one
+// SDWA shift.
+#define NSMLP_BYTE4_HELPER(B)                                                                         \
+  __device__ __forceinline__ uint32_t byte_x4_##B(uint32_t w) {                                       \
+    uint32_t r;                                                                                       \
+    asm("v_lshlrev_b32_sdwa %0, %1, %2 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:BYTE_" #B \
+        : "=v"(r) : "v"(2u), "v"(w));                                                                 \
+    return r;                                                                                         \
+  }
+NSMLP_BYTE4_HELPER(0)
+NSMLP_BYTE4_HELPER(1)
+NSMLP_BYTE4_HELPER(2)
+NSMLP_BYTE4_HELPER(3)
+#undef NSMLP_BYTE4_HELPER
+
+__device__ __forceinline__ uint32_t pair_at(const char* lut, uint32_t off) {
+  return *reinterpret_cast<const uint32_t*>(lut + off);
+}
+
+__device__ __forceinline__ float nf4_dot8_pairs(uint32_t v, const uint32_t* xp, const char* lut, float acc) {
+  const uint32_t p0 = pair_at(lut, byte_x4_0(v)), p1 = pair_at(lut, byte_x4_1(v));
+  const uint32_t p2 = pair_at(lut, byte_x4_2(v)), p3 = pair_at(lut, byte_x4_3(v));
+  acc = __builtin_amdgcn_fdot2(as_half2(p0), as_half2(xp[0]), acc, false);
+  acc = __builtin_amdgcn_fdot2(as_half2(p1), as_half2(xp[1]), acc, false);
+  acc = __builtin_amdgcn_fdot2(as_half2(p2), as_half2(xp[2]), acc, false);
+  acc = __builtin_amdgcn_fdot2(as_half2(p3), as_half2(xp[3]), acc, false);
+  return acc;
+}
+
+// 32 NF4 codes dotted with 16 activation pairs through the byte-pair table.
+__device__ __forceinline__ float nf4_dot32_pairs(const uint4 w, const uint32_t* xp, const char* lut) {
+  float acc = nf4_dot8_pairs(w.x, xp, lut, 0.0f);
+  acc = nf4_dot8_pairs(w.y, xp + 4, lut, acc);
+  acc = nf4_dot8_pairs(w.z, xp + 8, lut, acc);
+  return nf4_dot8_pairs(w.w, xp + 12, lut, acc);
+}
+
+// Fill the 256-entry byte-pair table (1 KB of LDS); needs >= 256 threads.
+__device__ __forceinline__ void pair_lut_fill(char* lut, const float* code, int tid) {
+  if (tid < 256) {
+    const uint32_t hi = __builtin_bit_cast(uint16_t, (_Float16)code[tid >> 4]);
+    const uint32_t lo = __builtin_bit_cast(uint16_t, (_Float16)code[tid & 15]);
+    reinterpret_cast<uint32_t*>(lut)[tid] = hi | (lo << 16);
+  }
+}
+
+// Lane-replicated byte-pair table (64 KB of LDS, which must start at LDS
+// address 0): entry e of copy c sits at byte e * 256 + c * 4, so a lane that
+// always reads copy c always hits bank c and the 64 lookups of a wave never
+// conflict, whatever bytes they decode.  The lane keeps c * 4 in the low byte
+// of an address register; one SDWA move writes the packed byte into bits
+// 8..15 and preserves the rest, so a lookup costs one VALU op and one
+// ds_read_b32.
+constexpr int kRepLutBytes = 65536;
+
+#define NSMLP_SET_BYTE1(ad, w, sel) \
+  asm("v_mov_b32_sdwa %0, %1 dst_sel:BYTE_1 dst_unused:UNUSED_PRESERVE src0_sel:" sel : "+v"(ad) : "v"(w))
+
+typedef const __attribute__((address_space(3))) uint32_t* lds_u32_ptr;
+__device__ __forceinline__ uint32_t lds_ld_u32(uint32_t byte_addr) {
+  return *reinterpret_cast<lds_u32_ptr>(static_cast<uintptr_t>(byte_addr));
+}
+
+__device__ __forceinline__ float rep_dot8(uint32_t v, const uint32_t* xp, uint32_t (&ad)[4], float acc) {
+  NSMLP_SET_BYTE1(ad[0], v, "BYTE_0");
+  NSMLP_SET_BYTE1(ad[1], v, "BYTE_1");
+  NSMLP_SET_BYTE1(ad[2], v, "BYTE_2");
+  NSMLP_SET_BYTE1(ad[3], v, "BYTE_3");
+  const uint32_t p0 = lds_ld_u32(ad[0]), p1 = lds_ld_u32(ad[1]);
+  const uint32_t p2 = lds_ld_u32(ad[2]), p3 = lds_ld_u32(ad[3]);
+  acc = __builtin_amdgcn_fdot2(as_half2(p0), as_half2(xp[0]), acc, false);
+  acc = __builtin_amdgcn_fdot2(as_half2(p1), as_half2(xp[1]), acc, false);
+  acc = __builtin_amdgcn_fdot2(as_half2(p2), as_half2(xp[2]), acc, false);
+  acc = __builtin_amdgcn_fdot2(as_half2(p3), as_half2(xp[3]), acc, false);
+  return acc;
+}
+
+// 32 NF4 codes (16 packed bytes) dotted with 16 fp16 pairs, fp32 accumulation
+// in element order (the same sequence of v_dot2 as nf4_dot32_pairs).
+__device__ __forceinline__ float rep_dot32(const uint4 w, const uint32_t* xp, uint32_t (&ad)[4]) {
+  float acc = rep_dot8(w.x, xp, ad, 0.0f);
+  acc = rep_dot8(w.y, xp + 4, ad, acc);
+  acc = rep_dot8(w.z, xp + 8, ad, acc);
+  return rep_dot8(w.w, xp + 12, ad, acc);
+}
+
+// Nontemporal (streaming) loads for weight data read exactly once.
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ uint4 ld_stream16(const uint8_t* p) {
+  const u32x4_t t = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(p));
+  return make_uint4(t.x, t.y, t.z, t.w);
+}
+__device__ __forceinline__ float ld_stream_f32(const float* p) { return __builtin_nontemporal_load(p); }
+
+// fp32 variant for the multi-row linears: code book as 16 fp32 values in LDS.
+__device__ __forceinline__ float nf4_dot32_f32(const uint4 w, const float* __restrict__ xf, const float* lut) {
   float acc = 0.0f;
   const uint32_t words[4] = {w.x, w.y, w.z, w.w};
 #pragma unroll
@@ -141,6 +293,34 @@ __device__ __forceinline__ float nf4_dot32(const uint4 w, const float* __restric
     }
   }
   return acc;
+}
+
+// Fill a 16-entry fp16 code book at a 16-byte stride (256 bytes of LDS).
+__device__ __forceinline__ void lut_fill(char* lut, const float* code, int tid) {
+  if (tid < 16) *reinterpret_cast<_Float16*>(lut + 16 * tid) = (_Float16)code[tid];
+}
+
+// Coherent (L2 write-through / bypass) accesses for data handed between
+// workgroups inside one launch; ordering: stores, then s_waitcnt vmcnt(0),
+// then the counter atomic.
+__device__ __forceinline__ void st_coherent(float* p, float v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void st_coherent_u32(uint32_t* p, uint32_t v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float ld_coherent(const float* p) {
+  return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void wait_stores() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+__device__ __forceinline__ int ld_coherent_i32(const int* p) {
+  return __hip_atomic_load(const_cast<int*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint32_t ld_coherent_u32(const uint32_t* p) {
+  return __hip_atomic_load(const_cast<uint32_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void st_coherent_i32(int* p, int v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 __device__ __forceinline__ float silu_mul(float g, float u) { return g / (1.0f + __expf(-g)) * u; }
@@ -161,6 +341,7 @@ struct DecodeArgs {
   const uint16_t* x;    // [H] fp16
   int H;
   int qbs;
+  int qbs_shift;         // log2(qbs)
   int k;                 // selected blocks
   int cs;                // columns per gate/up split
   int splits;            // H / cs
@@ -184,11 +365,24 @@ struct DecodeArgs {
   float* out_f32;        // [H] fp32 result before rounding, or nullptr
   // workspace
   float* part;           // [k][splits][64]
-  float* act;            // [k][32]
+  uint32_t* act;         // [k][16] fp16 pairs of silu(gate)*up, scaled by 2^act_exp
+  float* act_scale;      // [k] 2^-act_exp (undoes the scaling)
   int* blk_count;        // [k]
   float* outpart;        // [groups][H]
   int* row_count;        // [H / rows_per_chunk]
   int* status;           // [1] device error flag
+  int chunks;            // down row chunks
+  // streaming path (hidden size a multiple of 2048)
+  float* st_act;         // [k][32] silu(gate) * up of the selected blocks
+  uint32_t* st_enc;      // [k] resolved block references
+  int st_gu_wgs;         // gate/up workgroups (0: streaming path not used)
+  int st_gu_rounds;      // gate/up rounds per workgroup
+  int st_dn_gx;          // down workgroups per 64-row chunk (block groups)
+  int st_dn_per;         // blocks per down wave (<= 64)
+  int st_gu_bytes;       // extent of one gate/up slot: packed bytes, absmax bytes
+  int st_gu_abytes;
+  int st_dn_bytes;       // extent of one down block: packed bytes, absmax bytes
+  int st_dn_abytes;
 };
 
 // Resolve selected position j to (storage view index, validity):
@@ -219,6 +413,12 @@ __device__ __forceinline__ BlockRef resolve_block(const DecodeArgs& a, int j) {
 
 void launch_decode_gate_up(const DecodeArgs& a, hipStream_t s);
 void launch_decode_down(const DecodeArgs& a, hipStream_t s);
+// Streaming decode (hidden size a multiple of 2048): gate/up, down, final sum.
+// Sets the st_* tiling fields for a device with `cus` compute units; false
+// (and st_gu_wgs = 0) when the streaming kernels do not apply.
+bool plan_streaming(DecodeArgs& a, int cus);
+void launch_decode_streaming(const DecodeArgs& a, hipStream_t s);
+int device_cus();
 
 struct RouteArgs {
   const uint16_t* x;       // [rows][H]

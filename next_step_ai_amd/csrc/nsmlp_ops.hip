@@ -53,7 +53,7 @@ __global__ void __launch_bounds__(kThreads) k_out_partial(LinearArgs a) {
   __syncthreads();
 #pragma unroll
   for (int i = 0; i < NR; ++i) {
-    float acc = nf4_dot32(w[i], xf, lut) * am[i];
+    float acc = nf4_dot32_f32(w[i], xf, lut) * am[i];
 #pragma unroll
     for (int m = LPR / 2; m >= 1; m >>= 1) acc += __shfl_xor(acc, m, kWave);
     if (cc == 0) a.part[((long long)task * a.splits + s) * 32 + r0 + i * kStep] = acc;
@@ -118,7 +118,7 @@ __global__ void __launch_bounds__(kThreads) k_in_linear(LinearArgs a) {
     }
 #pragma unroll
     for (int i = 0; i < kInBatch; ++i)
-      if (slots[i] >= 0) acc += nf4_dot32(w[i], xs[i], lut) * am[i];
+      if (slots[i] >= 0) acc += nf4_dot32_f32(w[i], xs[i], lut) * am[i];
   }
   if (live) {
     if (a.bias != nullptr) acc += h2f(a.bias[o]);

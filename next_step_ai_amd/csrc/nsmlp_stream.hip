@@ -1,0 +1,532 @@
+// Streaming sparse-MLP decode for hidden sizes that are a multiple of 2048
+// (one wave covers a 2048-column split: 64 lanes x 32 columns).
+//
+//   k_gu_rep    gate/up.  An 8-wave workgroup works in rounds; in a round every
+//               wave decodes one item: gate rows 2p, 2p+1 and up rows 2p, 2p+1
+//               of one selected block over the wave's split (4 x 1 KB of
+//               packed NF4, 16 bytes per lane and row), the token's split held
+//               in registers as fp16 pairs.  Items stream through a register
+//               pipeline of kGuStages rounds.  Each wave reduces its 4 row sums
+//               over its lanes; the split sums meet in LDS behind one s_barrier
+//               per round (LDS counter only: the loads in flight are not
+//               drained) and two lanes write silu(gate) * up of rows 2p, 2p+1
+//               (fp32, splits added in order).  Gate/up biases and the flat
+//               mask are applied there, in a separate instantiation, so that
+//               the plain path has no loads outside the weight stream.  The
+//               kernel also publishes the resolved block references.
+//   k_down_rep  down.  A workgroup owns 64 output rows (one per lane) and one
+//               group of selected blocks, split over its 8 waves.  It turns
+//               the group's activations into fp16 pairs scaled by a power of
+//               two per block (max |act| in [0.5, 1)), then every wave streams
+//               2-block items (16 packed bytes and one absmax per row and
+//               block) through a register pipeline, accumulating in fp32 in
+//               block order; the 8 wave sums meet in LDS (wave order).  When
+//               the 64-row chunks alone give a workgroup per CU (one group),
+//               the workgroup writes the fp16 output itself; otherwise it
+//               writes a partial and k_fin_rep adds the groups in order.
+//
+// Weights are read with buffer loads through a per-block descriptor whose
+// extent is zero for an invalid block or a round past the end: such a load
+// returns zeros without touching memory, so every load in the stream is
+// unconditional and the compiler's wait counts stay exact (a branch around a
+// load would make it wait for the whole pipeline).  Both streaming kernels
+// decode through the lane-replicated byte-pair table (64 KB of dynamic LDS at
+// address 0; no static LDS in these kernels), filled with 16-byte LDS writes
+// while the first weight loads are in flight.  Block references are resolved
+// once, lane i holding item i, and read with v_readlane per item, so no
+// dependent lookups sit in the stream.
+#include <mutex>
+
+#include "nsmlp_internal.h"
+
+namespace nsmlp {
+
+namespace {
+
+constexpr int kSplit = 2048;               // columns per split
+constexpr int kWaves = 8;                  // waves per workgroup
+constexpr int kThreads8 = kWaves * kWave;  // 512
+constexpr int kGuStages = 4;
+constexpr int kDnStages = 6;
+constexpr int kMaxItems = 64;      // items per wave resolved up front (one per lane)
+constexpr int kMaxDnBlocks = 512;  // blocks per down workgroup (activations in LDS)
+constexpr int kLutWords = kRepLutBytes / 4;
+// dynamic LDS: table, split sums [2][8][4]
+constexpr size_t kGuLds = kRepLutBytes + 2 * kWaves * 4 * sizeof(float);
+// dynamic LDS: table, activation pairs [512][16], scales [512], wave sums [8][64]
+constexpr size_t kDnLds = kRepLutBytes + kMaxDnBlocks * 16 * 4 + kMaxDnBlocks * 4 + kWaves * kWave * 4;
+
+// Encoded block reference: < 2^30 -> HBM slot; bit 30 -> host copy of the
+// block id in the low bits; bit 31 -> invalid (zero contribution).
+constexpr uint32_t kHostBit = 0x40000000u;
+constexpr uint32_t kBad = 0x80000000u;
+
+__device__ __forceinline__ uint32_t encode_ref(const BlockRef& br) {
+  if (!br.ok) return kBad;
+  return br.dev ? (uint32_t)br.q : (kHostBit | (uint32_t)br.q);
+}
+
+__device__ __forceinline__ uint32_t lane_value(uint32_t v, int lane) {
+  return (uint32_t)__builtin_amdgcn_readlane((int)v, lane);
+}
+
+// Wait for this wave's LDS traffic, then the workgroup barrier.  Loads from
+// global memory that are in flight stay in flight.
+__device__ __forceinline__ void lds_barrier() {
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
+// Keeps the compiler from moving instructions across this point (load issue
+// order decides which waits drain the weight stream).
+__device__ __forceinline__ void sched_fence() { __builtin_amdgcn_sched_barrier(0); }
+
+// Raw buffer descriptors (gfx9 family dword format) and nontemporal loads.
+typedef __amdgpu_buffer_rsrc_t rsrc_t;
+constexpr int kRsrcWord3 = 0x00020000;
+constexpr int kNontemporal = 2;
+
+__device__ __forceinline__ rsrc_t make_rsrc(const void* base, int bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, bytes, kRsrcWord3);
+}
+__device__ __forceinline__ uint4 buf_ld16(rsrc_t r, uint32_t voff, uint32_t soff) {
+  const u32x4_t t = __builtin_amdgcn_raw_buffer_load_b128(r, (int)voff, (int)soff, kNontemporal);
+  return make_uint4(t.x, t.y, t.z, t.w);
+}
+__device__ __forceinline__ float buf_ldf(rsrc_t r, uint32_t voff, uint32_t soff) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, (int)voff, (int)soff, kNontemporal));
+}
+
+// Replicated pair table, filled by 512 threads in 8 passes of one 16-byte LDS
+// write each: pass ps writes entry e = 32 ps + tid / 16, copies 4 (tid % 16)
+// .. +3 (copies 0..31 decode code_a, 32..63 code_b).  The entry's low half is
+// the code of its high nibble (e / 16 = 2 ps + tid / 256), the high half the
+// code of its low nibble ((tid / 16) % 16).
+struct LutCodes {
+  float lo[8];
+  float hi;
+};
+
+__device__ __forceinline__ void lut_codes_load(const float* code_a, const float* code_b, int tid, LutCodes& c) {
+  const float* code = (tid & 15) >= 8 ? code_b : code_a;
+#pragma unroll
+  for (int ps = 0; ps < 8; ++ps) c.lo[ps] = code[2 * ps + (tid >> 8)];
+  c.hi = code[(tid >> 4) & 15];
+}
+
+__device__ __forceinline__ void lut_store(uint32_t* lut, const LutCodes& c, int tid) {
+  const uint32_t hi = (uint32_t)f2h(c.hi) << 16;
+#pragma unroll
+  for (int ps = 0; ps < 8; ++ps) {
+    const uint32_t v = (uint32_t)f2h(c.lo[ps]) | hi;
+    const int e = ps * 32 + (tid >> 4);
+    *reinterpret_cast<uint4*>(lut + e * 64 + (tid & 15) * 4) = make_uint4(v, v, v, v);
+  }
+}
+
+struct GuStage {
+  uint4 w[4];  // gate 2p, gate 2p+1, up 2p, up 2p+1: this lane's 32 columns
+  float am[4];
+};
+
+// Issue the loads of one item (block reference enc, row pair p).  cb / ca4:
+// this lane's byte offsets of its columns inside a row of packed / absmax.
+__device__ __forceinline__ void gu_issue(const DecodeArgs& a, uint32_t enc, int p, uint32_t cb, uint32_t ca4,
+                                         GuStage& st) {
+  const bool bad = (enc & kBad) != 0;
+  const bool dev = (enc & kHostBit) == 0;
+  const long long q = bad ? 0 : (long long)(enc & (kHostBit - 1));
+  const int nb = bad ? 0 : a.st_gu_bytes, na = bad ? 0 : a.st_gu_abytes;
+  const rsrc_t rg = make_rsrc((dev ? a.gate.packed : a.host_gate.packed) + q * a.gate.blk_stride, nb);
+  const rsrc_t ru = make_rsrc((dev ? a.up.packed : a.host_up.packed) + q * a.up.blk_stride, nb);
+  const rsrc_t rga = make_rsrc((dev ? a.gate.absmax : a.host_gate.absmax) + q * a.gate.abs_blk_stride, na);
+  const rsrc_t rua = make_rsrc((dev ? a.up.absmax : a.host_up.absmax) + q * a.up.abs_blk_stride, na);
+  const uint32_t rs = (uint32_t)a.gate.row_stride, ars4 = (uint32_t)a.gate.abs_row_stride * 4u;
+  const uint32_t s0 = (uint32_t)(2 * p) * rs, as0 = (uint32_t)(2 * p) * ars4;
+  st.w[0] = buf_ld16(rg, cb, s0);
+  st.w[1] = buf_ld16(rg, cb, s0 + rs);
+  st.w[2] = buf_ld16(ru, cb, s0);
+  st.w[3] = buf_ld16(ru, cb, s0 + rs);
+  st.am[0] = buf_ldf(rga, ca4, as0);
+  st.am[1] = buf_ldf(rga, ca4, as0 + ars4);
+  st.am[2] = buf_ldf(rua, ca4, as0);
+  st.am[3] = buf_ldf(rua, ca4, as0 + ars4);
+}
+
+// Reduce-scatter of 4 per-lane row sums over the 64 lanes: afterwards every
+// lane holds the full sum of row (lane >> 4) & 3.
+__device__ __forceinline__ float reduce4(const float (&v)[4], int lane) {
+  const bool b5 = lane & 32, b4 = lane & 16;
+  const float s0 = b5 ? v[0] : v[2], s1 = b5 ? v[1] : v[3];
+  float k0 = b5 ? v[2] : v[0], k1 = b5 ? v[3] : v[1];
+  k0 += __shfl_xor(s0, 32, kWave);
+  k1 += __shfl_xor(s1, 32, kWave);
+  const float s = b4 ? k0 : k1;
+  float k = b4 ? k1 : k0;
+  k += __shfl_xor(s, 16, kWave);
+  k += __shfl_xor(k, 8, kWave);
+  k += __shfl_xor(k, 4, kWave);
+  k += __shfl_xor(k, 2, kWave);
+  k += __shfl_xor(k, 1, kWave);
+  return k;
+}
+
+template <bool AFFINE>
+__global__ void __launch_bounds__(kThreads8, 2) k_gu_rep(DecodeArgs a) {
+  extern __shared__ __attribute__((aligned(16))) uint32_t lds[];
+  float* comb = reinterpret_cast<float*>(lds + kLutWords);
+  const int tid = threadIdx.x, lane = tid & (kWave - 1);
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform per wave
+  const int S = a.splits;                                     // 1, 2, 4 or 8
+  const int NS = kWaves / S;
+  const int s = wave & (S - 1), q = wave / S;
+  const int R = a.st_gu_rounds;
+  const int nwg = (int)gridDim.x, wg = (int)blockIdx.x;
+  const int n_items = 16 * a.k;
+  const uint32_t col = (uint32_t)(s * kSplit + lane * 32);
+  const uint32_t cb = col >> 1, ca4 = (col >> a.qbs_shift) * 4u;
+
+  // lane i: block reference of this wave's round-i item.  Split 0 of row
+  // pair 0 reports an invalid block and publishes the reference.
+  uint32_t enc_v = kBad;
+  {
+    const int id = (lane * nwg + wg) * NS + q;
+    if (lane < R && id < n_items) {
+      const BlockRef br = resolve_block(a, id >> 4);
+      enc_v = encode_ref(br);
+      if (s == 0 && (id & 15) == 0) {
+        if (!br.ok && !br.silent) atomicOr(a.status, 1);
+        a.st_enc[id >> 4] = enc_v;
+      }
+    }
+  }
+  // The code book and the token split are loaded while the references
+  // resolve, and before the weight stream, so that waiting for them never
+  // drains it.
+  LutCodes codes;
+  lut_codes_load(a.code, a.code_up, tid, codes);
+  uint32_t xp[16];
+  {
+    const uint4* xv = reinterpret_cast<const uint4*>(a.x + col);
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const uint4 t = xv[v];
+      xp[4 * v] = t.x;
+      xp[4 * v + 1] = t.y;
+      xp[4 * v + 2] = t.z;
+      xp[4 * v + 3] = t.w;
+    }
+  }
+  sched_fence();
+  GuStage st[kGuStages];
+#pragma unroll
+  for (int i = 0; i < kGuStages; ++i)
+    gu_issue(a, i < R ? lane_value(enc_v, i) : kBad, ((i * nwg + wg) * NS + q) & 15, cb, ca4, st[i]);
+  sched_fence();
+
+  lut_store(lds, codes, tid);
+  lds_barrier();
+
+  uint32_t adg[4], adu[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    adg[i] = (uint32_t)(lane & 31) * 4u;
+    adu[i] = 128u + (uint32_t)(lane & 31) * 4u;
+  }
+
+  for (int r0 = 0; r0 < R; r0 += kGuStages) {
+#pragma unroll
+    for (int i = 0; i < kGuStages; ++i) {
+      const int r = r0 + i;
+      const bool live = r < R;  // uniform over the workgroup
+      float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+      if (live) {
+        acc[0] = rep_dot32(st[i].w[0], xp, adg) * st[i].am[0];
+        acc[1] = rep_dot32(st[i].w[1], xp, adg) * st[i].am[1];
+        acc[2] = rep_dot32(st[i].w[2], xp, adu) * st[i].am[2];
+        acc[3] = rep_dot32(st[i].w[3], xp, adu) * st[i].am[3];
+      }
+      const int rn = r + kGuStages;
+      gu_issue(a, rn < R ? lane_value(enc_v, rn < kMaxItems ? rn : 0) : kBad, ((rn * nwg + wg) * NS + q) & 15, cb,
+               ca4, st[i]);
+      if (live) {
+        const float v = reduce4(acc, lane);
+        if ((lane & 15) == 0) comb[(r & 1) * (kWaves * 4) + wave * 4 + (lane >> 4)] = v;
+        lds_barrier();
+        const int id = (r * nwg + wg) * NS + q;
+        if (s == 0 && lane < 2 && id < n_items) {
+          // row 2p + lane: gate and up sums, splits added in order
+          const float* cs = comb + (r & 1) * (kWaves * 4) + q * S * 4;
+          float g = 0.0f, u = 0.0f;
+          for (int sp = 0; sp < S; ++sp) {
+            g += cs[sp * 4 + lane];
+            u += cs[sp * 4 + 2 + lane];
+          }
+          const int j = id >> 4;
+          const int n = 2 * (id & 15) + lane;
+          if constexpr (AFFINE) {
+            const uint32_t enc = lane_value(enc_v, r);
+            if (!(enc & kBad)) {
+              const long long bn = (long long)(a.sel ? a.sel[j] : j) * 32 + n;
+              if (a.gate_bias != nullptr) g += h2f(a.gate_bias[bn]);
+              if (a.up_bias != nullptr) u += h2f(a.up_bias[bn]);
+              if (a.mask != nullptr) {
+                const float m = h2f(a.mask[bn]);
+                g *= m;
+                u *= m;
+              }
+            }
+          }
+          a.st_act[(long long)j * 32 + n] = silu_mul(g, u);
+        }
+      }
+    }
+  }
+}
+
+struct DnStage {
+  uint4 w[2];
+  float am[2];
+};
+
+__device__ __forceinline__ void dn_issue(const DecodeArgs& a, uint32_t enc, uint32_t roff, uint32_t aroff4, uint4& w,
+                                         float& am) {
+  const bool bad = (enc & kBad) != 0;
+  const bool dev = (enc & kHostBit) == 0;
+  const long long q = bad ? 0 : (long long)(enc & (kHostBit - 1));
+  const rsrc_t rp = make_rsrc((dev ? a.down.packed : a.host_down.packed) + q * a.down.blk_stride,
+                              bad ? 0 : a.st_dn_bytes);
+  const rsrc_t ra = make_rsrc((dev ? a.down.absmax : a.host_down.absmax) + q * a.down.abs_blk_stride,
+                              bad ? 0 : a.st_dn_abytes);
+  w = buf_ld16(rp, roff, 0);
+  am = buf_ldf(ra, aroff4, 0);
+}
+
+__global__ void __launch_bounds__(kThreads8, 2) k_down_rep(DecodeArgs a) {
+  extern __shared__ __attribute__((aligned(16))) uint32_t lds[];
+  uint32_t* actp = lds + kLutWords;                                    // [512][16] fp16 pairs
+  float* ascale = reinterpret_cast<float*>(actp + kMaxDnBlocks * 16);  // [512]
+  float* wsum = ascale + kMaxDnBlocks;                                 // [8][64]
+  const int tid = threadIdx.x, lane = tid & (kWave - 1);
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int GX = a.st_dn_gx, per = a.st_dn_per;
+  const int gx = (int)blockIdx.x % GX, c = (int)blockIdx.x / GX;
+  const int nbw_all = (a.k + GX - 1) / GX;
+  const int jb0 = gx * nbw_all;
+  const int nbw = max(0, min(a.k - jb0, nbw_all));  // blocks of this workgroup
+  const int jw0 = wave * per;                       // this wave's blocks (workgroup-local)
+  const int nbv = max(0, min(nbw - jw0, per));
+  const int T = (nbv + 1) >> 1;  // 2-block items (uniform per wave)
+  const uint32_t o = (uint32_t)(c * kWave + lane);
+  const uint32_t roff = o * (uint32_t)a.down.row_stride;
+  const uint32_t aroff4 = o * (uint32_t)a.down.abs_row_stride * 4u;
+
+  // Independent loads first: code book, block references, and (thread t <
+  // nbw) the 32 activations of the workgroup's block t.  They are
+  // unconditional loads from clamped, valid indices: a load under a branch
+  // would be waited for on its own.
+  const uint32_t* encs = a.st_enc + jb0;
+  uint32_t enc_v = encs[lane < nbv ? jw0 + lane : 0];
+  sched_fence();
+  LutCodes codes;
+  lut_codes_load(a.code_down, a.code_down, tid, codes);
+  const bool own = tid < nbw;
+  uint32_t my_enc = encs[own ? tid : 0];
+  if (!own) my_enc = kBad;
+  float4 av[8];
+  {
+    const float4* ap = reinterpret_cast<const float4*>(a.st_act + (long long)(jb0 + (own ? tid : 0)) * 32);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) av[i] = ap[i];
+  }
+  sched_fence();
+  if (lane >= nbv) enc_v = kBad;
+  DnStage st[kDnStages];
+#pragma unroll
+  for (int i = 0; i < kDnStages; ++i) {
+    const bool in = i < T;
+    dn_issue(a, in ? lane_value(enc_v, 2 * i) : kBad, roff, aroff4, st[i].w[0], st[i].am[0]);
+    dn_issue(a, in ? lane_value(enc_v, 2 * i + 1) : kBad, roff, aroff4, st[i].w[1], st[i].am[1]);
+  }
+  sched_fence();
+
+  lut_store(lds, codes, tid);
+  // block tid's activations as fp16 pairs scaled by a power of two (max |act|
+  // in [0.5, 1)); invalid blocks and blocks past the group's end are zero
+  {
+    const bool live = !(my_enc & kBad);
+    float mx = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+      mx = fmaxf(mx, fmaxf(fmaxf(fabsf(av[i].x), fabsf(av[i].y)), fmaxf(fabsf(av[i].z), fabsf(av[i].w))));
+    int ex = 0;
+    if (live && mx > 0.0f) frexpf(mx, &ex);
+    uint32_t hp[16];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const float f[4] = {av[i].x, av[i].y, av[i].z, av[i].w};
+      uint32_t h[4];
+#pragma unroll
+      for (int m = 0; m < 4; ++m) h[m] = live ? f2h(ldexpf(f[m], -ex)) : 0u;
+      hp[2 * i] = h[0] | (h[1] << 16);
+      hp[2 * i + 1] = h[2] | (h[3] << 16);
+    }
+    uint4* dst = reinterpret_cast<uint4*>(actp + tid * 16);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) dst[i] = make_uint4(hp[4 * i], hp[4 * i + 1], hp[4 * i + 2], hp[4 * i + 3]);
+    ascale[tid] = ldexpf(1.0f, ex);
+  }
+  lds_barrier();
+
+  uint32_t ad[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) ad[i] = (uint32_t)lane * 4u;
+  const uint32_t* wact = actp + jw0 * 16;
+  const float* wscale = ascale + jw0;
+  float acc = 0.0f;
+  for (int t0 = 0; t0 < T; t0 += kDnStages) {
+#pragma unroll
+    for (int i = 0; i < kDnStages; ++i) {
+      const int t = t0 + i;
+      if (t < T) {
+        const int jj = 2 * t;
+        acc += rep_dot32(st[i].w[0], wact + jj * 16, ad) * (st[i].am[0] * wscale[jj]);
+        acc += rep_dot32(st[i].w[1], wact + jj * 16 + 16, ad) * (st[i].am[1] * wscale[jj + 1]);
+      }
+      const int tn = t + kDnStages;
+      const bool in = tn < T;
+      dn_issue(a, in ? lane_value(enc_v, in ? 2 * tn : 0) : kBad, roff, aroff4, st[i].w[0], st[i].am[0]);
+      dn_issue(a, in ? lane_value(enc_v, in ? 2 * tn + 1 : 0) : kBad, roff, aroff4, st[i].w[1], st[i].am[1]);
+    }
+  }
+  // wave sums added in wave (block) order
+  wsum[wave * kWave + lane] = acc;
+  lds_barrier();
+  if (wave == 0) {
+    float y = 0.0f;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) y += wsum[w * kWave + lane];
+    if (GX == 1) {
+      if (a.out_f32 != nullptr) a.out_f32[o] = y;
+      if (a.down_bias != nullptr) y += h2f(a.down_bias[o]);
+      a.out[o] = f2h(y);
+    } else {
+      a.outpart[(long long)gx * a.H + o] = y;
+    }
+  }
+}
+
+__global__ void __launch_bounds__(256) k_fin_rep(DecodeArgs a) {
+  const int o = (int)blockIdx.x * 256 + (int)threadIdx.x;
+  if (o >= a.H) return;
+  const int G = a.st_dn_gx;
+  const float* p = a.outpart + o;
+  float y = 0.0f;
+  int g = 0;
+  for (; g + 8 <= G; g += 8) {
+    float v[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) v[i] = p[(long long)(g + i) * a.H];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) y += v[i];
+  }
+  for (; g < G; ++g) y += p[(long long)g * a.H];
+  if (a.out_f32 != nullptr) a.out_f32[o] = y;
+  if (a.down_bias != nullptr) y += h2f(a.down_bias[o]);
+  a.out[o] = f2h(y);
+}
+
+int env_or(const char* name, int dflt) {
+  const char* v = getenv(name);
+  return (v != nullptr && *v != 0) ? atoi(v) : dflt;
+}
+
+std::once_flag g_attr_once;
+
+template <typename K>
+void set_lds_limit(K kernel, size_t bytes) {
+  (void)hipFuncSetAttribute(reinterpret_cast<const void*>(kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
+                            (int)bytes);
+}
+
+}  // namespace
+
+int device_cus() {
+  static int cached[64] = {0};
+  int dev = 0;
+  (void)hipGetDevice(&dev);
+  if (dev < 0 || dev >= 64) dev = 0;
+  if (cached[dev] == 0) {
+    hipDeviceProp_t prop;
+    cached[dev] = hipGetDeviceProperties(&prop, dev) == hipSuccess ? prop.multiProcessorCount : 256;
+  }
+  return cached[dev];
+}
+
+bool plan_streaming(DecodeArgs& a, int cus) {
+  a.st_gu_wgs = 0;
+  if (a.H % kSplit != 0 || a.H / kSplit > kWaves || cus <= 0) return false;
+  if (a.n_slots >= (1 << 30)) return false;
+  // one set of strides for HBM slots and host copies; 32-bit extents
+  if (a.gate.row_stride != a.up.row_stride || a.gate.abs_row_stride != a.up.abs_row_stride) return false;
+  if (a.host_gate.packed != nullptr &&
+      (a.host_gate.row_stride != a.gate.row_stride || a.host_up.row_stride != a.gate.row_stride ||
+       a.host_gate.abs_row_stride != a.gate.abs_row_stride || a.host_up.abs_row_stride != a.gate.abs_row_stride ||
+       a.host_down.row_stride != a.down.row_stride || a.host_down.abs_row_stride != a.down.abs_row_stride))
+    return false;
+  const long long gu_bytes = 31 * a.gate.row_stride + a.H / 2;
+  const long long gu_abytes = (31 * a.gate.abs_row_stride + a.H / a.qbs) * 4;
+  const long long dn_bytes = (long long)(a.H - 1) * a.down.row_stride + 16;
+  const long long dn_abytes = ((long long)(a.H - 1) * a.down.abs_row_stride + 1) * 4;
+  const long long lim = 1LL << 31;
+  if (gu_bytes >= lim || gu_abytes >= lim || dn_bytes >= lim || dn_abytes >= lim) return false;
+  const int S = a.H / kSplit;
+  const int NS = kWaves / S;
+  // gate/up: rounds of NS items per workgroup, balanced over the workgroups
+  const long long items = 16LL * a.k;
+  const int gu_per_cu = env_or("NSMLP_GU_WGS_PER_CU", 1) > 1 ? 2 : 1;
+  const long long per_round = (long long)cus * gu_per_cu * NS;
+  const long long R = (items + per_round - 1) / per_round;
+  if (R > kMaxItems) return false;
+  const long long nwg = (items + R * NS - 1) / (R * NS);
+  // down: 64-row chunks x GX block groups, at least one workgroup per CU
+  const long long chunks = a.H / kWave;
+  long long GX = (cus + chunks - 1) / chunks;
+  const long long forced = env_or("NSMLP_DOWN_GX", 0);
+  if (forced > 0) GX = forced;
+  if (GX > a.k) GX = a.k;
+  if (GX > 64) GX = 64;
+  const long long nbw = (a.k + GX - 1) / GX;
+  if (nbw > kMaxDnBlocks) return false;
+  GX = (a.k + nbw - 1) / nbw;
+  const long long per = (nbw + kWaves - 1) / kWaves;
+  a.cs = kSplit;
+  a.splits = S;
+  a.st_gu_rounds = (int)R;
+  a.st_gu_wgs = (int)nwg;
+  a.st_dn_gx = (int)GX;
+  a.st_dn_per = (int)per;
+  a.st_gu_bytes = (int)gu_bytes;
+  a.st_gu_abytes = (int)gu_abytes;
+  a.st_dn_bytes = (int)dn_bytes;
+  a.st_dn_abytes = (int)dn_abytes;
+  return true;
+}
+
+void launch_decode_streaming(const DecodeArgs& a, hipStream_t s) {
+  std::call_once(g_attr_once, [] {
+    set_lds_limit(k_gu_rep<false>, kGuLds);
+    set_lds_limit(k_gu_rep<true>, kGuLds);
+    set_lds_limit(k_down_rep, kDnLds);
+  });
+  const bool affine = a.gate_bias != nullptr || a.up_bias != nullptr || a.mask != nullptr;
+  if (affine)
+    hipLaunchKernelGGL(k_gu_rep<true>, dim3(a.st_gu_wgs), dim3(kThreads8), kGuLds, s, a);
+  else
+    hipLaunchKernelGGL(k_gu_rep<false>, dim3(a.st_gu_wgs), dim3(kThreads8), kGuLds, s, a);
+  hipLaunchKernelGGL(k_down_rep, dim3((a.H / kWave) * a.st_dn_gx), dim3(kThreads8), kDnLds, s, a);
+  if (a.st_dn_gx > 1) hipLaunchKernelGGL(k_fin_rep, dim3(a.H / 256), dim3(256), 0, s, a);
+}
+
+}  // namespace nsmlp
