@@ -11,12 +11,18 @@ Reported (one JSON line):
   value         decode_tok_s = 1e6 / (126 * us_per_layer), MLP-only (router +
                 sparse MLP per layer, 126 layers per token)
   ms_per_step   wall time per layer (router + MLP), inputs resident in HBM
-  roofline      the sparse-MLP decode kernels (gate/up + down) timed with HIP
-                events on the launch stream: algorithmic bytes per launch
-                (selected packed NF4 + fp32 absmax + x + out) / duration
+  roofline      the sparse-MLP decode launch pair (k_gu_rep + k_down_rep),
+                timed with HIP events on its launch stream: algorithmic bytes
+                per launch (selected packed NF4 + fp32 absmax + x + out) /
+                duration.  traffic: HBM bytes per launch from the rocprofv3
+                FETCH_SIZE / WRITE_SIZE summary committed for this workload,
+                scaled by the same counters on a plain copy (null without it)
   cpu_baseline  the oracle's restatement of the reference PyTorch path
                 (router + dequant fallback with fp16 rounding points) on the
                 host cores, on the same layer shape
+
+--copy-calibration BYTES runs only a plain device copy of BYTES (the
+reference kernel for the counter calibration) and prints its size.
 """
 from __future__ import annotations
 
@@ -40,6 +46,7 @@ WORKLOADS = {
     1: "8B-shaped MLP layer decode: hidden 4096, intermediate 14336, block 32 (448 blocks), top-k 64",
     2: "405B-shaped MLP layer decode: hidden 16384, intermediate 53248, block 32 (1664 blocks), top-k 208",
 }
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic_sparse_mlp_decode.json")
 
 
 def algorithmic_bytes(H: int, k: int, qbs: int) -> int:
@@ -71,6 +78,20 @@ def cpu_model() -> str:
     except OSError:
         pass
     return "unknown"
+
+
+def measured_traffic(config: int):
+    """HBM bytes per sparse-MLP launch pair from the committed counter
+    summary, or None when there is none for this workload."""
+    try:
+        with open(TRAFFIC_FILE) as f:
+            t = json.load(f)
+    except (OSError, ValueError):
+        return None
+    entry = t.get("configs", {}).get(str(config))
+    if not entry:
+        return None
+    return int(entry["fetch_bytes"] + entry["write_bytes"])
 
 
 def cpu_baseline(layer, sel, runs: int, H: int, I: int, k: int, qbs: int) -> dict:
@@ -123,6 +144,20 @@ def cpu_baseline(layer, sel, runs: int, H: int, I: int, k: int, qbs: int) -> dic
     }
 
 
+def copy_calibration(nbytes: int) -> int:
+    import torch
+
+    dev = torch.device("cuda", 0)
+    a = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+    b = torch.empty_like(a)
+    a.fill_(1)
+    torch.cuda.synchronize()
+    b.copy_(a)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_bytes": nbytes, "read_bytes": nbytes, "write_bytes": nbytes}), flush=True)
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -132,14 +167,19 @@ def main() -> int:
     ap.add_argument("--layers", type=int, default=8, help="distinct layers rotated over the steps")
     ap.add_argument("--cpu-runs", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="BYTES")
     args = ap.parse_args()
     if args.gpus != 1:
-        print(f"bench.py runs on one GPU only; --gpus {args.gpus} is not supported (this path has no "
-              "multi-GPU mode: see the sharding note in DESIGN.md)", file=sys.stderr)
+        print(f"bench.py runs on one GPU only; --gpus {args.gpus} is not supported: this decode path has no "
+              "multi-GPU mode (one GPU holds a whole layer's slot table)", file=sys.stderr)
         return 2
+    if args.copy_calibration > 0:
+        return copy_calibration(args.copy_calibration)
 
     import torch
 
+    from next_step_ai_amd._runtime import workspace
+    from next_step_ai_amd.slot_table import SparseMlpLayer
     from next_step_ai_amd.synth import make_synthetic_layer
 
     device = torch.device("cuda", 0)
@@ -151,8 +191,6 @@ def main() -> int:
     for l in range(args.layers):
         L = make_synthetic_layer(H=H, I=I, R=R, seed=1000 * args.config + l, device=device)
         L.table = L.slot_table(drop_reference_down=True)
-        from next_step_ai_amd.slot_table import SparseMlpLayer
-
         L.mlp = SparseMlpLayer(L.router(), L.table, k)
         layers.append(L)
     torch.cuda.synchronize()
@@ -161,9 +199,6 @@ def main() -> int:
 
     outs = [torch.empty(H, dtype=torch.float16, device=device) for _ in layers]
     sels = [torch.empty(k, dtype=torch.int32, device=device) for _ in layers]
-    ws = None
-    from next_step_ai_amd._runtime import workspace
-
     ws = workspace(layers[0].mlp.workspace_bytes(), device)
     n = len(layers)
     for i in range(args.warmup):
@@ -179,7 +214,8 @@ def main() -> int:
     us_per_layer = (t1 - t0) / args.steps * 1e6
     print(f"[bench] {args.steps} steps: {us_per_layer:.2f} us/layer (router + MLP)", file=sys.stderr, flush=True)
 
-    # Sparse-MLP kernels alone, timed with HIP events on the launch stream.
+    # Sparse-MLP decode launch pair alone, HIP events on its launch stream
+    # (torch's current stream, the one the C ABI is given).
     for j in range(n):
         layers[j].table.decode(layers[j].x, sels[j], out=outs[j])
     torch.cuda.synchronize()
@@ -190,23 +226,8 @@ def main() -> int:
         layers[j].table.decode(layers[j].x, sels[j], out=outs[j])
         ev[i][1].record()
     torch.cuda.synchronize()
-    mlp_ms = [a.elapsed_time(b) for a, b in ev]
-    mlp_us = statistics.mean(mlp_ms) * 1e3
-    # Router alone (route kernels), same method.
-    from next_step_ai_amd.router import route_tokens
-
-    rdicts = [L.routing_dict(k) for L in layers]
-    for j in range(n):
-        route_tokens(layers[j].x.reshape(1, H), rdicts[j], k, sorted_by_score=False)
-    torch.cuda.synchronize()
-    rev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(args.steps)]
-    for i in range(args.steps):
-        j = i % n
-        rev[i][0].record()
-        route_tokens(layers[j].x.reshape(1, H), rdicts[j], k, sorted_by_score=False)
-        rev[i][1].record()
-    torch.cuda.synchronize()
-    route_us = statistics.mean(a.elapsed_time(b) for a, b in rev) * 1e3
+    mlp_us = statistics.mean(a.elapsed_time(b) for a, b in ev) * 1e3
+    route_us = max(0.0, us_per_layer - mlp_us)
 
     abytes = algorithmic_bytes(H, k, qbs)
     achieved = abytes / (mlp_us * 1e-6) / 1e9
@@ -221,7 +242,7 @@ def main() -> int:
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "f32",
+        "dtype": "nf4(u8)*f16->f32",
         "data": "synthetic",
         "config": {
             "workload": WORKLOADS[args.config] + f"; NF4 qbs {qbs} with fp32 absmax; all blocks HBM-resident; "
@@ -241,8 +262,8 @@ def main() -> int:
             "peak": PEAK_GBS,
             "unit": "GB/s",
             "frac": round(achieved / PEAK_GBS, 4),
-            "traffic": None,
-            "kernels": "k_gate_up + k_down (one sparse-MLP decode launch pair)",
+            "traffic": measured_traffic(args.config),
+            "kernels": "k_gu_rep + k_down_rep (the sparse-MLP decode launch pair)",
         },
     }
     if not args.no_cpu_baseline:

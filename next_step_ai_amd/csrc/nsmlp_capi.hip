@@ -27,7 +27,6 @@ constexpr int kMaxRowChunks = 1024;
 constexpr size_t kCounterBytes = kRowCountOff + (size_t)kMaxRowChunks * sizeof(int) + 256;
 
 constexpr int kRowsPerChunk = 256;
-constexpr int kLatCols = 2048;
 constexpr int kMaxGroups = 64;
 
 size_t align_up(size_t v) { return (v + kAlign - 1) / kAlign * kAlign; }
@@ -109,15 +108,14 @@ DecodeWs decode_ws_layout(int H, int k) {
 }
 
 struct RouteWs {
-  size_t lat_part, scores, total;
+  size_t lat16, scores, total;
 };
 
 RouteWs route_ws_layout(size_t base, int rows, int H, int R, int NB) {
   RouteWs w;
-  int splits = (H + kLatCols - 1) / kLatCols;
   size_t off = align_up(base);
-  w.lat_part = off;
-  off += align_up((size_t)rows * R * splits * 3 * sizeof(double));
+  w.lat16 = off;
+  off += align_up((size_t)rows * R * sizeof(uint16_t));
   w.scores = off;
   off += align_up((size_t)rows * NB * sizeof(uint16_t));
   w.total = off;
@@ -227,13 +225,11 @@ int fill_route(RouteArgs& r, const void* x, int rows, int H, const void* enc_w, 
   r.legacy_abs = (flags & NSMLP_ROUTE_LEGACY_ABS) ? 1 : 0;
   r.sorted = (flags & NSMLP_ROUTE_SORTED) ? 1 : 0;
   r.k = k;
-  r.lat_cols = kLatCols;
-  r.lat_splits = (H + kLatCols - 1) / kLatCols;
   r.vec = (H % 8 == 0) && aligned16(x) && aligned16(enc_w);
   r.sel = sel;
   r.latent_out = (uint16_t*)latent_out;
   r.scores_out = (uint16_t*)scores_out;
-  r.lat_part = (double*)(base + L.lat_part);
+  r.lat16 = (uint16_t*)(base + L.lat16);
   r.scores = (uint16_t*)(base + L.scores);
   r.status = (int*)(base + kStatusOff);
   return NSMLP_OK;

@@ -430,14 +430,12 @@ struct RouteArgs {
   const uint16_t* score_b; // [NB] or nullptr
   const uint16_t* dbn;     // [NB] fp16 or nullptr
   int NB, legacy_abs, sorted, k;
-  int lat_splits;          // H / lat_cols
-  int lat_cols;            // columns per latent workgroup
   int vec;                 // 16-byte loads allowed for x / enc_w
   int32_t* sel;            // [rows][k]
   uint16_t* latent_out;    // [rows][R] or nullptr
   uint16_t* scores_out;    // [rows][NB] or nullptr
   // workspace
-  double* lat_part;        // [rows][R][lat_splits][3]
+  uint16_t* lat16;         // [rows][R] fp16 latent
   uint16_t* scores;        // [rows][NB]
   int* status;
 };

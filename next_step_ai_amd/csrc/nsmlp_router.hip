@@ -1,59 +1,54 @@
 // Learned-basis router of the blockwise-sparse MLP (the reference's
 // _compute_sparse_basis_latent + _route_sparse_mlp, RT:4209-4238 and
 // RT:4311-4352), as three gfx950 kernels:
-//   1. latent partials : exact fp16 dot products of x with enc_w, split over
-//                        many workgroups (the 2 MiB enc_w read is spread
-//                        over the chip), accumulated with Exact3.
-//   2. scores          : exact merge of the partials -> fp16 latent (+ the
-//                        basis_top_k mask) -> exact score dots -> fp16,
-//                        clamp, optional down_block_norm scaling.
-//   3. select          : one workgroup per token; radix select of the k-th
-//                        largest 32-bit key (fp16 order key << 16 | ~index),
-//                        so ties resolve to the lowest block index, then an
-//                        ordered compaction (ascending block ids) or a rank
-//                        sort (score desc, index asc).
+//   1. latent          : one workgroup per latent row: exact fp16 dot product
+//                        of x with the enc_w row (Exact3), one fp16 rounding.
+//   2. scores          : fp16 latent (+ the basis_top_k mask) -> exact score
+//                        dots (8 lanes per block) -> fp16, clamp, optional
+//                        down_block_norm scaling.
+//   3. select          : one workgroup per token; two 8-bit histogram passes
+//                        find the k-th largest score T, then an ordered
+//                        compaction takes every score above T and the lowest
+//                        block ids among the scores equal to T (the order of
+//                        the unique key fp16 order key << 16 | ~index), in
+//                        ascending block order or, sorted, by rank.
 #include "nsmlp_internal.h"
 
 namespace nsmlp {
 
 namespace {
 
-constexpr int kLatThreads = 256;
+constexpr int kLatThreads = 1024;
 constexpr int kScoreThreads = 256;
 constexpr int kSelThreads = 1024;
 
+// One workgroup per (latent row, token): the exact dot product over the
+// whole hidden size, rounded once to fp16 (RT:4221-4222).
 template <bool kVec>
-__global__ void __launch_bounds__(kLatThreads) k_latent_partial(RouteArgs a) {
-  const int s = blockIdx.x;    // column split
-  const int r = blockIdx.y;    // latent row
-  const int row = blockIdx.z;  // token
+__global__ void __launch_bounds__(kLatThreads) k_latent(RouteArgs a) {
+  const int r = blockIdx.x;    // latent row
+  const int row = blockIdx.y;  // token
   const int tid = threadIdx.x;
   const uint16_t* __restrict__ x = a.x + (long long)row * a.H;
   const uint16_t* __restrict__ w = a.enc_w + (long long)r * a.H;
-  const int c0 = s * a.lat_cols + tid * 8;
   Exact3 acc = exact_zero();
   if (kVec) {
-    if (c0 < a.H) {
-      uint4 xv = *reinterpret_cast<const uint4*>(x + c0);
-      uint4 wv = *reinterpret_cast<const uint4*>(w + c0);
+#pragma unroll 8
+    for (int c0 = tid * 8; c0 < a.H; c0 += kLatThreads * 8) {
+      const uint4 xv = *reinterpret_cast<const uint4*>(x + c0);
+      const uint4 wv = *reinterpret_cast<const uint4*>(w + c0);
       const uint32_t xs[4] = {xv.x, xv.y, xv.z, xv.w};
       const uint32_t ws[4] = {wv.x, wv.y, wv.z, wv.w};
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
-        float p0 = h2f((uint16_t)(xs[q] & 0xFFFFu)) * h2f((uint16_t)(ws[q] & 0xFFFFu));
-        float p1 = h2f((uint16_t)(xs[q] >> 16)) * h2f((uint16_t)(ws[q] >> 16));
-        exact_add(acc, (double)p0);
-        exact_add(acc, (double)p1);
+        exact_add(acc, (double)(h2f((uint16_t)(xs[q] & 0xFFFFu)) * h2f((uint16_t)(ws[q] & 0xFFFFu))));
+        exact_add(acc, (double)(h2f((uint16_t)(xs[q] >> 16)) * h2f((uint16_t)(ws[q] >> 16))));
       }
     }
   } else {
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      int c = c0 + i;
-      if (c < a.H) exact_add(acc, (double)(h2f(x[c]) * h2f(w[c])));
-    }
+    for (int c = tid; c < a.H; c += kLatThreads) exact_add(acc, (double)(h2f(x[c]) * h2f(w[c])));
   }
-  if (s == 0 && tid == 0 && a.enc_b != nullptr) exact_add(acc, (double)h2f(a.enc_b[r]));
+  if (tid == 0 && a.enc_b != nullptr) exact_add(acc, (double)h2f(a.enc_b[r]));
   acc = wave_sum_exact(acc);
   __shared__ double red[kLatThreads / kWave][3];
   const int wave = tid / kWave, lane = tid % kWave;
@@ -66,24 +61,33 @@ __global__ void __launch_bounds__(kLatThreads) k_latent_partial(RouteArgs a) {
   if (tid == 0) {
     Exact3 t = exact_zero();
     for (int wv = 0; wv < kLatThreads / kWave; ++wv) exact_merge(t, Exact3{red[wv][0], red[wv][1], red[wv][2]});
-    double* dst = a.lat_part + (((long long)row * a.R + r) * a.lat_splits + s) * 3;
-    dst[0] = t.a0;
-    dst[1] = t.a1;
-    dst[2] = t.a2;
+    a.lat16[(long long)row * a.R + r] = exact_to_f16(t);
   }
 }
+
+// Scores: 8 lanes per block (kScoreLanes), each summing every 8th basis
+// term exactly; the lane partials are merged exactly (plain fp64 adds of
+// Exact3 parts) and rounded once.
+constexpr int kScoreLanes = 8;
+constexpr int kScoresPerWg = kScoreThreads / kScoreLanes;
 
 __global__ void __launch_bounds__(kScoreThreads) k_scores(RouteArgs a) {
   const int row = blockIdx.y;
   const int tid = threadIdx.x;
   extern __shared__ uint16_t lat16[];  // [R]
-  // Latent: exact merge of the split partials, one fp16 rounding (RT:4221-4222).
-  for (int r = tid; r < a.R; r += kScoreThreads) {
-    const double* src = a.lat_part + ((long long)row * a.R + r) * a.lat_splits * 3;
-    Exact3 e = exact_zero();
-    for (int s = 0; s < a.lat_splits; ++s) exact_merge(e, Exact3{src[3 * s], src[3 * s + 1], src[3 * s + 2]});
-    lat16[r] = exact_to_f16(e);
+  // score_w terms of this lane (loaded before waiting for the latent)
+  const int j = blockIdx.x * kScoresPerWg + tid / kScoreLanes;
+  const int part = tid % kScoreLanes;
+  const int jj = j < a.NB ? j : a.NB - 1;  // all lanes take part in the merge
+  const uint16_t* __restrict__ w = a.score_w + (long long)jj * a.R;
+  constexpr int kPre = 16;  // prefetched terms per lane (R <= 128)
+  uint16_t wv[kPre];
+#pragma unroll
+  for (int i = 0; i < kPre; ++i) {
+    const int r = part + i * kScoreLanes;
+    wv[i] = r < a.R ? w[r] : (uint16_t)0;
   }
+  for (int r = tid; r < a.R; r += kScoreThreads) lat16[r] = a.lat16[(long long)row * a.R + r];
   __syncthreads();
   // basis_top_k mask over |latent| (RT:4233-4238); ties keep the lower index.
   int btk = a.basis_top_k < 1 ? 1 : (a.basis_top_k > a.R ? a.R : a.basis_top_k);
@@ -106,25 +110,27 @@ __global__ void __launch_bounds__(kScoreThreads) k_scores(RouteArgs a) {
   }
   if (blockIdx.x == 0 && a.latent_out != nullptr)
     for (int r = tid; r < a.R; r += kScoreThreads) a.latent_out[(long long)row * a.R + r] = lat16[r];
-  const int j = blockIdx.x * kScoreThreads + tid;
-  if (j >= a.NB) return;
-  const uint16_t* __restrict__ w = a.score_w + (long long)j * a.R;
   Exact3 acc = exact_zero();
   const uint16_t amask = a.legacy_abs ? 0x7FFFu : 0xFFFFu;
-  for (int r = 0; r < a.R; ++r) {
-    float p = h2f((uint16_t)(lat16[r] & amask)) * h2f(w[r]);
+#pragma unroll
+  for (int i = 0; i < kPre; ++i) {
+    const int r = part + i * kScoreLanes;
+    if (r < a.R) exact_add(acc, (double)(h2f((uint16_t)(lat16[r] & amask)) * h2f(wv[i])));
+  }
+  for (int r = part + kPre * kScoreLanes; r < a.R; r += kScoreLanes) {
+    const float p = h2f((uint16_t)(lat16[r] & amask)) * h2f(w[r]);
     exact_add(acc, (double)p);
   }
+#pragma unroll
+  for (int m = 1; m < kScoreLanes; m <<= 1)
+    exact_merge(acc, Exact3{__shfl_xor(acc.a0, m, kWave), __shfl_xor(acc.a1, m, kWave), __shfl_xor(acc.a2, m, kWave)});
+  if (part != 0 || j >= a.NB) return;
   if (!a.legacy_abs && a.score_b != nullptr) exact_add(acc, (double)h2f(a.score_b[j]));
   uint16_t sc = exact_to_f16(acc);
   if (!a.legacy_abs && (sc & 0x8000u)) sc = 0;  // clamp_min(0) (RT:4331)
   if (a.dbn != nullptr) sc = f2h(h2f(sc) * h2f(a.dbn[j]));  // fp16 x fp16 is exact in fp32
   a.scores[(long long)row * a.NB + j] = sc;
   if (a.scores_out != nullptr) a.scores_out[(long long)row * a.NB + j] = sc;
-}
-
-__device__ __forceinline__ uint32_t sel_key(const uint16_t* sc, int i) {
-  return (f16_order_key(sc[i]) << 16) | (uint32_t)(0xFFFFu - (uint32_t)i);
 }
 
 __device__ __forceinline__ int wave_incl_scan(int v, int lane) {
@@ -136,6 +142,40 @@ __device__ __forceinline__ int wave_incl_scan(int v, int lane) {
   return v;
 }
 
+// Wave 0: the digit (from the top) holding the remaining-th largest entry of
+// hist; sets *digit and *above (count of entries in higher digits).
+__device__ __forceinline__ void find_digit(const unsigned* hist, unsigned remaining, int lane, unsigned* digit,
+                                           unsigned* above) {
+  unsigned c[4];
+  unsigned local = 0;
+#pragma unroll
+  for (int b = 0; b < 4; ++b) {
+    c[b] = hist[255 - 4 * lane - b];
+    local += c[b];
+  }
+  const unsigned incl = (unsigned)wave_incl_scan((int)local, lane);
+  const unsigned excl = incl - local;
+  if (excl < remaining && remaining <= incl) {
+    unsigned cum = excl;
+#pragma unroll
+    for (int b = 0; b < 4; ++b) {
+      if (cum + c[b] >= remaining) {
+        *digit = 255u - 4u * lane - b;
+        *above = cum;
+        break;
+      }
+      cum += c[b];
+    }
+  }
+}
+
+// Top-k of one token's scores (keys: fp16 order key, ties to the lower block
+// index).  Each thread holds KPT consecutive keys in registers.  Two 8-bit
+// histogram passes find the threshold score T and how many entries equal to
+// T are taken (`need`); an ordered compaction then takes every score above T
+// and the first `need` scores equal to T in block order.  Output: ascending
+// block ids, or (sorted) score descending with ties by ascending id.
+template <int KPT>
 __global__ void __launch_bounds__(kSelThreads) k_select(RouteArgs a) {
   const int row = blockIdx.x;
   const int tid = threadIdx.x;
@@ -146,54 +186,38 @@ __global__ void __launch_bounds__(kSelThreads) k_select(RouteArgs a) {
   __shared__ unsigned hist[256];
   __shared__ unsigned s_digit, s_above;
   __shared__ int wsum[kSelThreads / kWave];
-  uint32_t prefix = 0, mask = 0;
+  const int i0 = tid * KPT;
+  uint32_t key[KPT];
+#pragma unroll
+  for (int m = 0; m < KPT; ++m) key[m] = i0 + m < NB ? f16_order_key(sc[i0 + m]) : 0u;
+  uint32_t T = 0;
   unsigned remaining = (unsigned)k;
-  for (int pass = 0; pass < 4; ++pass) {
-    const int shift = 24 - 8 * pass;
+  for (int pass = 0; pass < 2; ++pass) {
     for (int i = tid; i < 256; i += kSelThreads) hist[i] = 0;
     __syncthreads();
-    for (int i = tid; i < NB; i += kSelThreads) {
-      uint32_t key = sel_key(sc, i);
-      if ((key & mask) == prefix) atomicAdd(&hist[(key >> shift) & 0xFFu], 1u);
+#pragma unroll
+    for (int m = 0; m < KPT; ++m) {
+      if (i0 + m >= NB) continue;
+      if (pass == 0)
+        atomicAdd(&hist[key[m] >> 8], 1u);
+      else if ((key[m] >> 8) == (T >> 8))
+        atomicAdd(&hist[key[m] & 0xFFu], 1u);
     }
     __syncthreads();
-    if (wave == 0) {
-      unsigned c[4];
-      unsigned local = 0;
-#pragma unroll
-      for (int b = 0; b < 4; ++b) {
-        c[b] = hist[255 - 4 * lane - b];
-        local += c[b];
-      }
-      unsigned incl = (unsigned)wave_incl_scan((int)local, lane);
-      unsigned excl = incl - local;
-      if (excl < remaining && remaining <= incl) {
-        unsigned cum = excl;
-#pragma unroll
-        for (int b = 0; b < 4; ++b) {
-          if (cum + c[b] >= remaining) {
-            s_digit = 255u - 4u * lane - b;
-            s_above = cum;
-            break;
-          }
-          cum += c[b];
-        }
-      }
-    }
+    if (wave == 0) find_digit(hist, remaining, lane, &s_digit, &s_above);
     __syncthreads();
-    prefix |= s_digit << shift;
-    mask |= 0xFFu << shift;
+    T |= s_digit << (pass == 0 ? 8 : 0);
     remaining -= s_above;
     __syncthreads();
   }
-  const uint32_t T = prefix;  // the k-th largest key (keys are unique)
-  // Ordered compaction: selected = keys >= T, ascending block index.
-  const int per = (NB + kSelThreads - 1) / kSelThreads;
-  const int i0 = tid * per;
-  const int i1 = min(NB, i0 + per);
+  const unsigned need = remaining;  // entries equal to T that are taken
+  // Ordered compaction: counts above T and equal to T, packed in one scanned
+  // word (each < 2^16).
   int cnt = 0;
-  for (int i = i0; i < i1; ++i) cnt += sel_key(sc, i) >= T;
-  int incl = wave_incl_scan(cnt, lane);
+#pragma unroll
+  for (int m = 0; m < KPT; ++m)
+    if (i0 + m < NB) cnt += key[m] > T ? (1 << 16) : (key[m] == T ? 1 : 0);
+  const int incl = wave_incl_scan(cnt, lane);
   if (lane == kWave - 1) wsum[wave] = incl;
   __syncthreads();
   if (wave == 0) {
@@ -202,21 +226,38 @@ __global__ void __launch_bounds__(kSelThreads) k_select(RouteArgs a) {
     if (lane < kSelThreads / kWave) wsum[lane] = vi - v;
   }
   __syncthreads();
-  int pos = wsum[wave] + incl - cnt;
+  const int before = wsum[wave] + incl - cnt;
+  unsigned gt = (unsigned)before >> 16, eq = (unsigned)before & 0xFFFFu;
   int32_t* out = a.sel + (long long)row * k;
-  if (!a.sorted) {
-    for (int i = i0; i < i1; ++i)
-      if (sel_key(sc, i) >= T && pos < k) out[pos++] = i;
-    return;
+  extern __shared__ uint32_t selkeys[];  // [k] (sorted output)
+#pragma unroll
+  for (int m = 0; m < KPT; ++m) {
+    const int i = i0 + m;
+    if (i >= NB) continue;
+    unsigned pos;
+    if (key[m] > T) {
+      pos = gt + (eq < need ? eq : need);
+      ++gt;
+    } else if (key[m] == T) {
+      if (eq >= need) {
+        ++eq;
+        continue;
+      }
+      pos = gt + eq;
+      ++eq;
+    } else {
+      continue;
+    }
+    if (pos >= (unsigned)k) continue;
+    if (!a.sorted)
+      out[pos] = i;
+    else
+      selkeys[pos] = (key[m] << 16) | (0xFFFFu - (uint32_t)i);
   }
-  extern __shared__ uint32_t selkeys[];  // [k]
-  for (int i = i0; i < i1; ++i) {
-    uint32_t key = sel_key(sc, i);
-    if (key >= T && pos < k) selkeys[pos++] = key;
-  }
+  if (!a.sorted) return;
   __syncthreads();
   for (int t = tid; t < k; t += kSelThreads) {
-    uint32_t kt = selkeys[t];
+    const uint32_t kt = selkeys[t];
     int rank = 0;
     for (int q = 0; q < k; ++q) rank += selkeys[q] > kt;
     if (rank < k) out[rank] = (int32_t)(0xFFFFu - (kt & 0xFFFFu));
@@ -226,15 +267,22 @@ __global__ void __launch_bounds__(kSelThreads) k_select(RouteArgs a) {
 }  // namespace
 
 void launch_route(const RouteArgs& a, hipStream_t s) {
-  dim3 g1(a.lat_splits, a.R, a.rows);
+  dim3 g1(a.R, a.rows);
   if (a.vec)
-    hipLaunchKernelGGL(k_latent_partial<true>, g1, dim3(kLatThreads), 0, s, a);
+    hipLaunchKernelGGL(k_latent<true>, g1, dim3(kLatThreads), 0, s, a);
   else
-    hipLaunchKernelGGL(k_latent_partial<false>, g1, dim3(kLatThreads), 0, s, a);
-  dim3 g2((a.NB + kScoreThreads - 1) / kScoreThreads, a.rows);
+    hipLaunchKernelGGL(k_latent<false>, g1, dim3(kLatThreads), 0, s, a);
+  dim3 g2((a.NB + kScoresPerWg - 1) / kScoresPerWg, a.rows);
   hipLaunchKernelGGL(k_scores, g2, dim3(kScoreThreads), (size_t)a.R * sizeof(uint16_t), s, a);
-  size_t lds = a.sorted ? (size_t)a.k * sizeof(uint32_t) : 0;
-  hipLaunchKernelGGL(k_select, dim3(a.rows), dim3(kSelThreads), lds, s, a);
+  const size_t lds = a.sorted ? (size_t)a.k * sizeof(uint32_t) : 0;
+  const int kpt = (a.NB + kSelThreads - 1) / kSelThreads;  // NB <= 65535: kpt <= 64
+  const dim3 g3(a.rows), b3(kSelThreads);
+  if (kpt <= 2)
+    hipLaunchKernelGGL(k_select<2>, g3, b3, lds, s, a);
+  else if (kpt <= 8)
+    hipLaunchKernelGGL(k_select<8>, g3, b3, lds, s, a);
+  else
+    hipLaunchKernelGGL(k_select<64>, g3, b3, lds, s, a);
 }
 
 }  // namespace nsmlp
