@@ -1,0 +1,98 @@
+"""The oracle and the package's host-side slot-table logic against the
+expectations the reference's own tests assert (tests/golden fixture)."""
+import json
+import os
+
+import numpy as np
+import torch
+
+FIX = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "reference_test_expectations.json")
+
+
+def _fix():
+    with open(FIX) as f:
+        return json.load(f)
+
+
+def _check_plan(case, slots, ids, scores, active):
+    assert int(active) == case["expected_active_count"]
+    assert [int(v) for v in slots] == case["expected_slots"]
+    assert [int(v) for v in ids] == case["expected_block_ids"]
+    for i, lo in case["expected_scores_above"].items():
+        assert float(scores[int(i)]) > lo
+
+
+def test_fixed_capacity_plan_oracle(orc):
+    c = _fix()["plan_fixed_capacity_bank_update"]
+    _check_plan(c, *orc.plan_fixed_capacity_bank_update(c["existing_block_ids"], c["existing_scores"],
+                                                        c["active_count"], c["capacity"], c["novel_blocks"]))
+
+
+def test_fixed_capacity_plan_package():
+    from next_step_ai_amd.slot_table import plan_fixed_capacity_bank_update
+
+    c = _fix()["plan_fixed_capacity_bank_update"]
+    slots, ids, scores, active = plan_fixed_capacity_bank_update(
+        existing_block_ids_cpu=torch.tensor(c["existing_block_ids"], dtype=torch.long),
+        existing_scores_cpu=torch.tensor(c["existing_scores"], dtype=torch.float32),
+        active_count=c["active_count"], capacity=c["capacity"],
+        novel_blocks_cpu=torch.tensor(c["novel_blocks"], dtype=torch.long))
+    _check_plan(c, slots.tolist(), ids.tolist(), scores, active)
+
+
+def test_down_column_gather_oracle(orc):
+    c = _fix()["down_column_gather"]
+    p, a = orc.gather_down_columns(np.array(c["packed"], dtype=np.uint8), np.array(c["absmax"], dtype=np.float32),
+                                   c["blocks"], c["h_out"], c["in_features"], c["qbs"], block_size=c["block_size"])
+    assert p.shape == (c["h_out"], len(c["blocks"]), c["block_size"] // 2) and p.dtype == np.uint8
+    assert a.shape == (c["h_out"], len(c["blocks"])) and a.dtype == np.float32
+    assert p.tolist() == c["expected_packed"]
+    assert a.tolist() == c["expected_absmax"]
+
+
+def test_hot_cold_partition_package():
+    from next_step_ai_amd.slot_table import partition_cached_block_lookup
+
+    for case in _fix()["hot_cold_partition"]["cases"]:
+        lookup = torch.full((case["total_blocks"],), -1, dtype=torch.int32)
+        hot = torch.tensor(case["hot_blocks"], dtype=torch.long)
+        if hot.numel():
+            lookup[hot] = torch.arange(hot.numel(), dtype=torch.int32)
+        routing = torch.tensor(case["routing"], dtype=torch.long)
+        pos, slots, cold, cold_mask = partition_cached_block_lookup(lookup.index_select(0, routing),
+                                                                    ordered_blocks=routing)
+        assert cold.tolist() == case["expected_cold"]
+        n_hot = len(case["routing"]) - len(case["expected_cold"])
+        assert (0 if pos is None else int(pos.numel())) == n_hot
+        if slots is not None:
+            assert all(int(lookup[routing[int(p)]]) == int(s) for p, s in zip(pos, slots))
+
+
+def test_active_layout_oracle_and_package(orc):
+    """Ordered blocks are the ascending unique in-range ids (CPU unique,
+    RT:4873); active_local inverts them; each flat_mask row has 32 ones per
+    own valid block (RT:4883-4901); neurons are the blocks' 32-row ranges."""
+    from next_step_ai_amd.layout import build_sparse_active_layout
+
+    rng = np.random.default_rng(7)
+    for rows, k, nb in [(1, 9, 40), (3, 6, 20), (4, 5, 12)]:
+        ab = rng.integers(-2, nb + 3, size=(rows, k))
+        ordered, local, mask, neurons = orc.active_layout(ab, nb)
+        valid = ab[(ab >= 0) & (ab < nb)]
+        assert ordered.tolist() == sorted(set(valid.tolist()))
+        for t in range(rows):
+            for i in range(k):
+                b = ab[t, i]
+                if 0 <= b < nb:
+                    assert ordered[local[t, i]] == b
+                else:
+                    assert local[t, i] == -1
+            own = set(ab[t][(ab[t] >= 0) & (ab[t] < nb)].tolist())
+            assert mask[t].sum() == 32 * len(own)
+        assert neurons.tolist() == [32 * b + r for b in ordered.tolist() for r in range(32)]
+        po, pl, pm, _ = build_sparse_active_layout(active_blocks=torch.from_numpy(ab), rows=rows, block_size=32,
+                                                   max_valid_blocks=nb, dtype=torch.float32,
+                                                   device=torch.device("cpu"))
+        assert po.tolist() == ordered.tolist()
+        assert pl.numpy().tolist() == local.tolist()
+        assert np.array_equal(pm.numpy(), mask)
