@@ -46,8 +46,8 @@ namespace {
 constexpr int kSplit = 2048;               // columns per split
 constexpr int kWaves = 8;                  // waves per workgroup
 constexpr int kThreads8 = kWaves * kWave;  // 512
-constexpr int kGuStages = 4;
-constexpr int kDnStages = 6;
+constexpr int kGuStages = 2;
+constexpr int kDnStages = 2;
 constexpr int kMaxItems = 64;      // items per wave resolved up front (one per lane)
 constexpr int kMaxDnBlocks = 512;  // blocks per down workgroup (activations in LDS)
 constexpr int kLutWords = kRepLutBytes / 4;
