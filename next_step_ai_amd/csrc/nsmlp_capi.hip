@@ -385,6 +385,16 @@ int nsmlp_decode_layer_f16(const nsmlp_router* router, const nsmlp_slot_table* t
              router->score_b, router->down_block_norm, router->NB, router->flags & NSMLP_ROUTE_LEGACY_ABS, k, sel,
              nullptr, nullptr, (char*)ws, dtotal);
   hipStream_t s = (hipStream_t)stream;
+  if (a.st_gu_wgs > 0 && streaming_can_select(a.NB, k)) {
+    // the streaming gate/up kernel selects the blocks itself from the scores
+    launch_route_scores(r, s);
+    rc = check_launch("route");
+    if (rc) return rc;
+    a.sel = nullptr;
+    a.sel_scores = r.scores;
+    a.sel_out = sel_out;
+    return run_decode(a, s);
+  }
   launch_route(r, s);
   rc = check_launch("route");
   if (rc) return rc;

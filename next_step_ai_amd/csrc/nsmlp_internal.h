@@ -325,6 +325,112 @@ __device__ __forceinline__ void st_coherent_i32(int* p, int v) {
 
 __device__ __forceinline__ float silu_mul(float g, float u) { return g / (1.0f + __expf(-g)) * u; }
 
+// ------------------------------------------------------------------ top-k --
+// Workgroup top-k of NB fp16 scores.  Keys are fp16 order keys; among equal
+// scores the lower block index ranks higher (the order of the unique key
+// order16 << 16 | ~index).  Each of NTHR threads holds KPT consecutive keys
+// (thread t: indices t*KPT ..).  Two 8-bit histogram passes find the k-th
+// largest score T and how many entries equal to T are taken (`need`); the
+// scan gives each thread the counts above T (gt) and equal to T (eq) before
+// its range, so an ordered compaction can place every selected index.
+struct TopkLds {
+  unsigned hist[256];
+  int wsum[16];
+  unsigned digit, above;
+};
+
+__device__ __forceinline__ int wave_incl_scan(int v, int lane) {
+#pragma unroll
+  for (int d = 1; d < kWave; d <<= 1) {
+    int o = __shfl_up(v, d, kWave);
+    if (lane >= d) v += o;
+  }
+  return v;
+}
+
+// Wave 0: the digit (from the top) holding the remaining-th largest entry.
+__device__ __forceinline__ void topk_find_digit(TopkLds& L, unsigned remaining, int lane) {
+  unsigned c[4];
+  unsigned local = 0;
+#pragma unroll
+  for (int b = 0; b < 4; ++b) {
+    c[b] = L.hist[255 - 4 * lane - b];
+    local += c[b];
+  }
+  const unsigned incl = (unsigned)wave_incl_scan((int)local, lane);
+  const unsigned excl = incl - local;
+  if (excl < remaining && remaining <= incl) {
+    unsigned cum = excl;
+#pragma unroll
+    for (int b = 0; b < 4; ++b) {
+      if (cum + c[b] >= remaining) {
+        L.digit = 255u - 4u * lane - b;
+        L.above = cum;
+        break;
+      }
+      cum += c[b];
+    }
+  }
+}
+
+template <int NTHR, int KPT>
+__device__ __forceinline__ void topk_threshold(const uint32_t (&key)[KPT], int i0, int NB, int k, TopkLds& L,
+                                               uint32_t& T, unsigned& need, unsigned& gt, unsigned& eq) {
+  const int tid = threadIdx.x, lane = tid % kWave, wave = tid / kWave;
+  T = 0;
+  unsigned remaining = (unsigned)k;
+  for (int pass = 0; pass < 2; ++pass) {
+    for (int i = tid; i < 256; i += NTHR) L.hist[i] = 0;
+    __syncthreads();
+#pragma unroll
+    for (int m = 0; m < KPT; ++m) {
+      if (i0 + m >= NB) continue;
+      if (pass == 0)
+        atomicAdd(&L.hist[key[m] >> 8], 1u);
+      else if ((key[m] >> 8) == (T >> 8))
+        atomicAdd(&L.hist[key[m] & 0xFFu], 1u);
+    }
+    __syncthreads();
+    if (wave == 0) topk_find_digit(L, remaining, lane);
+    __syncthreads();
+    T |= L.digit << (pass == 0 ? 8 : 0);
+    remaining -= L.above;
+    __syncthreads();
+  }
+  need = remaining;
+  int cnt = 0;
+#pragma unroll
+  for (int m = 0; m < KPT; ++m)
+    if (i0 + m < NB) cnt += key[m] > T ? (1 << 16) : (key[m] == T ? 1 : 0);
+  const int incl = wave_incl_scan(cnt, lane);
+  if (lane == kWave - 1) L.wsum[wave] = incl;
+  __syncthreads();
+  if (wave == 0) {
+    int v = lane < NTHR / kWave ? L.wsum[lane] : 0;
+    int vi = wave_incl_scan(v, lane);
+    if (lane < NTHR / kWave) L.wsum[lane] = vi - v;
+  }
+  __syncthreads();
+  const int before = L.wsum[wave] + incl - cnt;
+  gt = (unsigned)before >> 16;
+  eq = (unsigned)before & 0xFFFFu;
+}
+
+// Position of key m in ascending block order among the selected, or -1.
+__device__ __forceinline__ int topk_position(uint32_t key, uint32_t T, unsigned need, unsigned& gt, unsigned& eq) {
+  if (key > T) {
+    const int pos = (int)(gt + (eq < need ? eq : need));
+    ++gt;
+    return pos;
+  }
+  if (key == T) {
+    const int pos = eq < need ? (int)(gt + eq) : -1;
+    ++eq;
+    return pos;
+  }
+  return -1;
+}
+
 // ------------------------------------------------------------- launches --
 // Descriptor of one NF4 projection's block storage.  A block (slot) holds 32
 // rows of a gate/up weight, or a 32-column block of the down weight.
@@ -383,6 +489,11 @@ struct DecodeArgs {
   int st_gu_abytes;
   int st_dn_bytes;       // extent of one down block: packed bytes, absmax bytes
   int st_dn_abytes;
+  // with sel_scores != nullptr the gate/up kernel selects the top k of these
+  // fp16 scores itself (ascending ids, ties to the lower id) and writes them
+  // to sel_out; sel is then unused
+  const uint16_t* sel_scores;  // [NB]
+  int32_t* sel_out;            // [k]
 };
 
 // Resolve selected position j to (storage view index, validity):
@@ -397,9 +508,9 @@ struct BlockRef {
   bool silent;  // invalid but expected (skipped entry)
 };
 
-__device__ __forceinline__ BlockRef resolve_block(const DecodeArgs& a, int j) {
+// Same, from the block id b = sel[j] already loaded.
+__device__ __forceinline__ BlockRef resolve_id(const DecodeArgs& a, int b) {
   BlockRef r;
-  const int b = a.sel ? a.sel[j] : j;
   r.b = b;
   r.ok = b >= 0 && b < a.NB;
   r.silent = a.skip_negative && b < 0;
@@ -411,12 +522,18 @@ __device__ __forceinline__ BlockRef resolve_block(const DecodeArgs& a, int j) {
   return r;
 }
 
+__device__ __forceinline__ BlockRef resolve_block(const DecodeArgs& a, int j) {
+  return resolve_id(a, a.sel ? a.sel[j] : j);
+}
+
 void launch_decode_gate_up(const DecodeArgs& a, hipStream_t s);
 void launch_decode_down(const DecodeArgs& a, hipStream_t s);
 // Streaming decode (hidden size a multiple of 2048): gate/up, down, final sum.
 // Sets the st_* tiling fields for a device with `cus` compute units; false
 // (and st_gu_wgs = 0) when the streaming kernels do not apply.
 bool plan_streaming(DecodeArgs& a, int cus);
+// Whether the streaming kernels can select the top k themselves (NB, k limits).
+bool streaming_can_select(int NB, int k);
 void launch_decode_streaming(const DecodeArgs& a, hipStream_t s);
 int device_cus();
 
@@ -441,6 +558,8 @@ struct RouteArgs {
 };
 
 void launch_route(const RouteArgs& a, hipStream_t s);
+// The latent and score kernels only (the top-k runs inside the decode).
+void launch_route_scores(const RouteArgs& a, hipStream_t s);
 
 struct LinearArgs {
   const uint16_t* x;          // [rows][in_dim]

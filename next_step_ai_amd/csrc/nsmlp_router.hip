@@ -133,42 +133,6 @@ __global__ void __launch_bounds__(kScoreThreads) k_scores(RouteArgs a) {
   if (a.scores_out != nullptr) a.scores_out[(long long)row * a.NB + j] = sc;
 }
 
-__device__ __forceinline__ int wave_incl_scan(int v, int lane) {
-#pragma unroll
-  for (int d = 1; d < kWave; d <<= 1) {
-    int o = __shfl_up(v, d, kWave);
-    if (lane >= d) v += o;
-  }
-  return v;
-}
-
-// Wave 0: the digit (from the top) holding the remaining-th largest entry of
-// hist; sets *digit and *above (count of entries in higher digits).
-__device__ __forceinline__ void find_digit(const unsigned* hist, unsigned remaining, int lane, unsigned* digit,
-                                           unsigned* above) {
-  unsigned c[4];
-  unsigned local = 0;
-#pragma unroll
-  for (int b = 0; b < 4; ++b) {
-    c[b] = hist[255 - 4 * lane - b];
-    local += c[b];
-  }
-  const unsigned incl = (unsigned)wave_incl_scan((int)local, lane);
-  const unsigned excl = incl - local;
-  if (excl < remaining && remaining <= incl) {
-    unsigned cum = excl;
-#pragma unroll
-    for (int b = 0; b < 4; ++b) {
-      if (cum + c[b] >= remaining) {
-        *digit = 255u - 4u * lane - b;
-        *above = cum;
-        break;
-      }
-      cum += c[b];
-    }
-  }
-}
-
 // Top-k of one token's scores (keys: fp16 order key, ties to the lower block
 // index).  Each thread holds KPT consecutive keys in registers.  Two 8-bit
 // histogram passes find the threshold score T and how many entries equal to
@@ -179,76 +143,25 @@ template <int KPT>
 __global__ void __launch_bounds__(kSelThreads) k_select(RouteArgs a) {
   const int row = blockIdx.x;
   const int tid = threadIdx.x;
-  const int lane = tid % kWave, wave = tid / kWave;
   const uint16_t* sc = a.scores + (long long)row * a.NB;
   const int NB = a.NB;
   const int k = a.k;
-  __shared__ unsigned hist[256];
-  __shared__ unsigned s_digit, s_above;
-  __shared__ int wsum[kSelThreads / kWave];
+  __shared__ TopkLds L;
   const int i0 = tid * KPT;
   uint32_t key[KPT];
 #pragma unroll
   for (int m = 0; m < KPT; ++m) key[m] = i0 + m < NB ? f16_order_key(sc[i0 + m]) : 0u;
-  uint32_t T = 0;
-  unsigned remaining = (unsigned)k;
-  for (int pass = 0; pass < 2; ++pass) {
-    for (int i = tid; i < 256; i += kSelThreads) hist[i] = 0;
-    __syncthreads();
-#pragma unroll
-    for (int m = 0; m < KPT; ++m) {
-      if (i0 + m >= NB) continue;
-      if (pass == 0)
-        atomicAdd(&hist[key[m] >> 8], 1u);
-      else if ((key[m] >> 8) == (T >> 8))
-        atomicAdd(&hist[key[m] & 0xFFu], 1u);
-    }
-    __syncthreads();
-    if (wave == 0) find_digit(hist, remaining, lane, &s_digit, &s_above);
-    __syncthreads();
-    T |= s_digit << (pass == 0 ? 8 : 0);
-    remaining -= s_above;
-    __syncthreads();
-  }
-  const unsigned need = remaining;  // entries equal to T that are taken
-  // Ordered compaction: counts above T and equal to T, packed in one scanned
-  // word (each < 2^16).
-  int cnt = 0;
-#pragma unroll
-  for (int m = 0; m < KPT; ++m)
-    if (i0 + m < NB) cnt += key[m] > T ? (1 << 16) : (key[m] == T ? 1 : 0);
-  const int incl = wave_incl_scan(cnt, lane);
-  if (lane == kWave - 1) wsum[wave] = incl;
-  __syncthreads();
-  if (wave == 0) {
-    int v = lane < kSelThreads / kWave ? wsum[lane] : 0;
-    int vi = wave_incl_scan(v, lane);
-    if (lane < kSelThreads / kWave) wsum[lane] = vi - v;
-  }
-  __syncthreads();
-  const int before = wsum[wave] + incl - cnt;
-  unsigned gt = (unsigned)before >> 16, eq = (unsigned)before & 0xFFFFu;
+  uint32_t T;
+  unsigned need, gt, eq;
+  topk_threshold<kSelThreads, KPT>(key, i0, NB, k, L, T, need, gt, eq);
   int32_t* out = a.sel + (long long)row * k;
   extern __shared__ uint32_t selkeys[];  // [k] (sorted output)
 #pragma unroll
   for (int m = 0; m < KPT; ++m) {
     const int i = i0 + m;
     if (i >= NB) continue;
-    unsigned pos;
-    if (key[m] > T) {
-      pos = gt + (eq < need ? eq : need);
-      ++gt;
-    } else if (key[m] == T) {
-      if (eq >= need) {
-        ++eq;
-        continue;
-      }
-      pos = gt + eq;
-      ++eq;
-    } else {
-      continue;
-    }
-    if (pos >= (unsigned)k) continue;
+    const int pos = topk_position(key[m], T, need, gt, eq);
+    if (pos < 0 || pos >= k) continue;
     if (!a.sorted)
       out[pos] = i;
     else
@@ -265,6 +178,16 @@ __global__ void __launch_bounds__(kSelThreads) k_select(RouteArgs a) {
 }
 
 }  // namespace
+
+void launch_route_scores(const RouteArgs& a, hipStream_t s) {
+  dim3 g1(a.R, a.rows);
+  if (a.vec)
+    hipLaunchKernelGGL(k_latent<true>, g1, dim3(kLatThreads), 0, s, a);
+  else
+    hipLaunchKernelGGL(k_latent<false>, g1, dim3(kLatThreads), 0, s, a);
+  dim3 g2((a.NB + kScoresPerWg - 1) / kScoresPerWg, a.rows);
+  hipLaunchKernelGGL(k_scores, g2, dim3(kScoreThreads), (size_t)a.R * sizeof(uint16_t), s, a);
+}
 
 void launch_route(const RouteArgs& a, hipStream_t s) {
   dim3 g1(a.R, a.rows);

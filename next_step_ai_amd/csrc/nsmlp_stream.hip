@@ -51,8 +51,14 @@ constexpr int kDnStages = 2;
 constexpr int kMaxItems = 64;      // items per wave resolved up front (one per lane)
 constexpr int kMaxDnBlocks = 512;  // blocks per down workgroup (activations in LDS)
 constexpr int kLutWords = kRepLutBytes / 4;
-// dynamic LDS: table, split sums [2][8][4]
+// dynamic LDS: table, split sums [2][8][4]; with the in-kernel top-k also the
+// selection state and the selected ids [k]
 constexpr size_t kGuLds = kRepLutBytes + 2 * kWaves * 4 * sizeof(float);
+constexpr int kGuTopkWord = (int)(kGuLds / 4);
+constexpr int kGuSelWord = kGuTopkWord + (int)((sizeof(TopkLds) + 15) / 16 * 4);
+constexpr int kSelMaxNB = 4096;  // 8 scores per thread
+constexpr int kSelMaxK = 2048;
+constexpr size_t kGuSelLds = (size_t)kGuSelWord * 4 + kSelMaxK * sizeof(int32_t);
 // dynamic LDS: table, activation pairs [512][16], scales [512], wave sums [8][64]
 constexpr size_t kDnLds = kRepLutBytes + kMaxDnBlocks * 16 * 4 + kMaxDnBlocks * 4 + kWaves * kWave * 4;
 
@@ -172,7 +178,10 @@ __device__ __forceinline__ float reduce4(const float (&v)[4], int lane) {
   return k;
 }
 
-template <bool AFFINE>
+// SKPT > 0: the workgroup first selects the top k of a.sel_scores itself (SKPT
+// scores per thread; ascending ids, ties to the lower id), so the selection
+// needs no launch of its own; workgroup 0 also writes the ids to a.sel_out.
+template <bool AFFINE, int SKPT>
 __global__ void __launch_bounds__(kThreads8, 2) k_gu_rep(DecodeArgs a) {
   extern __shared__ __attribute__((aligned(16))) uint32_t lds[];
   float* comb = reinterpret_cast<float*>(lds + kLutWords);
@@ -187,23 +196,24 @@ __global__ void __launch_bounds__(kThreads8, 2) k_gu_rep(DecodeArgs a) {
   const uint32_t col = (uint32_t)(s * kSplit + lane * 32);
   const uint32_t cb = col >> 1, ca4 = (col >> a.qbs_shift) * 4u;
 
-  // lane i: block reference of this wave's round-i item.  Split 0 of row
-  // pair 0 reports an invalid block and publishes the reference.
-  uint32_t enc_v = kBad;
-  {
-    const int id = (lane * nwg + wg) * NS + q;
-    if (lane < R && id < n_items) {
-      const BlockRef br = resolve_block(a, id >> 4);
-      enc_v = encode_ref(br);
-      if (s == 0 && (id & 15) == 0) {
-        if (!br.ok && !br.silent) atomicOr(a.status, 1);
-        a.st_enc[id >> 4] = enc_v;
-      }
+  // Independent loads first: the block id of each lane's item (lane i:
+  // round i), the code book and the token split.
+  const int id0 = (lane * nwg + wg) * NS + q;
+  const bool own = lane < R && id0 < n_items;
+  const int jb = own ? id0 >> 4 : 0;
+  int b_id = 0;
+  constexpr int kKeys = SKPT > 0 ? SKPT : 1;
+  uint32_t skey[kKeys];
+  const int i0 = tid * kKeys;
+  if constexpr (SKPT == 0) {
+    b_id = a.sel ? a.sel[jb] : jb;
+  } else {
+#pragma unroll
+    for (int m = 0; m < SKPT; ++m) {
+      const int i = i0 + m < a.NB ? i0 + m : a.NB - 1;  // clamped: the load is unconditional
+      skey[m] = f16_order_key(a.sel_scores[i]);
     }
   }
-  // The code book and the token split are loaded while the references
-  // resolve, and before the weight stream, so that waiting for them never
-  // drains it.
   LutCodes codes;
   lut_codes_load(a.code, a.code_up, tid, codes);
   uint32_t xp[16];
@@ -219,14 +229,45 @@ __global__ void __launch_bounds__(kThreads8, 2) k_gu_rep(DecodeArgs a) {
     }
   }
   sched_fence();
-  GuStage st[kGuStages];
+  lut_store(lds, codes, tid);
+  int32_t* sel_l = reinterpret_cast<int32_t*>(lds + kGuSelWord);
+  if constexpr (SKPT > 0) {
+    TopkLds& tl = *reinterpret_cast<TopkLds*>(lds + kGuTopkWord);
+    uint32_t T;
+    unsigned need, gt, eq;
+    topk_threshold<kThreads8, SKPT>(skey, i0, a.NB, a.k, tl, T, need, gt, eq);
+    int32_t* sel_out = wg == 0 ? a.sel_out : nullptr;
 #pragma unroll
-  for (int i = 0; i < kGuStages; ++i)
+    for (int m = 0; m < SKPT; ++m) {
+      if (i0 + m >= a.NB) continue;
+      const int pos = topk_position(skey[m], T, need, gt, eq);
+      if (pos < 0 || pos >= a.k) continue;
+      sel_l[pos] = i0 + m;
+      if (sel_out != nullptr) sel_out[pos] = i0 + m;
+    }
+    lds_barrier();
+    b_id = sel_l[jb];
+  }
+  // Block references (slot lookup).  Split 0 of row pair 0 reports an
+  // invalid block and publishes the reference for the down kernel.
+  uint32_t enc_v = kBad;
+  if (own) {
+    const BlockRef br = resolve_id(a, b_id);
+    enc_v = encode_ref(br);
+    if (s == 0 && (id0 & 15) == 0) {
+      if (!br.ok && !br.silent) atomicOr(a.status, 1);
+      a.st_enc[id0 >> 4] = enc_v;
+    }
+  }
+  // Stage 0 of every wave goes out before any later stage; the barrier also
+  // publishes the code table.
+  GuStage st[kGuStages];
+  gu_issue(a, R > 0 ? lane_value(enc_v, 0) : kBad, (wg * NS + q) & 15, cb, ca4, st[0]);
+  lds_barrier();
+#pragma unroll
+  for (int i = 1; i < kGuStages; ++i)
     gu_issue(a, i < R ? lane_value(enc_v, i) : kBad, ((i * nwg + wg) * NS + q) & 15, cb, ca4, st[i]);
   sched_fence();
-
-  lut_store(lds, codes, tid);
-  lds_barrier();
 
   uint32_t adg[4], adu[4];
 #pragma unroll
@@ -268,7 +309,8 @@ __global__ void __launch_bounds__(kThreads8, 2) k_gu_rep(DecodeArgs a) {
           if constexpr (AFFINE) {
             const uint32_t enc = lane_value(enc_v, r);
             if (!(enc & kBad)) {
-              const long long bn = (long long)(a.sel ? a.sel[j] : j) * 32 + n;
+              const int bj = SKPT > 0 ? sel_l[j] : (a.sel ? a.sel[j] : j);
+              const long long bn = (long long)bj * 32 + n;
               if (a.gate_bias != nullptr) g += h2f(a.gate_bias[bn]);
               if (a.up_bias != nullptr) u += h2f(a.up_bias[bn]);
               if (a.mask != nullptr) {
@@ -514,17 +556,27 @@ bool plan_streaming(DecodeArgs& a, int cus) {
   return true;
 }
 
+bool streaming_can_select(int NB, int k) { return NB >= 1 && NB <= kSelMaxNB && k >= 1 && k <= NB && k <= kSelMaxK; }
+
 void launch_decode_streaming(const DecodeArgs& a, hipStream_t s) {
   std::call_once(g_attr_once, [] {
-    set_lds_limit(k_gu_rep<false>, kGuLds);
-    set_lds_limit(k_gu_rep<true>, kGuLds);
+    set_lds_limit(k_gu_rep<false, 0>, kGuLds);
+    set_lds_limit(k_gu_rep<true, 0>, kGuLds);
+    set_lds_limit(k_gu_rep<false, 4>, kGuSelLds);
+    set_lds_limit(k_gu_rep<true, 4>, kGuSelLds);
+    set_lds_limit(k_gu_rep<false, 8>, kGuSelLds);
+    set_lds_limit(k_gu_rep<true, 8>, kGuSelLds);
     set_lds_limit(k_down_rep, kDnLds);
   });
   const bool affine = a.gate_bias != nullptr || a.up_bias != nullptr || a.mask != nullptr;
-  if (affine)
-    hipLaunchKernelGGL(k_gu_rep<true>, dim3(a.st_gu_wgs), dim3(kThreads8), kGuLds, s, a);
-  else
-    hipLaunchKernelGGL(k_gu_rep<false>, dim3(a.st_gu_wgs), dim3(kThreads8), kGuLds, s, a);
+  void (*gu)(DecodeArgs) = affine ? k_gu_rep<true, 0> : k_gu_rep<false, 0>;
+  size_t gu_lds = kGuLds;
+  if (a.sel_scores != nullptr) {
+    const bool four = a.NB <= 4 * kThreads8;
+    gu = affine ? (four ? k_gu_rep<true, 4> : k_gu_rep<true, 8>) : (four ? k_gu_rep<false, 4> : k_gu_rep<false, 8>);
+    gu_lds = (size_t)kGuSelWord * 4 + (size_t)a.k * sizeof(int32_t);
+  }
+  gu<<<dim3(a.st_gu_wgs), dim3(kThreads8), gu_lds, s>>>(a);
   hipLaunchKernelGGL(k_down_rep, dim3((a.H / kWave) * a.st_dn_gx), dim3(kThreads8), kDnLds, s, a);
   if (a.st_dn_gx > 1) hipLaunchKernelGGL(k_fin_rep, dim3(a.H / 256), dim3(256), 0, s, a);
 }

@@ -74,6 +74,39 @@ def test_decode_layer_matches_oracle(gpu, orc, H, I, R, k, seed):
     assert torch.equal(out2, out) and torch.equal(sel2, sel)
 
 
+@pytest.mark.parametrize("H,I,k,n_pos", [
+    (2048, 2048, 64, 10),      # k = NB: every block
+    (2048, 8192, 200, 37),     # ties at the clamped score 0 decide most of the selection
+    (2048, 81920, 300, 250),   # 2560 blocks: 8 scores per thread in the in-kernel top-k
+    (2048, 81920, 2048, 3000), # the largest k the in-kernel top-k takes
+])
+def test_decode_layer_selection_and_ties(gpu, orc, H, I, k, n_pos):
+    """The one-call layer path selects inside the gate/up kernel; its blocks and
+    output equal routing on its own followed by the slot-table decode."""
+    from next_step_ai_amd.router import route_tokens
+    from next_step_ai_amd.synth import make_synthetic_layer
+
+    print(f"layer selection H={H} I={I} k={k} positive={n_pos}", flush=True)
+    L = make_synthetic_layer(H=H, I=I, R=16, seed=77, device=gpu)
+    NB = L.NB
+    rng = np.random.default_rng(k)
+    neg = rng.permutation(NB)[: max(NB - n_pos, 0)]
+    sb = L.score_b.clone()
+    sb[torch.from_numpy(neg).to(gpu)] = -1000.0  # score < 0 -> clamped to 0: ties
+    L.score_b = sb
+    layer = L.layer(k)
+    out, sel = layer.forward(L.x)
+    torch.cuda.synchronize()
+    _, _, sel_o = orc.route(_u16(L.x), _u16(L.enc_w), _u16(L.enc_b), _u16(L.score_w), _u16(L.score_b), k)
+    sel_g = _np(sel).astype(np.int64)
+    assert np.array_equal(sel_g, np.sort(sel_o)), "routed blocks differ from the oracle"
+    sel_r = route_tokens(L.x.reshape(1, H), L.routing_dict(k), k, sorted_by_score=False).reshape(-1)
+    assert torch.equal(sel_r.to(torch.int32), sel)
+    ref = layer.table.decode(L.x, sel_r.to(torch.int32))
+    torch.cuda.synchronize()
+    assert torch.equal(out, ref), "layer output differs from route + slot decode"
+
+
 def test_single_kernel_dropin_matches_slot_path(gpu, orc):
     from next_step_ai_amd.sparse_mlp import (
         triton_fused_sparse_mlp_decode_4bit,
