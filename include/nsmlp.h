@@ -23,6 +23,14 @@
  *   "Slot" storage (the HBM hot-block table) is block-major:
  *     gate/up packed [slots][32][H/2] u8,  absmax [slots][32][H/qbs] f32
  *     down    packed [slots][H][16]  u8,   absmax [slots][H] f32
+ *   Double-quantised absmax (the bitsandbytes nested quant state, which the
+ *   reference resolves to fp32 at RT:4621-4625): u8 codes q in the absmax
+ *   shapes above, one fp32 absmax2 per dq_block consecutive absmax of the
+ *   full row-major weight, a 256-entry code2 and an fp32 offset:
+ *     absmax = fp32(fp32(code2[q] * absmax2[f / dq_block]) + offset)
+ *   where f is the absmax's index in the full weight (gate/up [I][H/qbs],
+ *   down [H][I/qbs]); both roundings are kept (no fused multiply-add), so
+ *   the result equals the reference's resolved fp32 absmax bit for bit.
  */
 #ifndef NSMLP_H
 #define NSMLP_H
@@ -113,6 +121,26 @@ typedef struct nsmlp_slot_table {
   const float* host_down_absmax;
   const float* code;                 /* [16] NF4 code book (device) */
   const void* down_bias;             /* [H] fp16 or NULL */
+  /* Double-quantised absmax (version >= 101).  dq_block == 0: the fp32
+   * *_absmax above are read.  dq_block > 0 (a power of two; bitsandbytes
+   * uses 256): the fp32 *_absmax are ignored and the u8 codes below, in the
+   * same shapes and slot layout, are read instead. */
+  int dq_block;
+  const uint8_t* gate_qabsmax;       /* [n_slots][32][H/qbs] u8 */
+  const uint8_t* up_qabsmax;
+  const uint8_t* down_qabsmax;       /* [n_slots][H] u8 */
+  const uint8_t* host_gate_qabsmax;  /* host copies (with the host packed copies) */
+  const uint8_t* host_up_qabsmax;
+  const uint8_t* host_down_qabsmax;
+  const float* gate_absmax2;         /* [ceil(I*H/qbs / dq_block)] f32 (device) */
+  const float* up_absmax2;
+  const float* down_absmax2;         /* [ceil(H*I/qbs / dq_block)] f32 (device) */
+  const float* gate_code2;           /* [256] f32 second-level code book (device) */
+  const float* up_code2;
+  const float* down_code2;
+  float gate_offset;
+  float up_offset;
+  float down_offset;
 } nsmlp_slot_table;
 
 size_t nsmlp_decode_workspace_bytes(int H, int k);
@@ -219,6 +247,31 @@ int nsmlp_gather_row_blocks(const uint8_t* src_packed, const float* src_absmax, 
 int nsmlp_gather_down_columns(const uint8_t* src_packed, const float* src_absmax, const int32_t* blocks, int n,
                               int out_features, int in_features, int qbs, int dst_layout, uint8_t* dst_packed,
                               float* dst_absmax, void* stream);
+
+/* The same two gathers for double-quantised absmax (u8 codes in the fp32
+ * absmax positions; the packed bytes are gathered as above).  Replace the
+ * same reference code, with the nested state kept instead of resolved
+ * (RT:4621-4625). */
+int nsmlp_gather_row_blocks_q8(const uint8_t* src_packed, const uint8_t* src_qabsmax, int src_blocks,
+                               const int32_t* blocks, int n, int in_features, int qbs, uint8_t* dst_packed,
+                               uint8_t* dst_qabsmax, void* stream);
+int nsmlp_gather_down_columns_q8(const uint8_t* src_packed, const uint8_t* src_qabsmax, const int32_t* blocks, int n,
+                                 int out_features, int in_features, int qbs, int dst_layout, uint8_t* dst_packed,
+                                 uint8_t* dst_qabsmax, void* stream);
+
+/* Double quantisation of an fp32 absmax vector (bitsandbytes
+ * compress_statistics, restated; the reference reads the result back with
+ * dequantize_blockwise + offset at RT:4621-4625 and safetensor_loader.py:
+ * 403-406): a = absmax - offset; per dq_block consecutive entries absmax2 =
+ * max |a|, q = index of the code2 entry nearest to a * fp32(1 / absmax2)
+ * (ties: the lower index; code2 ascending, 256 entries).  The caller gives
+ * the offset (bitsandbytes: the mean of absmax). */
+int nsmlp_absmax_dq_quantize(const float* absmax, long long n, int dq_block, const float* code2, float offset,
+                             uint8_t* q, float* absmax2, void* stream);
+/* Its inverse, as the runtime resolves it (RT:4621-4625):
+ * out[i] = fp32(fp32(code2[q[i]] * absmax2[i / dq_block]) + offset). */
+int nsmlp_absmax_dq_dequantize(const uint8_t* q, long long n, int dq_block, const float* code2, const float* absmax2,
+                               float offset, float* out, void* stream);
 
 /* Device-side address of pinned host memory (hipHostMalloc'd, e.g. a torch
  * pinned tensor) for the slot table's host_* pointers: misses are read by the

@@ -43,6 +43,12 @@ class SlotTable(ctypes.Structure):
         ("host_down_packed", P), ("host_down_absmax", P),
         ("code", P),
         ("down_bias", P),
+        ("dq_block", I32),
+        ("gate_qabsmax", P), ("up_qabsmax", P), ("down_qabsmax", P),
+        ("host_gate_qabsmax", P), ("host_up_qabsmax", P), ("host_down_qabsmax", P),
+        ("gate_absmax2", P), ("up_absmax2", P), ("down_absmax2", P),
+        ("gate_code2", P), ("up_code2", P), ("down_code2", P),
+        ("gate_offset", F32), ("up_offset", F32), ("down_offset", F32),
     ]
 
 
@@ -77,6 +83,10 @@ SIGNATURES: dict[str, tuple] = {
     "nsmlp_silu_mul_f16": (I32, [P, P, P, I64, P]),
     "nsmlp_gather_row_blocks": (I32, [P, P, I32, P, I32, I32, I32, P, P, P]),
     "nsmlp_gather_down_columns": (I32, [P, P, P, I32, I32, I32, I32, I32, P, P, P]),
+    "nsmlp_gather_row_blocks_q8": (I32, [P, P, I32, P, I32, I32, I32, P, P, P]),
+    "nsmlp_gather_down_columns_q8": (I32, [P, P, P, I32, I32, I32, I32, I32, P, P, P]),
+    "nsmlp_absmax_dq_quantize": (I32, [P, I64, I32, P, F32, P, P, P]),
+    "nsmlp_absmax_dq_dequantize": (I32, [P, I64, I32, P, P, F32, P, P]),
     "nsmlp_host_device_pointer": (I32, [P, ctypes.POINTER(P)]),
     "nsmlp_synth_normal_f16": (I32, [U64, I64, F32, P, P]),
     "nsmlp_synth_normal_f32": (I32, [U64, I64, F32, P, P]),

@@ -168,6 +168,7 @@ int fill_decode_ws(DecodeArgs& a, void* ws, size_t ws_bytes) {
   // [k][H/256][64] split partials of the generic path
   a.st_act = a.part;
   a.st_enc = (uint32_t*)(a.part + (size_t)a.k * 32);
+  a.st_bid = (int32_t*)(a.st_enc + a.k);
   a.act = (uint32_t*)(base + L.act);
   a.act_scale = (float*)(base + L.act_scale);
   a.outpart = (float*)(base + L.outpart);
@@ -238,9 +239,25 @@ int fill_route(RouteArgs& r, const void* x, int rows, int H, const void* enc_w, 
 int table_to_args(const nsmlp_slot_table* t, DecodeArgs& a) {
   if (t == nullptr) return set_error(NSMLP_EINVAL, "slot table is NULL");
   if (t->I <= 0 || t->I % 32 != 0) return set_error(NSMLP_EINVAL, "intermediate size %d must be a multiple of 32", t->I);
-  if (!t->gate_packed || !t->gate_absmax || !t->up_packed || !t->up_absmax || !t->down_packed || !t->down_absmax ||
-      !t->code)
-    if (t->n_slots > 0) return set_error(NSMLP_EINVAL, "slot storage pointers must be non-NULL");
+  const bool dq = t->dq_block > 0;
+  if (t->dq_block < 0 || (dq && (t->dq_block & (t->dq_block - 1)) != 0))
+    return set_error(NSMLP_EINVAL, "dq_block %d must be 0 or a power of two", t->dq_block);
+  if (t->code == nullptr) return set_error(NSMLP_EINVAL, "code must be non-NULL");
+  if (t->n_slots > 0) {
+    const bool abs_ok = dq ? (t->gate_qabsmax && t->up_qabsmax && t->down_qabsmax)
+                           : (t->gate_absmax && t->up_absmax && t->down_absmax);
+    if (!t->gate_packed || !t->up_packed || !t->down_packed || !abs_ok)
+      return set_error(NSMLP_EINVAL, "slot storage pointers must be non-NULL");
+  }
+  if (t->host_gate_packed != nullptr) {
+    const bool abs_ok = dq ? (t->host_gate_qabsmax && t->host_up_qabsmax && t->host_down_qabsmax)
+                           : (t->host_gate_absmax && t->host_up_absmax && t->host_down_absmax);
+    if (!t->host_up_packed || !t->host_down_packed || !abs_ok)
+      return set_error(NSMLP_EINVAL, "host copy pointers must all be non-NULL (or host_gate_packed NULL)");
+  }
+  if (dq && (!t->gate_absmax2 || !t->up_absmax2 || !t->down_absmax2 || !t->gate_code2 || !t->up_code2 ||
+             !t->down_code2))
+    return set_error(NSMLP_EINVAL, "double-quantised absmax needs absmax2 and code2 of every projection");
   if (t->n_slots < 0) return set_error(NSMLP_EINVAL, "n_slots must be >= 0");
   if (t->lookup == nullptr && t->n_slots < t->I / 32)
     return set_error(NSMLP_EINVAL, "identity lookup needs n_slots >= num_blocks");
@@ -262,6 +279,27 @@ int table_to_args(const nsmlp_slot_table* t, DecodeArgs& a) {
   a.host_down = down_block_major_view(t->host_down_packed, t->host_down_absmax, t->H);
   a.code = a.code_up = a.code_down = t->code;
   a.down_bias = (const uint16_t*)t->down_bias;
+  if (dq) {
+    a.dq = 1;
+    a.dq_shift = __builtin_ctz((unsigned)t->dq_block);
+    a.gate.absmax = a.up.absmax = a.down.absmax = nullptr;
+    a.host_gate.absmax = a.host_up.absmax = a.host_down.absmax = nullptr;
+    a.gate.qabsmax = t->gate_qabsmax;
+    a.up.qabsmax = t->up_qabsmax;
+    a.down.qabsmax = t->down_qabsmax;
+    a.host_gate.qabsmax = t->host_gate_qabsmax;
+    a.host_up.qabsmax = t->host_up_qabsmax;
+    a.host_down.qabsmax = t->host_down_qabsmax;
+    a.gate.absmax2 = a.host_gate.absmax2 = t->gate_absmax2;
+    a.up.absmax2 = a.host_up.absmax2 = t->up_absmax2;
+    a.down.absmax2 = a.host_down.absmax2 = t->down_absmax2;
+    a.gate.code2 = a.host_gate.code2 = t->gate_code2;
+    a.up.code2 = a.host_up.code2 = t->up_code2;
+    a.down.code2 = a.host_down.code2 = t->down_code2;
+    a.gate.offset = a.host_gate.offset = t->gate_offset;
+    a.up.offset = a.host_up.offset = t->up_offset;
+    a.down.offset = a.host_down.offset = t->down_offset;
+  }
   return NSMLP_OK;
 }
 
@@ -285,11 +323,50 @@ int check_launch(const char* what) {
 
 using namespace nsmlp;
 
+namespace nsmlp {
+namespace {
+
+template <typename AbsT>
+int gather_rows_impl(const uint8_t* src_packed, const AbsT* src_absmax, int src_blocks, const int32_t* blocks, int n,
+                     int in_features, int qbs, uint8_t* dst_packed, AbsT* dst_absmax, void* stream) {
+  if (n < 0 || src_blocks < 0 || in_features <= 0 || in_features % 32 != 0 || qbs <= 0 ||
+      (32LL * in_features) % qbs != 0)
+    return set_error(NSMLP_EINVAL, "bad row-block gather geometry");
+  if (n == 0) return NSMLP_OK;
+  if (!src_packed || !src_absmax || !blocks || !dst_packed || !dst_absmax)
+    return set_error(NSMLP_EINVAL, "NULL tensor argument");
+  if (!aligned16(src_packed) || !aligned16(dst_packed)) return set_error(NSMLP_EINVAL, "packed must be 16-byte aligned");
+  launch_gather_rows<AbsT>(src_packed, src_absmax, blocks, src_blocks, n, 16LL * in_features,
+                           32LL * in_features / qbs, dst_packed, dst_absmax, (hipStream_t)stream);
+  return check_launch("gather rows");
+}
+
+template <typename AbsT>
+int gather_down_impl(const uint8_t* src_packed, const AbsT* src_absmax, const int32_t* blocks, int n,
+                     int out_features, int in_features, int qbs, int dst_layout, uint8_t* dst_packed,
+                     AbsT* dst_absmax, void* stream) {
+  if (n < 0 || out_features <= 0 || in_features <= 0 || in_features % 32 != 0 || qbs <= 0 || qbs % 32 != 0 ||
+      in_features % qbs != 0)
+    return set_error(NSMLP_EINVAL, "bad down-column gather geometry");
+  if (dst_layout != NSMLP_DOWN_BLOCK_MAJOR && dst_layout != NSMLP_DOWN_GATHERED)
+    return set_error(NSMLP_EINVAL, "unknown down layout %d", dst_layout);
+  if (n == 0) return NSMLP_OK;
+  if (!src_packed || !src_absmax || !blocks || !dst_packed || !dst_absmax)
+    return set_error(NSMLP_EINVAL, "NULL tensor argument");
+  if (!aligned16(src_packed) || !aligned16(dst_packed)) return set_error(NSMLP_EINVAL, "packed must be 16-byte aligned");
+  launch_gather_down<AbsT>(src_packed, src_absmax, blocks, n, out_features, in_features, qbs, dst_layout, dst_packed,
+                           dst_absmax, (hipStream_t)stream);
+  return check_launch("gather down");
+}
+
+}  // namespace
+}  // namespace nsmlp
+
 extern "C" {
 
 const char* nsmlp_last_error(void) { return g_err; }
 
-int nsmlp_version(void) { return 100; }
+int nsmlp_version(void) { return 101; }
 
 int nsmlp_device_supported(int device) {
   hipDeviceProp_t prop;
@@ -573,34 +650,49 @@ int nsmlp_silu_mul_f16(const void* gate, const void* up, void* out, long long n,
 int nsmlp_gather_row_blocks(const uint8_t* src_packed, const float* src_absmax, int src_blocks,
                             const int32_t* blocks, int n, int in_features, int qbs, uint8_t* dst_packed,
                             float* dst_absmax, void* stream) {
-  if (n < 0 || src_blocks < 0 || in_features <= 0 || in_features % 32 != 0 || qbs <= 0 ||
-      (32LL * in_features) % qbs != 0)
-    return set_error(NSMLP_EINVAL, "bad row-block gather geometry");
-  if (n == 0) return NSMLP_OK;
-  if (!src_packed || !src_absmax || !blocks || !dst_packed || !dst_absmax)
-    return set_error(NSMLP_EINVAL, "NULL tensor argument");
-  if (!aligned16(src_packed) || !aligned16(dst_packed)) return set_error(NSMLP_EINVAL, "packed must be 16-byte aligned");
-  launch_gather_rows(src_packed, src_absmax, blocks, src_blocks, n, 16LL * in_features, 32LL * in_features / qbs,
-                     dst_packed,
-                     dst_absmax, (hipStream_t)stream);
-  return check_launch("gather rows");
+  return gather_rows_impl<float>(src_packed, src_absmax, src_blocks, blocks, n, in_features, qbs, dst_packed,
+                                 dst_absmax, stream);
+}
+
+int nsmlp_gather_row_blocks_q8(const uint8_t* src_packed, const uint8_t* src_qabsmax, int src_blocks,
+                               const int32_t* blocks, int n, int in_features, int qbs, uint8_t* dst_packed,
+                               uint8_t* dst_qabsmax, void* stream) {
+  return gather_rows_impl<uint8_t>(src_packed, src_qabsmax, src_blocks, blocks, n, in_features, qbs, dst_packed,
+                                   dst_qabsmax, stream);
 }
 
 int nsmlp_gather_down_columns(const uint8_t* src_packed, const float* src_absmax, const int32_t* blocks, int n,
                               int out_features, int in_features, int qbs, int dst_layout, uint8_t* dst_packed,
                               float* dst_absmax, void* stream) {
-  if (n < 0 || out_features <= 0 || in_features <= 0 || in_features % 32 != 0 || qbs <= 0 || qbs % 32 != 0 ||
-      in_features % qbs != 0)
-    return set_error(NSMLP_EINVAL, "bad down-column gather geometry");
-  if (dst_layout != NSMLP_DOWN_BLOCK_MAJOR && dst_layout != NSMLP_DOWN_GATHERED)
-    return set_error(NSMLP_EINVAL, "unknown down layout %d", dst_layout);
+  return gather_down_impl<float>(src_packed, src_absmax, blocks, n, out_features, in_features, qbs, dst_layout,
+                                 dst_packed, dst_absmax, stream);
+}
+
+int nsmlp_gather_down_columns_q8(const uint8_t* src_packed, const uint8_t* src_qabsmax, const int32_t* blocks, int n,
+                                 int out_features, int in_features, int qbs, int dst_layout, uint8_t* dst_packed,
+                                 uint8_t* dst_qabsmax, void* stream) {
+  return gather_down_impl<uint8_t>(src_packed, src_qabsmax, blocks, n, out_features, in_features, qbs, dst_layout,
+                                   dst_packed, dst_qabsmax, stream);
+}
+
+int nsmlp_absmax_dq_quantize(const float* absmax, long long n, int dq_block, const float* code2, float offset,
+                             uint8_t* q, float* absmax2, void* stream) {
+  if (n < 0 || dq_block <= 0 || dq_block > 4096 || (dq_block & (dq_block - 1)) != 0)
+    return set_error(NSMLP_EINVAL, "dq_block %d must be a power of two in [1, 4096]", dq_block);
   if (n == 0) return NSMLP_OK;
-  if (!src_packed || !src_absmax || !blocks || !dst_packed || !dst_absmax)
-    return set_error(NSMLP_EINVAL, "NULL tensor argument");
-  if (!aligned16(src_packed) || !aligned16(dst_packed)) return set_error(NSMLP_EINVAL, "packed must be 16-byte aligned");
-  launch_gather_down(src_packed, src_absmax, blocks, n, out_features, in_features, qbs, dst_layout, dst_packed,
-                     dst_absmax, (hipStream_t)stream);
-  return check_launch("gather down");
+  if (!absmax || !code2 || !q || !absmax2) return set_error(NSMLP_EINVAL, "NULL tensor argument");
+  launch_absmax_dq(absmax, n, dq_block, code2, offset, q, absmax2, (hipStream_t)stream);
+  return check_launch("absmax double quantisation");
+}
+
+int nsmlp_absmax_dq_dequantize(const uint8_t* q, long long n, int dq_block, const float* code2, const float* absmax2,
+                               float offset, float* out, void* stream) {
+  if (n < 0 || dq_block <= 0 || (dq_block & (dq_block - 1)) != 0)
+    return set_error(NSMLP_EINVAL, "dq_block %d must be a power of two", dq_block);
+  if (n == 0) return NSMLP_OK;
+  if (!q || !code2 || !absmax2 || !out) return set_error(NSMLP_EINVAL, "NULL tensor argument");
+  launch_absmax_undq(q, n, __builtin_ctz((unsigned)dq_block), code2, absmax2, offset, out, (hipStream_t)stream);
+  return check_launch("absmax double dequantisation");
 }
 
 int nsmlp_host_device_pointer(const void* host, void** device_ptr) {

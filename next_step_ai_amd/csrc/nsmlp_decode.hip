@@ -78,6 +78,8 @@ __device__ __forceinline__ void gate_up_task(const DecodeArgs& a, DecodeSmem& sm
   const uint8_t* ubase = (br.dev ? a.up.packed : a.host_up.packed) + br.q * a.up.blk_stride;
   const float* gabs = (br.dev ? a.gate.absmax : a.host_gate.absmax) + br.q * a.gate.abs_blk_stride;
   const float* uabs = (br.dev ? a.up.absmax : a.host_up.absmax) + br.q * a.up.abs_blk_stride;
+  const uint8_t* gq = (br.dev ? a.gate.qabsmax : a.host_gate.qabsmax) + br.q * a.gate.abs_blk_stride;
+  const uint8_t* uq = (br.dev ? a.up.qabsmax : a.host_up.qabsmax) + br.q * a.up.abs_blk_stride;
 
   const int cc = tid % LPR;
   const int r0 = tid / LPR;
@@ -98,7 +100,14 @@ __device__ __forceinline__ void gate_up_task(const DecodeArgs& a, DecodeSmem& sm
     am[i] = 0.0f;
     if (br.ok) {
       w[i] = *reinterpret_cast<const uint4*>(base + off + (uint32_t)(ri * kStep) * rs);
-      am[i] = abase[aoff + (uint32_t)(ri * kStep) * ars];
+      const uint32_t ai = aoff + (uint32_t)(ri * kStep) * ars;
+      if (a.dq) {
+        const ProjView& pv = i < NR / 2 ? a.gate : a.up;
+        const long long f = ((long long)br.b * 32 + r0 + ri * kStep) * ars + (col >> a.qbs_shift);
+        am[i] = dq_absmax(pv.code2[(i < NR / 2 ? gq : uq)[ai]], pv.absmax2[f >> a.dq_shift], pv.offset);
+      } else {
+        am[i] = abase[ai];
+      }
     }
   }
   uint32_t xp[16];
@@ -199,9 +208,15 @@ __device__ __forceinline__ void down_task(const DecodeArgs& a, DecodeSmem& sm, u
         const BlockRef br = resolve_block(a, j);
         const uint8_t* base = (br.dev ? a.down.packed : a.host_down.packed) + br.q * a.down.blk_stride;
         const float* abase = (br.dev ? a.down.absmax : a.host_down.absmax) + br.q * a.down.abs_blk_stride;
+        const uint8_t* qbase = (br.dev ? a.down.qabsmax : a.host_down.qabsmax) + br.q * a.down.abs_blk_stride;
         if (live && br.ok) {
           w[i] = *reinterpret_cast<const uint4*>(base + roff);
-          am[i] = abase[aroff];
+          if (a.dq) {
+            const long long f = (long long)o * ((long long)a.NB * 32 >> a.qbs_shift) + ((br.b * 32) >> a.qbs_shift);
+            am[i] = dq_absmax(a.down.code2[qbase[aroff]], a.down.absmax2[f >> a.dq_shift], a.down.offset);
+          } else {
+            am[i] = abase[aroff];
+          }
         }
       }
     }

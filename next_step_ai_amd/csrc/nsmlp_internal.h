@@ -350,26 +350,27 @@ __device__ __forceinline__ int wave_incl_scan(int v, int lane) {
 
 // Wave 0: the digit (from the top) holding the remaining-th largest entry.
 __device__ __forceinline__ void topk_find_digit(TopkLds& L, unsigned remaining, int lane) {
-  unsigned c[4];
-  unsigned local = 0;
-#pragma unroll
-  for (int b = 0; b < 4; ++b) {
-    c[b] = L.hist[255 - 4 * lane - b];
-    local += c[b];
-  }
+  // lane l holds digits 255 - 4l .. 252 - 4l (plain registers: no array, so
+  // nothing is placed in scratch memory)
+  const unsigned c0 = L.hist[255 - 4 * lane], c1 = L.hist[254 - 4 * lane];
+  const unsigned c2 = L.hist[253 - 4 * lane], c3 = L.hist[252 - 4 * lane];
+  const unsigned local = c0 + c1 + c2 + c3;
   const unsigned incl = (unsigned)wave_incl_scan((int)local, lane);
   const unsigned excl = incl - local;
   if (excl < remaining && remaining <= incl) {
-    unsigned cum = excl;
-#pragma unroll
-    for (int b = 0; b < 4; ++b) {
-      if (cum + c[b] >= remaining) {
-        L.digit = 255u - 4u * lane - b;
-        L.above = cum;
-        break;
-      }
-      cum += c[b];
+    unsigned b = 3, cum = excl + c0 + c1 + c2;
+    if (excl + c0 >= remaining) {
+      b = 0;
+      cum = excl;
+    } else if (excl + c0 + c1 >= remaining) {
+      b = 1;
+      cum = excl + c0;
+    } else if (excl + c0 + c1 + c2 >= remaining) {
+      b = 2;
+      cum = excl + c0 + c1;
     }
+    L.digit = 255u - 4u * lane - b;
+    L.above = cum;
   }
 }
 
@@ -416,18 +417,12 @@ __device__ __forceinline__ void topk_threshold(const uint32_t (&key)[KPT], int i
   eq = (unsigned)before & 0xFFFFu;
 }
 
-// Position of key m in ascending block order among the selected, or -1.
-__device__ __forceinline__ int topk_position(uint32_t key, uint32_t T, unsigned need, unsigned& gt, unsigned& eq) {
-  if (key > T) {
-    const int pos = (int)(gt + (eq < need ? eq : need));
-    ++gt;
-    return pos;
-  }
-  if (key == T) {
-    const int pos = eq < need ? (int)(gt + eq) : -1;
-    ++eq;
-    return pos;
-  }
+// Position of a key in ascending block order among the selected, or -1; gt /
+// eq count the keys above / equal to T before it.  The caller advances them
+// (gt += key > T, eq += key == T): plain values, so nothing goes to scratch.
+__device__ __forceinline__ int topk_position(uint32_t key, uint32_t T, unsigned need, unsigned gt, unsigned eq) {
+  if (key > T) return (int)(gt + (eq < need ? eq : need));
+  if (key == T && eq < need) return (int)(gt + eq);
   return -1;
 }
 
@@ -441,7 +436,21 @@ struct ProjView {
   long long row_stride;      // bytes between consecutive rows inside a slot
   long long abs_blk_stride;  // absmax entries between consecutive slots
   long long abs_row_stride;  // absmax entries between consecutive rows
+  // double-quantised absmax (DecodeArgs::dq): u8 codes at the absmax
+  // positions, second-level scales of the full weight, code book, offset
+  const uint8_t* qabsmax;
+  const float* absmax2;
+  const float* code2;
+  float offset;
 };
+
+// Double-quantised absmax value: fp32(fp32(code2[q] * absmax2) + offset),
+// both roundings kept (no fused multiply-add), as the reference resolves it
+// (dequantize_blockwise, then + offset; RT:4621-4625).
+__device__ __forceinline__ float dq_absmax(float code2_q, float absmax2, float offset) {
+#pragma clang fp contract(off)
+  return code2_q * absmax2 + offset;
+}
 
 struct DecodeArgs {
   const uint16_t* x;    // [H] fp16
@@ -494,6 +503,14 @@ struct DecodeArgs {
   // to sel_out; sel is then unused
   const uint16_t* sel_scores;  // [NB]
   int32_t* sel_out;            // [k]
+  // double-quantised absmax: absmax of flat index f (in the full weight:
+  // gate/up (32 b + r) * (H / qbs) + c / qbs, down o * (I / qbs) + 32 b / qbs)
+  // uses absmax2[f >> dq_shift]
+  int dq;
+  int dq_shift;
+  int32_t* st_bid;       // [k] block ids of the selected positions (streaming)
+  int st_gu_a2bytes;     // extent of gate/up absmax2 (bytes)
+  int st_dn_a2n;         // down absmax2 entries staged per 64-row chunk
 };
 
 // Resolve selected position j to (storage view index, validity):
@@ -581,10 +598,16 @@ void launch_output_linear(const LinearArgs& a, hipStream_t s);
 void launch_input_linear(const LinearArgs& a, hipStream_t s);
 void launch_zero_u32(uint32_t* p, long long n, hipStream_t s);
 void launch_silu_mul(const uint16_t* g, const uint16_t* u, uint16_t* out, long long n, hipStream_t s);
-void launch_gather_rows(const uint8_t* src, const float* src_abs, const int32_t* blocks, int src_blocks, int n,
-                        long long bpb, long long apb, uint8_t* dst, float* dst_abs, hipStream_t s);
-void launch_gather_down(const uint8_t* src, const float* src_abs, const int32_t* blocks, int n, int out_f, int in_f,
-                        int qbs, int layout, uint8_t* dst, float* dst_abs, hipStream_t s);
+template <typename AbsT>  // float or uint8_t (double-quantised codes)
+void launch_gather_rows(const uint8_t* src, const AbsT* src_abs, const int32_t* blocks, int src_blocks, int n,
+                        long long bpb, long long apb, uint8_t* dst, AbsT* dst_abs, hipStream_t s);
+template <typename AbsT>
+void launch_gather_down(const uint8_t* src, const AbsT* src_abs, const int32_t* blocks, int n, int out_f, int in_f,
+                        int qbs, int layout, uint8_t* dst, AbsT* dst_abs, hipStream_t s);
+void launch_absmax_dq(const float* absmax, long long n, int dq_block, const float* code2, float offset, uint8_t* q,
+                      float* absmax2, hipStream_t s);
+void launch_absmax_undq(const uint8_t* q, long long n, int dq_shift, const float* code2, const float* absmax2,
+                        float offset, float* out, hipStream_t s);
 void set_nf4_midpoints(const float* mid15);
 void launch_nf4_quant(const float* w, uint64_t seed, float std, long long n, int qbs, bool synth, uint8_t* packed,
                       float* absmax, hipStream_t s);

@@ -137,8 +137,9 @@ __global__ void k_silu_mul(const uint16_t* g, const uint16_t* u, uint16_t* out, 
 }
 
 // ----------------------------------------------------------------- gathers
-__global__ void k_gather_rows(const uint8_t* src, const float* src_abs, const int32_t* blocks, int src_blocks,
-                              long long bpb, long long apb, uint8_t* dst, float* dst_abs) {
+template <typename AbsT>
+__global__ void k_gather_rows(const uint8_t* src, const AbsT* src_abs, const int32_t* blocks, int src_blocks,
+                              long long bpb, long long apb, uint8_t* dst, AbsT* dst_abs) {
   const int i = blockIdx.y;
   const long long b = blocks[i];
   if (b < 0 || b >= src_blocks) return;  // out-of-range id: the destination block is left untouched
@@ -149,8 +150,9 @@ __global__ void k_gather_rows(const uint8_t* src, const float* src_abs, const in
     dst_abs[i * apb + v] = src_abs[b * apb + v];
 }
 
-__global__ void k_gather_down(const uint8_t* src, const float* src_abs, const int32_t* blocks, int n, int out_f,
-                              int in_f, int qbs, int layout, uint8_t* dst, float* dst_abs) {
+template <typename AbsT>
+__global__ void k_gather_down(const uint8_t* src, const AbsT* src_abs, const int32_t* blocks, int n, int out_f,
+                              int in_f, int qbs, int layout, uint8_t* dst, AbsT* dst_abs) {
   const long long idx = (long long)blockIdx.x * kThreads + threadIdx.x;  // o * n + i
   if (idx >= (long long)out_f * n) return;
   const long long o = idx / n;
@@ -158,10 +160,65 @@ __global__ void k_gather_down(const uint8_t* src, const float* src_abs, const in
   const long long b = blocks[i];
   if (b < 0 || b >= in_f / 32) return;  // out-of-range id: the destination is left untouched
   const uint4 v = *reinterpret_cast<const uint4*>(src + o * (in_f / 2) + b * 16);
-  const float am = src_abs[o * (in_f / qbs) + (b * 32) / qbs];
+  const AbsT am = src_abs[o * (in_f / qbs) + (b * 32) / qbs];
   const long long d = layout == NSMLP_DOWN_BLOCK_MAJOR ? i * out_f + o : o * n + i;
   reinterpret_cast<uint4*>(dst)[d] = v;
   dst_abs[d] = am;
+}
+
+// ------------------------------------------------------- double-quantised absmax
+// One workgroup of kDqThreads per block of dq_block absmax (dq_block a power
+// of two in [1, 4096]; each thread handles dq_block / kDqThreads entries or
+// one).  The same fp32 operations as the restated bitsandbytes quantiser:
+// a = absmax - offset, absmax2 = max |a|, v = a * fp32(1 / absmax2), nearest
+// code2 entry (ties: lower index).
+constexpr int kDqThreads = 256;
+
+__device__ __forceinline__ uint32_t nearest_code2(const float* c2, float v) {
+  // c2 ascending: lo = number of entries < v; the nearest is lo - 1 or lo,
+  // then the lowest index of equal computed distance
+  int lo = 0, hi = 256;
+  while (lo < hi) {
+    const int mid = (lo + hi) >> 1;
+    if (c2[mid] < v) lo = mid + 1; else hi = mid;
+  }
+  int best;
+  if (lo == 256) best = 255;
+  else if (lo == 0) best = 0;
+  else best = fabsf(c2[lo - 1] - v) <= fabsf(c2[lo] - v) ? lo - 1 : lo;
+  const float d = fabsf(c2[best] - v);
+  while (best > 0 && fabsf(c2[best - 1] - v) == d) --best;
+  return (uint32_t)best;
+}
+
+__global__ void __launch_bounds__(kDqThreads) k_absmax_dq(const float* absmax, long long n, int dq_block,
+                                                          const float* code2, float offset, uint8_t* q,
+                                                          float* absmax2) {
+  __shared__ float c2[256];
+  __shared__ float wmax[kDqThreads / kWave];
+  const int tid = threadIdx.x;
+  c2[tid] = code2[tid];
+  const long long lo = (long long)blockIdx.x * dq_block;
+  const long long hi = lo + dq_block < n ? lo + dq_block : n;
+  float m = 0.0f;
+  for (long long i = lo + tid; i < hi; i += kDqThreads) m = fmaxf(m, fabsf(__fsub_rn(absmax[i], offset)));
+#pragma unroll
+  for (int d = kWave / 2; d >= 1; d >>= 1) m = fmaxf(m, __shfl_xor(m, d, kWave));
+  if ((tid & (kWave - 1)) == 0) wmax[tid / kWave] = m;
+  __syncthreads();
+  float amax = 0.0f;
+#pragma unroll
+  for (int w = 0; w < kDqThreads / kWave; ++w) amax = fmaxf(amax, wmax[w]);
+  const float inv = amax > 0.0f ? __frcp_rn(amax) : 0.0f;
+  if (tid == 0) absmax2[blockIdx.x] = amax;
+  for (long long i = lo + tid; i < hi; i += kDqThreads)
+    q[i] = (uint8_t)nearest_code2(c2, __fmul_rn(__fsub_rn(absmax[i], offset), inv));
+}
+
+__global__ void k_absmax_undq(const uint8_t* q, long long n, int dq_shift, const float* code2, const float* absmax2,
+                              float offset, float* out) {
+  const long long i = (long long)blockIdx.x * kThreads + threadIdx.x;
+  if (i < n) out[i] = dq_absmax(code2[q[i]], absmax2[i >> dq_shift], offset);
 }
 
 // ---------------------------------------------------------------- synthetic
@@ -253,19 +310,39 @@ void launch_silu_mul(const uint16_t* g, const uint16_t* u, uint16_t* out, long l
   hipLaunchKernelGGL(k_silu_mul, dim3(grid_for(n)), dim3(kThreads), 0, s, g, u, out, n);
 }
 
-void launch_gather_rows(const uint8_t* src, const float* src_abs, const int32_t* blocks, int src_blocks, int n,
-                        long long bpb, long long apb, uint8_t* dst, float* dst_abs, hipStream_t s) {
+template <typename AbsT>
+void launch_gather_rows(const uint8_t* src, const AbsT* src_abs, const int32_t* blocks, int src_blocks, int n,
+                        long long bpb, long long apb, uint8_t* dst, AbsT* dst_abs, hipStream_t s) {
   long long per = (bpb / 16 > apb ? bpb / 16 : apb);
   unsigned gx = (unsigned)((per + kThreads - 1) / kThreads);
   if (gx > 64) gx = 64;
-  hipLaunchKernelGGL(k_gather_rows, dim3(gx, n), dim3(kThreads), 0, s, src, src_abs, blocks, src_blocks, bpb, apb, dst,
-                     dst_abs);
+  k_gather_rows<AbsT><<<dim3(gx, n), dim3(kThreads), 0, s>>>(src, src_abs, blocks, src_blocks, bpb, apb, dst, dst_abs);
+}
+template void launch_gather_rows<float>(const uint8_t*, const float*, const int32_t*, int, int, long long, long long,
+                                        uint8_t*, float*, hipStream_t);
+template void launch_gather_rows<uint8_t>(const uint8_t*, const uint8_t*, const int32_t*, int, int, long long,
+                                          long long, uint8_t*, uint8_t*, hipStream_t);
+
+template <typename AbsT>
+void launch_gather_down(const uint8_t* src, const AbsT* src_abs, const int32_t* blocks, int n, int out_f, int in_f,
+                        int qbs, int layout, uint8_t* dst, AbsT* dst_abs, hipStream_t s) {
+  k_gather_down<AbsT><<<dim3(grid_for((long long)out_f * n)), dim3(kThreads), 0, s>>>(src, src_abs, blocks, n, out_f,
+                                                                                      in_f, qbs, layout, dst, dst_abs);
+}
+template void launch_gather_down<float>(const uint8_t*, const float*, const int32_t*, int, int, int, int, int,
+                                        uint8_t*, float*, hipStream_t);
+template void launch_gather_down<uint8_t>(const uint8_t*, const uint8_t*, const int32_t*, int, int, int, int, int,
+                                          uint8_t*, uint8_t*, hipStream_t);
+
+void launch_absmax_dq(const float* absmax, long long n, int dq_block, const float* code2, float offset, uint8_t* q,
+                      float* absmax2, hipStream_t s) {
+  const long long nb = (n + dq_block - 1) / dq_block;
+  k_absmax_dq<<<dim3((unsigned)nb), dim3(kDqThreads), 0, s>>>(absmax, n, dq_block, code2, offset, q, absmax2);
 }
 
-void launch_gather_down(const uint8_t* src, const float* src_abs, const int32_t* blocks, int n, int out_f, int in_f,
-                        int qbs, int layout, uint8_t* dst, float* dst_abs, hipStream_t s) {
-  hipLaunchKernelGGL(k_gather_down, dim3(grid_for((long long)out_f * n)), dim3(kThreads), 0, s, src, src_abs, blocks,
-                     n, out_f, in_f, qbs, layout, dst, dst_abs);
+void launch_absmax_undq(const uint8_t* q, long long n, int dq_shift, const float* code2, const float* absmax2,
+                        float offset, float* out, hipStream_t s) {
+  k_absmax_undq<<<dim3(grid_for(n)), dim3(kThreads), 0, s>>>(q, n, dq_shift, code2, absmax2, offset, out);
 }
 
 void set_nf4_midpoints(const float* mid15) {

@@ -161,6 +161,8 @@ __global__ void __launch_bounds__(kSelThreads) k_select(RouteArgs a) {
     const int i = i0 + m;
     if (i >= NB) continue;
     const int pos = topk_position(key[m], T, need, gt, eq);
+    gt += key[m] > T;
+    eq += key[m] == T;
     if (pos < 0 || pos >= k) continue;
     if (!a.sorted)
       out[pos] = i;

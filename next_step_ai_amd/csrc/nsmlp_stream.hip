@@ -51,16 +51,23 @@ constexpr int kDnStages = 2;
 constexpr int kMaxItems = 64;      // items per wave resolved up front (one per lane)
 constexpr int kMaxDnBlocks = 512;  // blocks per down workgroup (activations in LDS)
 constexpr int kLutWords = kRepLutBytes / 4;
-// dynamic LDS: table, split sums [2][8][4]; with the in-kernel top-k also the
-// selection state and the selected ids [k]
-constexpr size_t kGuLds = kRepLutBytes + 2 * kWaves * 4 * sizeof(float);
-constexpr int kGuTopkWord = (int)(kGuLds / 4);
+// dynamic LDS: table, split sums [2][8][4]; with double-quantised absmax the
+// gate and up second-level code books [2][256]; with the in-kernel top-k also
+// the selection state and the selected ids [k]
+constexpr int kGuCode2Word = kLutWords + 2 * kWaves * 4;
+constexpr size_t kGuLds = (size_t)kGuCode2Word * 4;
+constexpr size_t kGuDqLds = kGuLds + 2 * 256 * sizeof(float);
+constexpr int kGuTopkWord = (int)(kGuDqLds / 4);
 constexpr int kGuSelWord = kGuTopkWord + (int)((sizeof(TopkLds) + 15) / 16 * 4);
 constexpr int kSelMaxNB = 4096;  // 8 scores per thread
 constexpr int kSelMaxK = 2048;
 constexpr size_t kGuSelLds = (size_t)kGuSelWord * 4 + kSelMaxK * sizeof(int32_t);
-// dynamic LDS: table, activation pairs [512][16], scales [512], wave sums [8][64]
+// dynamic LDS: table, activation pairs [512][16], scales [512], wave sums
+// [8][64]; with double-quantised absmax also the down code book [256] and the
+// absmax2 entries of the workgroup's 64 rows [kDnA2Max]
 constexpr size_t kDnLds = kRepLutBytes + kMaxDnBlocks * 16 * 4 + kMaxDnBlocks * 4 + kWaves * kWave * 4;
+constexpr int kDnA2Max = 1024;
+constexpr size_t kDnDqLds = kDnLds + (256 + kDnA2Max) * sizeof(float);
 
 // Encoded block reference: < 2^30 -> HBM slot; bit 30 -> host copy of the
 // block id in the low bits; bit 31 -> invalid (zero contribution).
@@ -103,6 +110,9 @@ __device__ __forceinline__ uint4 buf_ld16(rsrc_t r, uint32_t voff, uint32_t soff
 __device__ __forceinline__ float buf_ldf(rsrc_t r, uint32_t voff, uint32_t soff) {
   return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, (int)voff, (int)soff, kNontemporal));
 }
+__device__ __forceinline__ uint32_t buf_ldu8(rsrc_t r, uint32_t voff, uint32_t soff) {
+  return (uint32_t)__builtin_amdgcn_raw_buffer_load_b8(r, (int)voff, (int)soff, kNontemporal);
+}
 
 // Replicated pair table, filled by 512 threads in 8 passes of one 16-byte LDS
 // write each: pass ps writes entry e = 32 ps + tid / 16, copies 4 (tid % 16)
@@ -132,32 +142,66 @@ __device__ __forceinline__ void lut_store(uint32_t* lut, const LutCodes& c, int 
 }
 
 struct GuStage {
-  uint4 w[4];  // gate 2p, gate 2p+1, up 2p, up 2p+1: this lane's 32 columns
-  float am[4];
+  uint4 w[4];    // gate 2p, gate 2p+1, up 2p, up 2p+1: this lane's 32 columns
+  float am[4];   // absmax, or (double-quantised) the absmax2 of the row
+  uint32_t qa[4];  // double-quantised: the u8 absmax code
 };
 
-// Issue the loads of one item (block reference enc, row pair p).  cb / ca4:
-// this lane's byte offsets of its columns inside a row of packed / absmax.
-__device__ __forceinline__ void gu_issue(const DecodeArgs& a, uint32_t enc, int p, uint32_t cb, uint32_t ca4,
-                                         GuStage& st) {
+// Issue the loads of one item (block reference enc, block id bid, row pair
+// p).  ca: this lane's absmax entry inside a row (its columns / qbs); cb:
+// its byte offset inside a packed row.
+template <bool DQ>
+__device__ __forceinline__ void gu_issue(const DecodeArgs& a, uint32_t enc, uint32_t bid, int p, uint32_t cb,
+                                         uint32_t ca, GuStage& st) {
   const bool bad = (enc & kBad) != 0;
   const bool dev = (enc & kHostBit) == 0;
   const long long q = bad ? 0 : (long long)(enc & (kHostBit - 1));
   const int nb = bad ? 0 : a.st_gu_bytes, na = bad ? 0 : a.st_gu_abytes;
   const rsrc_t rg = make_rsrc((dev ? a.gate.packed : a.host_gate.packed) + q * a.gate.blk_stride, nb);
   const rsrc_t ru = make_rsrc((dev ? a.up.packed : a.host_up.packed) + q * a.up.blk_stride, nb);
-  const rsrc_t rga = make_rsrc((dev ? a.gate.absmax : a.host_gate.absmax) + q * a.gate.abs_blk_stride, na);
-  const rsrc_t rua = make_rsrc((dev ? a.up.absmax : a.host_up.absmax) + q * a.up.abs_blk_stride, na);
-  const uint32_t rs = (uint32_t)a.gate.row_stride, ars4 = (uint32_t)a.gate.abs_row_stride * 4u;
-  const uint32_t s0 = (uint32_t)(2 * p) * rs, as0 = (uint32_t)(2 * p) * ars4;
+  const uint32_t rs = (uint32_t)a.gate.row_stride, ars = (uint32_t)a.gate.abs_row_stride;
+  const uint32_t s0 = (uint32_t)(2 * p) * rs;
   st.w[0] = buf_ld16(rg, cb, s0);
   st.w[1] = buf_ld16(rg, cb, s0 + rs);
   st.w[2] = buf_ld16(ru, cb, s0);
   st.w[3] = buf_ld16(ru, cb, s0 + rs);
-  st.am[0] = buf_ldf(rga, ca4, as0);
-  st.am[1] = buf_ldf(rga, ca4, as0 + ars4);
-  st.am[2] = buf_ldf(rua, ca4, as0);
-  st.am[3] = buf_ldf(rua, ca4, as0 + ars4);
+  if constexpr (DQ) {
+    const rsrc_t rgq = make_rsrc((dev ? a.gate.qabsmax : a.host_gate.qabsmax) + q * a.gate.abs_blk_stride, na);
+    const rsrc_t ruq = make_rsrc((dev ? a.up.qabsmax : a.host_up.qabsmax) + q * a.up.abs_blk_stride, na);
+    const uint32_t as0 = (uint32_t)(2 * p) * ars;
+    st.qa[0] = buf_ldu8(rgq, ca, as0);
+    st.qa[1] = buf_ldu8(rgq, ca, as0 + ars);
+    st.qa[2] = buf_ldu8(ruq, ca, as0);
+    st.qa[3] = buf_ldu8(ruq, ca, as0 + ars);
+    // absmax2 of rows 32 bid + 2p (+1) at this lane's columns (one value per
+    // wave: a 2048-column split never straddles a second-level block)
+    const int n2 = bad ? 0 : a.st_gu_a2bytes;
+    const rsrc_t rg2 = make_rsrc(a.gate.absmax2, n2);
+    const rsrc_t ru2 = make_rsrc(a.up.absmax2, n2);
+    const uint32_t f0 = (32u * bid + 2u * (uint32_t)p) * ars + ca;
+    const uint32_t o0 = (f0 >> a.dq_shift) * 4u, o1 = ((f0 + ars) >> a.dq_shift) * 4u;
+    st.am[0] = buf_ldf(rg2, o0, 0);
+    st.am[1] = buf_ldf(rg2, o1, 0);
+    st.am[2] = buf_ldf(ru2, o0, 0);
+    st.am[3] = buf_ldf(ru2, o1, 0);
+  } else {
+    const rsrc_t rga = make_rsrc((dev ? a.gate.absmax : a.host_gate.absmax) + q * a.gate.abs_blk_stride, na);
+    const rsrc_t rua = make_rsrc((dev ? a.up.absmax : a.host_up.absmax) + q * a.up.abs_blk_stride, na);
+    const uint32_t ars4 = ars * 4u, as0 = (uint32_t)(2 * p) * ars4, ca4 = ca * 4u;
+    st.am[0] = buf_ldf(rga, ca4, as0);
+    st.am[1] = buf_ldf(rga, ca4, as0 + ars4);
+    st.am[2] = buf_ldf(rua, ca4, as0);
+    st.am[3] = buf_ldf(rua, ca4, as0 + ars4);
+  }
+}
+
+// The absmax of row i of a gate/up stage.
+template <bool DQ>
+__device__ __forceinline__ float gu_absmax(const DecodeArgs& a, const GuStage& st, const float* c2, int i) {
+  if constexpr (DQ)
+    return dq_absmax(c2[(i >= 2 ? 256 : 0) + st.qa[i]], st.am[i], i >= 2 ? a.up.offset : a.gate.offset);
+  else
+    return st.am[i];
 }
 
 // Reduce-scatter of 4 per-lane row sums over the 64 lanes: afterwards every
@@ -181,7 +225,7 @@ __device__ __forceinline__ float reduce4(const float (&v)[4], int lane) {
 // SKPT > 0: the workgroup first selects the top k of a.sel_scores itself (SKPT
 // scores per thread; ascending ids, ties to the lower id), so the selection
 // needs no launch of its own; workgroup 0 also writes the ids to a.sel_out.
-template <bool AFFINE, int SKPT>
+template <bool AFFINE, int SKPT, bool DQ>
 __global__ void __launch_bounds__(kThreads8, 2) k_gu_rep(DecodeArgs a) {
   extern __shared__ __attribute__((aligned(16))) uint32_t lds[];
   float* comb = reinterpret_cast<float*>(lds + kLutWords);
@@ -194,7 +238,8 @@ __global__ void __launch_bounds__(kThreads8, 2) k_gu_rep(DecodeArgs a) {
   const int nwg = (int)gridDim.x, wg = (int)blockIdx.x;
   const int n_items = 16 * a.k;
   const uint32_t col = (uint32_t)(s * kSplit + lane * 32);
-  const uint32_t cb = col >> 1, ca4 = (col >> a.qbs_shift) * 4u;
+  const uint32_t cb = col >> 1, ca = col >> a.qbs_shift;
+  const float* c2 = reinterpret_cast<const float*>(lds + kGuCode2Word);
 
   // Independent loads first: the block id of each lane's item (lane i:
   // round i), the code book and the token split.
@@ -216,6 +261,8 @@ __global__ void __launch_bounds__(kThreads8, 2) k_gu_rep(DecodeArgs a) {
   }
   LutCodes codes;
   lut_codes_load(a.code, a.code_up, tid, codes);
+  float c2v = 0.0f;
+  if constexpr (DQ) c2v = (tid < 256 ? a.gate.code2 : a.up.code2)[tid & 255];
   uint32_t xp[16];
   {
     const uint4* xv = reinterpret_cast<const uint4*>(a.x + col);
@@ -230,6 +277,7 @@ __global__ void __launch_bounds__(kThreads8, 2) k_gu_rep(DecodeArgs a) {
   }
   sched_fence();
   lut_store(lds, codes, tid);
+  if constexpr (DQ) lds[kGuCode2Word + tid] = __float_as_uint(c2v);
   int32_t* sel_l = reinterpret_cast<int32_t*>(lds + kGuSelWord);
   if constexpr (SKPT > 0) {
     TopkLds& tl = *reinterpret_cast<TopkLds*>(lds + kGuTopkWord);
@@ -241,6 +289,8 @@ __global__ void __launch_bounds__(kThreads8, 2) k_gu_rep(DecodeArgs a) {
     for (int m = 0; m < SKPT; ++m) {
       if (i0 + m >= a.NB) continue;
       const int pos = topk_position(skey[m], T, need, gt, eq);
+      gt += skey[m] > T;
+      eq += skey[m] == T;
       if (pos < 0 || pos >= a.k) continue;
       sel_l[pos] = i0 + m;
       if (sel_out != nullptr) sel_out[pos] = i0 + m;
@@ -250,23 +300,28 @@ __global__ void __launch_bounds__(kThreads8, 2) k_gu_rep(DecodeArgs a) {
   }
   // Block references (slot lookup).  Split 0 of row pair 0 reports an
   // invalid block and publishes the reference for the down kernel.
-  uint32_t enc_v = kBad;
+  // enc_v / bid_v: lane i holds item i's block reference and block id (0
+  // for an invalid block, so that index arithmetic on it stays in range)
+  uint32_t enc_v = kBad, bid_v = 0;
   if (own) {
     const BlockRef br = resolve_id(a, b_id);
     enc_v = encode_ref(br);
+    bid_v = br.ok ? (uint32_t)b_id : 0u;
     if (s == 0 && (id0 & 15) == 0) {
       if (!br.ok && !br.silent) atomicOr(a.status, 1);
       a.st_enc[id0 >> 4] = enc_v;
+      a.st_bid[id0 >> 4] = (int32_t)bid_v;
     }
   }
   // Stage 0 of every wave goes out before any later stage; the barrier also
   // publishes the code table.
   GuStage st[kGuStages];
-  gu_issue(a, R > 0 ? lane_value(enc_v, 0) : kBad, (wg * NS + q) & 15, cb, ca4, st[0]);
+  gu_issue<DQ>(a, R > 0 ? lane_value(enc_v, 0) : kBad, lane_value(bid_v, 0), (wg * NS + q) & 15, cb, ca, st[0]);
   lds_barrier();
 #pragma unroll
   for (int i = 1; i < kGuStages; ++i)
-    gu_issue(a, i < R ? lane_value(enc_v, i) : kBad, ((i * nwg + wg) * NS + q) & 15, cb, ca4, st[i]);
+    gu_issue<DQ>(a, i < R ? lane_value(enc_v, i) : kBad, lane_value(bid_v, i < R ? i : 0),
+                 ((i * nwg + wg) * NS + q) & 15, cb, ca, st[i]);
   sched_fence();
 
   uint32_t adg[4], adu[4];
@@ -283,14 +338,15 @@ __global__ void __launch_bounds__(kThreads8, 2) k_gu_rep(DecodeArgs a) {
       const bool live = r < R;  // uniform over the workgroup
       float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
       if (live) {
-        acc[0] = rep_dot32(st[i].w[0], xp, adg) * st[i].am[0];
-        acc[1] = rep_dot32(st[i].w[1], xp, adg) * st[i].am[1];
-        acc[2] = rep_dot32(st[i].w[2], xp, adu) * st[i].am[2];
-        acc[3] = rep_dot32(st[i].w[3], xp, adu) * st[i].am[3];
+        acc[0] = rep_dot32(st[i].w[0], xp, adg) * gu_absmax<DQ>(a, st[i], c2, 0);
+        acc[1] = rep_dot32(st[i].w[1], xp, adg) * gu_absmax<DQ>(a, st[i], c2, 1);
+        acc[2] = rep_dot32(st[i].w[2], xp, adu) * gu_absmax<DQ>(a, st[i], c2, 2);
+        acc[3] = rep_dot32(st[i].w[3], xp, adu) * gu_absmax<DQ>(a, st[i], c2, 3);
       }
       const int rn = r + kGuStages;
-      gu_issue(a, rn < R ? lane_value(enc_v, rn < kMaxItems ? rn : 0) : kBad, ((rn * nwg + wg) * NS + q) & 15, cb,
-               ca4, st[i]);
+      const int rl = rn < R && rn < kMaxItems ? rn : 0;
+      gu_issue<DQ>(a, rn < R ? lane_value(enc_v, rl) : kBad, lane_value(bid_v, rl), ((rn * nwg + wg) * NS + q) & 15,
+                   cb, ca, st[i]);
       if (live) {
         const float v = reduce4(acc, lane);
         if ((lane & 15) == 0) comb[(r & 1) * (kWaves * 4) + wave * 4 + (lane >> 4)] = v;
@@ -329,27 +385,39 @@ __global__ void __launch_bounds__(kThreads8, 2) k_gu_rep(DecodeArgs a) {
 
 struct DnStage {
   uint4 w[2];
-  float am[2];
+  float am[2];     // absmax (fp32 absmax storage)
+  uint32_t qa[2];  // u8 absmax code (double-quantised storage)
 };
 
-__device__ __forceinline__ void dn_issue(const DecodeArgs& a, uint32_t enc, uint32_t roff, uint32_t aroff4, uint4& w,
-                                         float& am) {
+// aoff: this lane's absmax entry in a block (its row o).
+template <bool DQ>
+__device__ __forceinline__ void dn_issue(const DecodeArgs& a, uint32_t enc, uint32_t roff, uint32_t aoff, uint4& w,
+                                         float& am, uint32_t& qa) {
   const bool bad = (enc & kBad) != 0;
   const bool dev = (enc & kHostBit) == 0;
   const long long q = bad ? 0 : (long long)(enc & (kHostBit - 1));
   const rsrc_t rp = make_rsrc((dev ? a.down.packed : a.host_down.packed) + q * a.down.blk_stride,
                               bad ? 0 : a.st_dn_bytes);
-  const rsrc_t ra = make_rsrc((dev ? a.down.absmax : a.host_down.absmax) + q * a.down.abs_blk_stride,
-                              bad ? 0 : a.st_dn_abytes);
   w = buf_ld16(rp, roff, 0);
-  am = buf_ldf(ra, aroff4, 0);
+  if constexpr (DQ) {
+    const rsrc_t ra = make_rsrc((dev ? a.down.qabsmax : a.host_down.qabsmax) + q * a.down.abs_blk_stride,
+                                bad ? 0 : a.st_dn_abytes);
+    qa = buf_ldu8(ra, aoff, 0);
+  } else {
+    const rsrc_t ra = make_rsrc((dev ? a.down.absmax : a.host_down.absmax) + q * a.down.abs_blk_stride,
+                                bad ? 0 : a.st_dn_abytes);
+    am = buf_ldf(ra, aoff * 4u, 0);
+  }
 }
 
+template <bool DQ>
 __global__ void __launch_bounds__(kThreads8, 2) k_down_rep(DecodeArgs a) {
   extern __shared__ __attribute__((aligned(16))) uint32_t lds[];
   uint32_t* actp = lds + kLutWords;                                    // [512][16] fp16 pairs
   float* ascale = reinterpret_cast<float*>(actp + kMaxDnBlocks * 16);  // [512]
   float* wsum = ascale + kMaxDnBlocks;                                 // [8][64]
+  float* c2 = wsum + kWaves * kWave;                                   // [256] (DQ)
+  float* a2 = c2 + 256;                                                // [kDnA2Max] (DQ)
   const int tid = threadIdx.x, lane = tid & (kWave - 1);
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int GX = a.st_dn_gx, per = a.st_dn_per;
@@ -362,7 +430,12 @@ __global__ void __launch_bounds__(kThreads8, 2) k_down_rep(DecodeArgs a) {
   const int T = (nbv + 1) >> 1;  // 2-block items (uniform per wave)
   const uint32_t o = (uint32_t)(c * kWave + lane);
   const uint32_t roff = o * (uint32_t)a.down.row_stride;
-  const uint32_t aroff4 = o * (uint32_t)a.down.abs_row_stride * 4u;
+  const uint32_t aoff = o * (uint32_t)a.down.abs_row_stride;
+  // double-quantised: absmax of (row o, block b) has flat index o * Ad +
+  // 32 b / qbs; the workgroup stages the absmax2 entries of its 64 rows,
+  // from g_lo on
+  const uint32_t Ad = (uint32_t)(a.NB * 32) >> a.qbs_shift;
+  const uint32_t g_lo = (uint32_t)(c * kWave) * Ad >> a.dq_shift;
 
   // Independent loads first: code book, block references, and (thread t <
   // nbw) the 32 activations of the workgroup's block t.  They are
@@ -370,9 +443,21 @@ __global__ void __launch_bounds__(kThreads8, 2) k_down_rep(DecodeArgs a) {
   // would be waited for on its own.
   const uint32_t* encs = a.st_enc + jb0;
   uint32_t enc_v = encs[lane < nbv ? jw0 + lane : 0];
+  uint32_t bid_v = 0;
+  if constexpr (DQ) bid_v = (uint32_t)a.st_bid[jb0 + (lane < nbv ? jw0 + lane : 0)];
   sched_fence();
   LutCodes codes;
   lut_codes_load(a.code_down, a.code_down, tid, codes);
+  float c2v = 0.0f, a2v[2] = {0.0f, 0.0f};
+  if constexpr (DQ) {
+    c2v = a.down.code2[tid & 255];
+    const uint32_t last = (uint32_t)((((long long)a.H * Ad) - 1) >> a.dq_shift);
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const uint32_t g = min(g_lo + (uint32_t)(tid + h * kThreads8), last);  // clamped: unconditional load
+      a2v[h] = a.down.absmax2[g];
+    }
+  }
   const bool own = tid < nbw;
   uint32_t my_enc = encs[own ? tid : 0];
   if (!own) my_enc = kBad;
@@ -388,12 +473,17 @@ __global__ void __launch_bounds__(kThreads8, 2) k_down_rep(DecodeArgs a) {
 #pragma unroll
   for (int i = 0; i < kDnStages; ++i) {
     const bool in = i < T;
-    dn_issue(a, in ? lane_value(enc_v, 2 * i) : kBad, roff, aroff4, st[i].w[0], st[i].am[0]);
-    dn_issue(a, in ? lane_value(enc_v, 2 * i + 1) : kBad, roff, aroff4, st[i].w[1], st[i].am[1]);
+    dn_issue<DQ>(a, in ? lane_value(enc_v, 2 * i) : kBad, roff, aoff, st[i].w[0], st[i].am[0], st[i].qa[0]);
+    dn_issue<DQ>(a, in ? lane_value(enc_v, 2 * i + 1) : kBad, roff, aoff, st[i].w[1], st[i].am[1], st[i].qa[1]);
   }
   sched_fence();
 
   lut_store(lds, codes, tid);
+  if constexpr (DQ) {
+    if (tid < 256) c2[tid] = c2v;
+    a2[tid] = a2v[0];
+    if (tid + kThreads8 < kDnA2Max) a2[tid + kThreads8] = a2v[1];
+  }
   // block tid's activations as fp16 pairs scaled by a power of two (max |act|
   // in [0.5, 1)); invalid blocks and blocks past the group's end are zero
   {
@@ -433,13 +523,26 @@ __global__ void __launch_bounds__(kThreads8, 2) k_down_rep(DecodeArgs a) {
       const int t = t0 + i;
       if (t < T) {
         const int jj = 2 * t;
-        acc += rep_dot32(st[i].w[0], wact + jj * 16, ad) * (st[i].am[0] * wscale[jj]);
-        acc += rep_dot32(st[i].w[1], wact + jj * 16 + 16, ad) * (st[i].am[1] * wscale[jj + 1]);
+        float am0 = st[i].am[0], am1 = st[i].am[1];
+        if constexpr (DQ) {
+          // an invalid block or a pad entry reads code 0: its absmax must be
+          // zero, as the zero-extent fp32 load gives it
+          const uint32_t b0 = lane_value(bid_v, jj), b1 = lane_value(bid_v, jj + 1);
+          const uint32_t f0 = o * Ad + ((32u * b0) >> a.qbs_shift), f1 = o * Ad + ((32u * b1) >> a.qbs_shift);
+          am0 = dq_absmax(c2[st[i].qa[0]], a2[(f0 >> a.dq_shift) - g_lo], a.down.offset);
+          am1 = dq_absmax(c2[st[i].qa[1]], a2[(f1 >> a.dq_shift) - g_lo], a.down.offset);
+          if (lane_value(enc_v, jj) & kBad) am0 = 0.0f;
+          if (lane_value(enc_v, jj + 1) & kBad) am1 = 0.0f;
+        }
+        acc += rep_dot32(st[i].w[0], wact + jj * 16, ad) * (am0 * wscale[jj]);
+        acc += rep_dot32(st[i].w[1], wact + jj * 16 + 16, ad) * (am1 * wscale[jj + 1]);
       }
       const int tn = t + kDnStages;
       const bool in = tn < T;
-      dn_issue(a, in ? lane_value(enc_v, in ? 2 * tn : 0) : kBad, roff, aroff4, st[i].w[0], st[i].am[0]);
-      dn_issue(a, in ? lane_value(enc_v, in ? 2 * tn + 1 : 0) : kBad, roff, aroff4, st[i].w[1], st[i].am[1]);
+      dn_issue<DQ>(a, in ? lane_value(enc_v, in ? 2 * tn : 0) : kBad, roff, aoff, st[i].w[0], st[i].am[0],
+                   st[i].qa[0]);
+      dn_issue<DQ>(a, in ? lane_value(enc_v, in ? 2 * tn + 1 : 0) : kBad, roff, aoff, st[i].w[1], st[i].am[1],
+                   st[i].qa[1]);
     }
   }
   // wave sums added in wave (block) order
@@ -517,12 +620,25 @@ bool plan_streaming(DecodeArgs& a, int cus) {
        a.host_gate.abs_row_stride != a.gate.abs_row_stride || a.host_up.abs_row_stride != a.gate.abs_row_stride ||
        a.host_down.row_stride != a.down.row_stride || a.host_down.abs_row_stride != a.down.abs_row_stride))
     return false;
+  const int ab = a.dq ? 1 : 4;  // bytes per stored absmax
   const long long gu_bytes = 31 * a.gate.row_stride + a.H / 2;
-  const long long gu_abytes = (31 * a.gate.abs_row_stride + a.H / a.qbs) * 4;
+  const long long gu_abytes = (31 * a.gate.abs_row_stride + a.H / a.qbs) * ab;
   const long long dn_bytes = (long long)(a.H - 1) * a.down.row_stride + 16;
-  const long long dn_abytes = ((long long)(a.H - 1) * a.down.abs_row_stride + 1) * 4;
+  const long long dn_abytes = ((long long)(a.H - 1) * a.down.abs_row_stride + 1) * ab;
   const long long lim = 1LL << 31;
   if (gu_bytes >= lim || gu_abytes >= lim || dn_bytes >= lim || dn_abytes >= lim) return false;
+  if (a.dq) {
+    // flat absmax indices in 32 bits; the down workgroup's absmax2 entries fit
+    // its LDS stage
+    const long long Ad = (long long)a.NB * 32 / a.qbs;
+    const long long n_abs = (long long)a.H * Ad;
+    if (n_abs >= lim) return false;
+    const long long n2 = (n_abs + (1LL << a.dq_shift) - 1) >> a.dq_shift;
+    const long long a2n = ((64 * Ad - 1) >> a.dq_shift) + 2;
+    if (a2n > kDnA2Max) return false;
+    a.st_gu_a2bytes = (int)(n2 * 4);
+    a.st_dn_a2n = (int)a2n;
+  }
   const int S = a.H / kSplit;
   const int NS = kWaves / S;
   // gate/up: rounds of NS items per workgroup, balanced over the workgroups
@@ -559,25 +675,30 @@ bool plan_streaming(DecodeArgs& a, int cus) {
 bool streaming_can_select(int NB, int k) { return NB >= 1 && NB <= kSelMaxNB && k >= 1 && k <= NB && k <= kSelMaxK; }
 
 void launch_decode_streaming(const DecodeArgs& a, hipStream_t s) {
+  using GuFn = void (*)(DecodeArgs);
+  // [dq][affine][0: given ids, 1: top-k of 4 scores per thread, 2: of 8]
+  static const GuFn gu_fns[2][2][3] = {
+      {{k_gu_rep<false, 0, false>, k_gu_rep<false, 4, false>, k_gu_rep<false, 8, false>},
+       {k_gu_rep<true, 0, false>, k_gu_rep<true, 4, false>, k_gu_rep<true, 8, false>}},
+      {{k_gu_rep<false, 0, true>, k_gu_rep<false, 4, true>, k_gu_rep<false, 8, true>},
+       {k_gu_rep<true, 0, true>, k_gu_rep<true, 4, true>, k_gu_rep<true, 8, true>}}};
   std::call_once(g_attr_once, [] {
-    set_lds_limit(k_gu_rep<false, 0>, kGuLds);
-    set_lds_limit(k_gu_rep<true, 0>, kGuLds);
-    set_lds_limit(k_gu_rep<false, 4>, kGuSelLds);
-    set_lds_limit(k_gu_rep<true, 4>, kGuSelLds);
-    set_lds_limit(k_gu_rep<false, 8>, kGuSelLds);
-    set_lds_limit(k_gu_rep<true, 8>, kGuSelLds);
-    set_lds_limit(k_down_rep, kDnLds);
+    for (int d = 0; d < 2; ++d)
+      for (int f = 0; f < 2; ++f)
+        for (int m = 0; m < 3; ++m) set_lds_limit(gu_fns[d][f][m], m ? kGuSelLds : (d ? kGuDqLds : kGuLds));
+    set_lds_limit(k_down_rep<false>, kDnLds);
+    set_lds_limit(k_down_rep<true>, kDnDqLds);
   });
   const bool affine = a.gate_bias != nullptr || a.up_bias != nullptr || a.mask != nullptr;
-  void (*gu)(DecodeArgs) = affine ? k_gu_rep<true, 0> : k_gu_rep<false, 0>;
-  size_t gu_lds = kGuLds;
-  if (a.sel_scores != nullptr) {
-    const bool four = a.NB <= 4 * kThreads8;
-    gu = affine ? (four ? k_gu_rep<true, 4> : k_gu_rep<true, 8>) : (four ? k_gu_rep<false, 4> : k_gu_rep<false, 8>);
-    gu_lds = (size_t)kGuSelWord * 4 + (size_t)a.k * sizeof(int32_t);
-  }
+  const int mode = a.sel_scores == nullptr ? 0 : (a.NB <= 4 * kThreads8 ? 1 : 2);
+  const GuFn gu = gu_fns[a.dq ? 1 : 0][affine ? 1 : 0][mode];
+  const size_t gu_lds = mode ? (size_t)kGuSelWord * 4 + (size_t)a.k * sizeof(int32_t) : (a.dq ? kGuDqLds : kGuLds);
   gu<<<dim3(a.st_gu_wgs), dim3(kThreads8), gu_lds, s>>>(a);
-  hipLaunchKernelGGL(k_down_rep, dim3((a.H / kWave) * a.st_dn_gx), dim3(kThreads8), kDnLds, s, a);
+  const dim3 gd((a.H / kWave) * a.st_dn_gx), bd(kThreads8);
+  if (a.dq)
+    k_down_rep<true><<<gd, bd, kDnDqLds, s>>>(a);
+  else
+    k_down_rep<false><<<gd, bd, kDnLds, s>>>(a);
   if (a.st_dn_gx > 1) hipLaunchKernelGGL(k_fin_rep, dim3(a.H / 256), dim3(256), 0, s, a);
 }
 

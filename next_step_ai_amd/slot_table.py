@@ -13,7 +13,9 @@ device and is read by the decode kernels directly:
   reference's [H, n, 16] column gather, RT:4491-4511, transposed so that a
   block's column is one contiguous 256 KB stream at the 405B shape);
 * optional pinned host copy of every block in the same layout; misses are
-  read by the kernels over the host link, without a host round trip.
+  read by the kernels over the host link, without a host round trip;
+* absmax either fp32 or double-quantised (``NestedAbsmax``: u8 codes in the
+  same positions, resolved by the kernels; RT:4621-4625).
 
 The fixed-capacity replacement policy keeps the reference's rule
 (``plan_fixed_capacity_bank_update``, RT:2576-2617).
@@ -26,6 +28,7 @@ import torch
 
 from . import _lib
 from ._runtime import nf4_code, ptr, require_device, stream_handle, workspace
+from .nested_absmax import NestedAbsmax
 
 BLOCK = 32
 
@@ -81,15 +84,18 @@ def partition_cached_block_lookup(lookup: torch.Tensor, *, ordered_blocks: torch
 def gather_row_blocks(packed: torch.Tensor, absmax: torch.Tensor, blocks: torch.Tensor, in_features: int,
                       qbs: int) -> tuple[torch.Tensor, torch.Tensor]:
     """Device gather of gate/up row blocks (RT:4530-4578 semantics):
-    returns [n, 32*in/2] u8 and [n, 32*in/qbs] f32."""
+    returns [n, 32*in/2] u8 and [n, 32*in/qbs] absmax (f32, or the u8 codes
+    of a double-quantised absmax)."""
     device = require_device(packed, "packed")
     b = blocks.to(device=device, dtype=torch.int32).contiguous()
     n = int(b.numel())
+    q8 = absmax.dtype == torch.uint8
     out_p = torch.empty((n, BLOCK * int(in_features) // 2), dtype=torch.uint8, device=device)
-    out_a = torch.empty((n, BLOCK * int(in_features) // int(qbs)), dtype=torch.float32, device=device)
+    out_a = torch.empty((n, BLOCK * int(in_features) // int(qbs)), dtype=absmax.dtype if q8 else torch.float32,
+                        device=device)
     src_blocks = int(packed.numel()) // (BLOCK * int(in_features) // 2)
-    _lib.call("nsmlp_gather_row_blocks", ptr(packed), ptr(absmax), src_blocks, ptr(b), n, int(in_features), int(qbs),
-              ptr(out_p), ptr(out_a), stream_handle(device))
+    _lib.call("nsmlp_gather_row_blocks_q8" if q8 else "nsmlp_gather_row_blocks", ptr(packed), ptr(absmax),
+              src_blocks, ptr(b), n, int(in_features), int(qbs), ptr(out_p), ptr(out_a), stream_handle(device))
     return out_p, out_a
 
 
@@ -103,16 +109,18 @@ def gather_down_columns(packed: torch.Tensor, absmax: torch.Tensor, blocks: torc
     b = blocks.to(device=device, dtype=torch.int32).contiguous()
     n = int(b.numel())
     H = int(out_features)
+    q8 = absmax.dtype == torch.uint8
+    adt = torch.uint8 if q8 else torch.float32
     if block_major:
         out_p = torch.empty((n, H, 16), dtype=torch.uint8, device=device)
-        out_a = torch.empty((n, H), dtype=torch.float32, device=device)
+        out_a = torch.empty((n, H), dtype=adt, device=device)
         layout = _lib.NSMLP_DOWN_BLOCK_MAJOR
     else:
         out_p = torch.empty((H, n, 16), dtype=torch.uint8, device=device)
-        out_a = torch.empty((H, n), dtype=torch.float32, device=device)
+        out_a = torch.empty((H, n), dtype=adt, device=device)
         layout = _lib.NSMLP_DOWN_GATHERED
-    _lib.call("nsmlp_gather_down_columns", ptr(packed), ptr(absmax), ptr(b), n, H, int(in_features), int(qbs),
-              layout, ptr(out_p), ptr(out_a), stream_handle(device))
+    _lib.call("nsmlp_gather_down_columns_q8" if q8 else "nsmlp_gather_down_columns", ptr(packed), ptr(absmax),
+              ptr(b), n, H, int(in_features), int(qbs), layout, ptr(out_p), ptr(out_a), stream_handle(device))
     return out_p, out_a
 
 
@@ -137,6 +145,9 @@ class SparseMlpSlotTable:
         self.block_ids: torch.Tensor | None = None
         self.gate_packed = self.gate_absmax = self.up_packed = self.up_absmax = None
         self.down_packed = self.down_absmax = None
+        # double-quantised absmax: *_absmax hold the u8 codes; second-level
+        # state per projection
+        self.nested: dict[str, NestedAbsmax] | None = None
         self.host: dict[str, torch.Tensor] = {}
         self.down_bias: torch.Tensor | None = None
         self.code = nf4_code(device)
@@ -147,17 +158,27 @@ class SparseMlpSlotTable:
         return 0 if self.gate_packed is None else int(self.gate_packed.shape[0])
 
     @classmethod
-    def from_reference(cls, *, gate_packed: torch.Tensor, gate_absmax: torch.Tensor, up_packed: torch.Tensor,
-                       up_absmax: torch.Tensor, down_packed: torch.Tensor, down_absmax: torch.Tensor, H: int, I: int,
-                       qbs: int = 64, resident_blocks: torch.Tensor | None = None,
-                       host_copy: bool = False) -> "SparseMlpSlotTable":
+    def from_reference(cls, *, gate_packed: torch.Tensor, gate_absmax, up_packed: torch.Tensor, up_absmax,
+                       down_packed: torch.Tensor, down_absmax, H: int, I: int, qbs: int = 64,
+                       resident_blocks: torch.Tensor | None = None, host_copy: bool = False) -> "SparseMlpSlotTable":
         """Build from the reference layouts on the device: gate/up ``[I*H/2]``
-        u8 + ``[I*H/qbs]`` f32, down ``[H*I/2]`` u8 + ``[H*I/qbs]`` f32.
-        ``resident_blocks`` (default: all) go to HBM slots in the given
-        order; with ``host_copy`` every block is also kept in pinned host
-        memory and non-resident blocks are served from there."""
+        u8 + ``[I*H/qbs]`` absmax, down ``[H*I/2]`` u8 + ``[H*I/qbs]`` absmax.
+        The absmax are fp32 tensors, or all three ``NestedAbsmax`` (the
+        double-quantised state, kept as u8 codes).  ``resident_blocks``
+        (default: all) go to HBM slots in the given order; with ``host_copy``
+        every block is also kept in pinned host memory and non-resident
+        blocks are served from there."""
         device = require_device(gate_packed, "gate_packed")
         t = cls(H=H, I=I, qbs=qbs, device=device)
+        nested = [isinstance(x, NestedAbsmax) for x in (gate_absmax, up_absmax, down_absmax)]
+        if any(nested):
+            if not all(nested):
+                raise RuntimeError("gate, up and down absmax must all be fp32 or all NestedAbsmax")
+            bs = {int(x.blocksize) for x in (gate_absmax, up_absmax, down_absmax)}
+            if len(bs) != 1:
+                raise RuntimeError(f"nested absmax block sizes differ: {sorted(bs)}")
+            t.nested = {"gate": gate_absmax, "up": up_absmax, "down": down_absmax}
+            gate_absmax, up_absmax, down_absmax = gate_absmax.q, up_absmax.q, down_absmax.q
         NB = t.NB
         all_blocks = torch.arange(NB, dtype=torch.int32, device=device)
         if resident_blocks is None:
@@ -211,6 +232,18 @@ class SparseMlpSlotTable:
             host_down_absmax=_host_dev_ptr(h.get("down_absmax")),
             code=ptr(self.code), down_bias=ptr(self.down_bias),
         )
+        if self.nested is not None:
+            # the u8 codes take the double-quantised fields; the fp32 ones stay NULL
+            st.gate_qabsmax, st.up_qabsmax, st.down_qabsmax = st.gate_absmax, st.up_absmax, st.down_absmax
+            st.host_gate_qabsmax, st.host_up_qabsmax = st.host_gate_absmax, st.host_up_absmax
+            st.host_down_qabsmax = st.host_down_absmax
+            st.gate_absmax = st.up_absmax = st.down_absmax = None
+            st.host_gate_absmax = st.host_up_absmax = st.host_down_absmax = None
+            g, u, d = self.nested["gate"], self.nested["up"], self.nested["down"]
+            st.dq_block = int(g.blocksize)
+            st.gate_absmax2, st.up_absmax2, st.down_absmax2 = ptr(g.absmax2), ptr(u.absmax2), ptr(d.absmax2)
+            st.gate_code2, st.up_code2, st.down_code2 = ptr(g.code2), ptr(u.code2), ptr(d.code2)
+            st.gate_offset, st.up_offset, st.down_offset = float(g.offset), float(u.offset), float(d.offset)
         self._struct = st
         return st
 

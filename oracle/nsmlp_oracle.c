@@ -382,17 +382,15 @@ void orc_dynamic_map_signed(float* out256) {
 }
 
 /* Double quantisation of an fp32 absmax vector (bitsandbytes compress_statistics):
- * offset = mean(absmax); a = absmax - offset; blocks of 256: absmax2 = max|a|,
- * q = index of the nearest map value to a/absmax2 (ties: lower index).
+ * offset = mean(absmax); a = absmax - offset; blocks of dq_block (bitsandbytes:
+ * 256): absmax2 = max|a|, q = index of the nearest map value to
+ * a * fl32(1/absmax2) (ties: lower index).
  * Dequantised absmax = fl32(fl32(map[q] * absmax2) + offset).               */
-void orc_double_quant(const float* absmax, long n, const float* map256, uint8_t* q, float* absmax2, float* offset_out) {
-  double s = 0.0;
-  for (long i = 0; i < n; ++i) s += absmax[i];
-  float offset = (float)(s / (double)n);
-  *offset_out = offset;
-  long nb = (n + 255) / 256;
+void orc_double_quant_ex(const float* absmax, long n, const float* map256, long dq_block, float offset, uint8_t* q,
+                         float* absmax2) {
+  long nb = (n + dq_block - 1) / dq_block;
   for (long b = 0; b < nb; ++b) {
-    long lo = b * 256, hi = lo + 256 < n ? lo + 256 : n;
+    long lo = b * dq_block, hi = lo + dq_block < n ? lo + dq_block : n;
     float amax = 0.0f;
     for (long i = lo; i < hi; ++i) {
       float a = fabsf(absmax[i] - offset);
@@ -416,11 +414,24 @@ void orc_double_quant(const float* absmax, long n, const float* map256, uint8_t*
   }
 }
 
-void orc_double_dequant(const uint8_t* q, const float* absmax2, float offset, const float* map256, long n, float* out) {
+void orc_double_quant(const float* absmax, long n, const float* map256, uint8_t* q, float* absmax2, float* offset_out) {
+  double s = 0.0;
+  for (long i = 0; i < n; ++i) s += absmax[i];
+  float offset = (float)(s / (double)n);
+  *offset_out = offset;
+  orc_double_quant_ex(absmax, n, map256, 256, offset, q, absmax2);
+}
+
+void orc_double_dequant_ex(const uint8_t* q, const float* absmax2, float offset, const float* map256, long n,
+                           long dq_block, float* out) {
   for (long i = 0; i < n; ++i) {
-    volatile float p = map256[q[i]] * absmax2[i / 256];
+    volatile float p = map256[q[i]] * absmax2[i / dq_block];
     out[i] = p + offset;
   }
+}
+
+void orc_double_dequant(const uint8_t* q, const float* absmax2, float offset, const float* map256, long n, float* out) {
+  orc_double_dequant_ex(q, absmax2, offset, map256, n, 256, out);
 }
 
 /* ------------------------------------------------------------------- MLP */

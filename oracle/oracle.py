@@ -74,6 +74,10 @@ def _load():
     lib.orc_double_quant.argtypes = [P, L, P, P, P, P]
     lib.orc_double_dequant.restype = None
     lib.orc_double_dequant.argtypes = [P, P, ctypes.c_float, P, L, P]
+    lib.orc_double_quant_ex.restype = None
+    lib.orc_double_quant_ex.argtypes = [P, L, P, L, ctypes.c_float, P, P]
+    lib.orc_double_dequant_ex.restype = None
+    lib.orc_double_dequant_ex.argtypes = [P, P, ctypes.c_float, P, L, L, P]
     lib.orc_sparse_mlp.restype = I
     lib.orc_sparse_mlp.argtypes = [I, I, I, I, P, P, I, P, P, P, P, P, P, P, P, P, P]
     for name in ("orc_f32_to_f16_array", "orc_f16_to_f32_array", "orc_f64_to_f16_array"):
@@ -329,23 +333,30 @@ def dynamic_map_signed() -> np.ndarray:
     return out
 
 
-def double_quant(absmax, map256=None):
+def double_quant(absmax, map256=None, *, dq_block=256, offset=None):
+    """bitsandbytes double quantisation of an fp32 absmax vector (restated):
+    returns (q u8, absmax2 f32, offset).  ``offset`` defaults to the mean."""
     absmax = _c(absmax, np.float32).reshape(-1)
     m = dynamic_map_signed() if map256 is None else _c(map256, np.float32)
     n = absmax.size
     q = np.empty(n, dtype=np.uint8)
-    a2 = np.empty((n + 255) // 256, dtype=np.float32)
-    off = np.empty(1, dtype=np.float32)
-    _load().orc_double_quant(_p(absmax), n, _p(m), _p(q), _p(a2), _p(off))
-    return q, a2, float(off[0])
+    a2 = np.empty((n + dq_block - 1) // dq_block, dtype=np.float32)
+    if offset is None:
+        if dq_block != 256:
+            raise ValueError("the mean offset is computed for dq_block=256 only; pass offset")
+        off = np.empty(1, dtype=np.float32)
+        _load().orc_double_quant(_p(absmax), n, _p(m), _p(q), _p(a2), _p(off))
+        return q, a2, float(off[0])
+    _load().orc_double_quant_ex(_p(absmax), n, _p(m), int(dq_block), ctypes.c_float(offset), _p(q), _p(a2))
+    return q, a2, float(np.float32(offset))
 
 
-def double_dequant(q, absmax2, offset, map256=None):
+def double_dequant(q, absmax2, offset, map256=None, *, dq_block=256):
     q = _c(q, np.uint8).reshape(-1)
     a2 = _c(absmax2, np.float32).reshape(-1)
     m = dynamic_map_signed() if map256 is None else _c(map256, np.float32)
     out = np.empty(q.size, dtype=np.float32)
-    _load().orc_double_dequant(_p(q), _p(a2), ctypes.c_float(offset), _p(m), q.size, _p(out))
+    _load().orc_double_dequant_ex(_p(q), _p(a2), ctypes.c_float(offset), _p(m), q.size, int(dq_block), _p(out))
     return out
 
 

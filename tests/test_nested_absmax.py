@@ -1,0 +1,69 @@
+"""Double-quantised absmax (bitsandbytes nested state) on the CPU: the
+oracle's quantiser checked against brute force and the mathematics, and the
+package's dynamic map against the oracle's.
+
+Parity at the bitsandbytes boundary itself (bitsandbytes==0.49.1, absent
+here) is unpinned: the map and the quantiser are restated from the published
+construction; the decode only consumes (q, absmax2, code2, offset) as data."""
+import numpy as np
+
+
+def _nearest_brute(m, v):
+    """Index of the nearest map entry to each v (fp32 distances, ties to the lower index)."""
+    d = np.abs(m[None, :].astype(np.float32) - v[:, None].astype(np.float32))
+    return np.argmin(d, axis=1)  # argmin returns the first minimum
+
+
+def test_package_dynamic_map_equals_oracle(orc):
+    from next_step_ai_amd.nested_absmax import dynamic_map_signed
+
+    a, b = dynamic_map_signed(), orc.dynamic_map_signed()
+    assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+    # 7 exponent levels of 2^i midpoints each side, plus 0 and 1; the largest
+    # level's midpoints lie in (0.1, 1): 64 positive values above 0.1
+    assert np.count_nonzero(a > 0.1) == 64 + 1 and np.count_nonzero((a > 0) & (a < 1e-6)) == 1
+    assert np.all(np.diff(a) > 0)  # strictly increasing: a nearest entry is unique up to ties
+
+
+def test_double_quant_nearest_and_group_max(orc):
+    m = orc.dynamic_map_signed()
+    rng = np.random.default_rng(11)
+    for dq_block in (64, 256):
+        n = 5 * dq_block + 37  # partial last block
+        absmax = (np.abs(rng.standard_normal(n)) * 0.03 + 0.002).astype(np.float32)
+        absmax[dq_block: 2 * dq_block] = np.float32(0.0125)  # a block equal to the offset: absmax2 = 0
+        off = np.float32(0.0125)
+        q, a2, off_r = orc.double_quant(absmax, m, dq_block=dq_block, offset=float(off))
+        assert off_r == float(off) and a2.size == (n + dq_block - 1) // dq_block
+        a = (absmax - off).astype(np.float32)
+        for b in range(a2.size):
+            blk = a[b * dq_block:(b + 1) * dq_block]
+            amax = np.float32(np.max(np.abs(blk)))
+            assert a2[b] == amax
+            inv = np.float32(1.0) / amax if amax > 0 else np.float32(0.0)
+            v = (blk * inv).astype(np.float32)
+            assert np.array_equal(q[b * dq_block:(b + 1) * dq_block], _nearest_brute(m, v))
+            if amax > 0:
+                i = int(np.argmax(np.abs(blk)))
+                # the block's extreme maps to +1 (index 255) or the most negative entry (index 0)
+                assert q[b * dq_block + i] == (255 if blk[i] > 0 else 0)
+            else:
+                assert np.all(m[q[b * dq_block:(b + 1) * dq_block]] == 0.0)
+        back = orc.double_dequant(q, a2, float(off), m, dq_block=dq_block)
+        gaps = np.max(np.diff(m))
+        bound = np.repeat(a2, dq_block)[:n] * gaps / 2 * 1.001 + 1e-7
+        assert np.all(np.abs(back - absmax) <= bound)
+
+
+def test_double_dequant_exact_for_representable_values(orc):
+    """absmax2 a power of two and offset 0: map[j] * absmax2 is exact, so
+    quantising those values and dequantising returns them bit for bit."""
+    m = orc.dynamic_map_signed()
+    a2 = np.float32(0.25)
+    vals = (m * a2).astype(np.float32)
+    vals[-1] = a2  # the block's max |a| is absmax2 itself (map value 1)
+    q, got_a2, _ = orc.double_quant(vals, m, dq_block=256, offset=0.0)
+    assert got_a2[0] == a2
+    assert np.array_equal(q, np.arange(256, dtype=np.uint8))
+    back = orc.double_dequant(q, got_a2, 0.0, m, dq_block=256)
+    assert np.array_equal(back.view(np.uint32), vals.view(np.uint32))
