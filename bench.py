@@ -13,13 +13,18 @@ Reported (one JSON line):
   ms_per_step   wall time per layer (router + MLP), inputs resident in HBM
   roofline      the sparse-MLP decode launch pair (k_gu_rep + k_down_rep),
                 timed with HIP events on its launch stream: algorithmic bytes
-                per launch (selected packed NF4 + fp32 absmax + x + out) /
-                duration.  traffic: HBM bytes per launch from the rocprofv3
+                per launch (selected packed NF4 + their absmax in the stored
+                format + x + out) / duration.  traffic: HBM bytes per launch from the rocprofv3
                 FETCH_SIZE / WRITE_SIZE summary committed for this workload,
                 scaled by the same counters on a plain copy (null without it)
   cpu_baseline  the oracle's restatement of the reference PyTorch path
                 (router + dequant fallback with fp16 rounding points) on the
                 host cores, on the same layer shape
+
+The weights are NF4 with double-quantised absmax (bitsandbytes
+compress_statistics: u8 codes, one fp32 scale per 256, an offset), the format
+the workload names; --absmax f32 stores the resolved fp32 absmax instead (the
+reference runtime's slot-table format, RT:4621-4625).
 
 --copy-calibration BYTES runs only a plain device copy of BYTES (the
 reference kernel for the counter calibration) and prints its size.
@@ -49,12 +54,19 @@ WORKLOADS = {
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic_sparse_mlp_decode.json")
 
 
-def algorithmic_bytes(H: int, k: int, qbs: int) -> int:
+def algorithmic_bytes(H: int, I: int, k: int, qbs: int, absmax: str = "dq8", dq_block: int = 256) -> int:
     """Bytes the sparse MLP must move once per layer: the selected blocks'
-    packed NF4 (gate, up: 32 x H/2; down: H x 16) and fp32 absmax
-    (gate, up: 32 x H/qbs; down: H, one per row and block), plus x and out."""
-    per_block = 2 * (32 * H // 2 + 4 * 32 * H // qbs) + (16 * H + 4 * H)
-    return k * per_block + 2 * H * 2
+    packed NF4 (gate, up: 32 x H/2; down: H x 16) and absmax (gate, up:
+    32 x H/qbs; down: H, one per row and block; 4 bytes fp32, or 1 byte u8
+    double-quantised plus the fp32 second-level scales they use: per gate/up
+    block its rows' 32 H/qbs / dq_block (at least 1), and the down weight's
+    whole H I/qbs / dq_block), plus x and out."""
+    ab = 4 if absmax == "f32" else 1
+    per_block = 2 * (32 * H // 2 + ab * 32 * H // qbs) + (16 * H + ab * H)
+    total = k * per_block + 2 * H * 2
+    if absmax != "f32":
+        total += 2 * k * 4 * max(1, 32 * H // qbs // dq_block) + 4 * (H * I // qbs // dq_block)
+    return total
 
 
 def router_bytes(H: int, R: int, NB: int) -> int:
@@ -80,7 +92,7 @@ def cpu_model() -> str:
     return "unknown"
 
 
-def measured_traffic(config: int):
+def measured_traffic(config: int, absmax: str):
     """HBM bytes per sparse-MLP launch pair from the committed counter
     summary, or None when there is none for this workload."""
     try:
@@ -88,13 +100,13 @@ def measured_traffic(config: int):
             t = json.load(f)
     except (OSError, ValueError):
         return None
-    entry = t.get("configs", {}).get(str(config))
+    entry = t.get("configs", {}).get(f"{config}-{absmax}")
     if not entry:
         return None
     return int(entry["fetch_bytes"] + entry["write_bytes"])
 
 
-def cpu_baseline(layer, sel, runs: int, H: int, I: int, k: int, qbs: int) -> dict:
+def cpu_baseline(layer, sel, runs: int, H: int, I: int, k: int, qbs: int, absmax: str) -> dict:
     """Time the oracle's restatement of the reference PyTorch path (router +
     dequant fallback over the gathered blocks) on the host cores."""
     import numpy as np
@@ -116,7 +128,12 @@ def cpu_baseline(layer, sel, runs: int, H: int, I: int, k: int, qbs: int) -> dic
     upk, ua = orc.gather_rows_blocks(npy(layer.up_packed), npy(layer.up_absmax), sel_np, H, qbs)
     t = layer.table
     dp = npy(t.down_packed)[sel_np].transpose(1, 0, 2).copy()  # block-major -> the reference's [H, k, 16]
-    da = npy(t.down_absmax)[sel_np].T.copy()
+    if layer.nested is not None:
+        # the reference computes with the resolved fp32 absmax (RT:4621-4625)
+        da_full = npy(layer.nested["down"].resolve()).reshape(H, I // qbs)
+        da = da_full[:, (sel_np * 32) // qbs].copy()
+    else:
+        da = npy(t.down_absmax)[sel_np].T.copy()
     x16, ew, eb, sw, sb = (u16(v) for v in (layer.x, layer.enc_w, layer.enc_b, layer.score_w, layer.score_b))
     al = np.arange(k, dtype=np.int32).reshape(1, k)
 
@@ -135,7 +152,7 @@ def cpu_baseline(layer, sel, runs: int, H: int, I: int, k: int, qbs: int) -> dic
         "value": round(1e6 / (MODEL_LAYERS * us), 6),
         "unit": "tok/s",
         "us_per_layer": round(us, 1),
-        "gbs": round(algorithmic_bytes(H, k, qbs) / (us * 1e-6) / 1e9, 3),
+        "gbs": round(algorithmic_bytes(H, I, k, qbs, absmax) / (us * 1e-6) / 1e9, 3),
         "cores": threads,
         "kind": "port",
         "cpu": cpu_model(),
@@ -168,6 +185,8 @@ def main() -> int:
     ap.add_argument("--cpu-runs", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="BYTES")
+    ap.add_argument("--absmax", choices=("dq8", "f32"), default="dq8",
+                    help="absmax storage: double-quantised u8 (default) or resolved fp32")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py runs on one GPU only; --gpus {args.gpus} is not supported: this decode path has no "
@@ -189,7 +208,8 @@ def main() -> int:
     t_gen = time.perf_counter()
     layers = []
     for l in range(args.layers):
-        L = make_synthetic_layer(H=H, I=I, R=R, seed=1000 * args.config + l, device=device)
+        L = make_synthetic_layer(H=H, I=I, R=R, seed=1000 * args.config + l, device=device,
+                                 double_quant=args.absmax == "dq8")
         L.table = L.slot_table(drop_reference_down=True)
         L.mlp = SparseMlpLayer(L.router(), L.table, k)
         layers.append(L)
@@ -229,7 +249,7 @@ def main() -> int:
     mlp_us = statistics.mean(a.elapsed_time(b) for a, b in ev) * 1e3
     route_us = max(0.0, us_per_layer - mlp_us)
 
-    abytes = algorithmic_bytes(H, k, qbs)
+    abytes = algorithmic_bytes(H, I, k, qbs, args.absmax)
     achieved = abytes / (mlp_us * 1e-6) / 1e9
     result = {
         "metric": METRIC,
@@ -245,10 +265,12 @@ def main() -> int:
         "dtype": "nf4(u8)*f16->f32",
         "data": "synthetic",
         "config": {
-            "workload": WORKLOADS[args.config] + f"; NF4 qbs {qbs} with fp32 absmax; all blocks HBM-resident; "
+            "workload": WORKLOADS[args.config] + f"; NF4 qbs {qbs} with "
+                        + ("double-quantised absmax (u8, fp32 per 256, offset)" if args.absmax == "dq8"
+                           else "fp32 absmax") + f"; all blocks HBM-resident; "
                         f"{args.layers} rotating seeded layers; batch 1 fp16 token",
             "hidden": H, "intermediate": I, "basis_rank": R, "top_k": k, "block": 32, "quant_block": qbs,
-            "rotating_layers": args.layers,
+            "absmax": args.absmax, "rotating_layers": args.layers,
         },
         "us_per_layer": round(us_per_layer, 3),
         "sparse_mlp_us": round(mlp_us, 3),
@@ -262,12 +284,12 @@ def main() -> int:
             "peak": PEAK_GBS,
             "unit": "GB/s",
             "frac": round(achieved / PEAK_GBS, 4),
-            "traffic": measured_traffic(args.config),
+            "traffic": measured_traffic(args.config, args.absmax),
             "kernels": "k_gu_rep + k_down_rep (the sparse-MLP decode launch pair)",
         },
     }
     if not args.no_cpu_baseline:
-        result["cpu_baseline"] = cpu_baseline(layers[0], sels[0], args.cpu_runs, H, I, k, qbs)
+        result["cpu_baseline"] = cpu_baseline(layers[0], sels[0], args.cpu_runs, H, I, k, qbs, args.absmax)
     print(json.dumps(result), flush=True)
     return 0
 

@@ -24,9 +24,11 @@
  *     gate/up packed [slots][32][H/2] u8,  absmax [slots][32][H/qbs] f32
  *     down    packed [slots][H][16]  u8,   absmax [slots][H] f32
  *   Double-quantised absmax (the bitsandbytes nested quant state, which the
- *   reference resolves to fp32 at RT:4621-4625): u8 codes q in the absmax
- *   shapes above, one fp32 absmax2 per dq_block consecutive absmax of the
- *   full row-major weight, a 256-entry code2 and an fp32 offset:
+ *   reference resolves to fp32 at RT:4621-4625): u8 codes q, stored in slots
+ *   as gate/up [slots][16][H/qbs][2] (rows 2p and 2p+1 interleaved, so one
+ *   16-bit read gives a row pair) and down [slots][H]; one fp32 absmax2 per
+ *   dq_block consecutive absmax of the full row-major weight, a 256-entry
+ *   code2 and an fp32 offset:
  *     absmax = fp32(fp32(code2[q] * absmax2[f / dq_block]) + offset)
  *   where f is the absmax's index in the full weight (gate/up [I][H/qbs],
  *   down [H][I/qbs]); both roundings are kept (no fused multiply-add), so
@@ -123,10 +125,10 @@ typedef struct nsmlp_slot_table {
   const void* down_bias;             /* [H] fp16 or NULL */
   /* Double-quantised absmax (version >= 101).  dq_block == 0: the fp32
    * *_absmax above are read.  dq_block > 0 (a power of two; bitsandbytes
-   * uses 256): the fp32 *_absmax are ignored and the u8 codes below, in the
-   * same shapes and slot layout, are read instead. */
+   * uses 256): the fp32 *_absmax are ignored and the u8 codes below are
+   * read instead. */
   int dq_block;
-  const uint8_t* gate_qabsmax;       /* [n_slots][32][H/qbs] u8 */
+  const uint8_t* gate_qabsmax;       /* [n_slots][16][H/qbs][2] u8 (row pairs interleaved) */
   const uint8_t* up_qabsmax;
   const uint8_t* down_qabsmax;       /* [n_slots][H] u8 */
   const uint8_t* host_gate_qabsmax;  /* host copies (with the host packed copies) */
@@ -248,9 +250,11 @@ int nsmlp_gather_down_columns(const uint8_t* src_packed, const float* src_absmax
                               int out_features, int in_features, int qbs, int dst_layout, uint8_t* dst_packed,
                               float* dst_absmax, void* stream);
 
-/* The same two gathers for double-quantised absmax (u8 codes in the fp32
- * absmax positions; the packed bytes are gathered as above).  Replace the
- * same reference code, with the nested state kept instead of resolved
+/* The same two gathers for double-quantised absmax: the u8 codes of a row
+ * block are written in the slot layout [n][16][in/qbs][2] (rows 2p, 2p+1
+ * interleaved); the down codes as [n][out] (or [out][n]).  src_packed and
+ * dst_packed may both be NULL to gather the codes only.  Replace the same
+ * reference code, with the nested state kept instead of resolved
  * (RT:4621-4625). */
 int nsmlp_gather_row_blocks_q8(const uint8_t* src_packed, const uint8_t* src_qabsmax, int src_blocks,
                                const int32_t* blocks, int n, int in_features, int qbs, uint8_t* dst_packed,

@@ -657,8 +657,16 @@ int nsmlp_gather_row_blocks(const uint8_t* src_packed, const float* src_absmax, 
 int nsmlp_gather_row_blocks_q8(const uint8_t* src_packed, const uint8_t* src_qabsmax, int src_blocks,
                                const int32_t* blocks, int n, int in_features, int qbs, uint8_t* dst_packed,
                                uint8_t* dst_qabsmax, void* stream) {
-  return gather_rows_impl<uint8_t>(src_packed, src_qabsmax, src_blocks, blocks, n, in_features, qbs, dst_packed,
-                                   dst_qabsmax, stream);
+  if (n < 0 || src_blocks < 0 || in_features <= 0 || in_features % 32 != 0 || qbs <= 0 || in_features % qbs != 0)
+    return set_error(NSMLP_EINVAL, "bad row-block gather geometry");
+  if (n == 0) return NSMLP_OK;
+  if (!src_qabsmax || !blocks || !dst_qabsmax || (src_packed == nullptr) != (dst_packed == nullptr))
+    return set_error(NSMLP_EINVAL, "NULL tensor argument");
+  if ((src_packed && !aligned16(src_packed)) || (dst_packed && !aligned16(dst_packed)))
+    return set_error(NSMLP_EINVAL, "packed must be 16-byte aligned");
+  launch_gather_rows_q8(src_packed, src_qabsmax, blocks, src_blocks, n, 16LL * in_features, in_features / qbs,
+                        dst_packed, dst_qabsmax, (hipStream_t)stream);
+  return check_launch("gather rows (u8 absmax)");
 }
 
 int nsmlp_gather_down_columns(const uint8_t* src_packed, const float* src_absmax, const int32_t* blocks, int n,

@@ -102,9 +102,12 @@ __device__ __forceinline__ void gate_up_task(const DecodeArgs& a, DecodeSmem& sm
       w[i] = *reinterpret_cast<const uint4*>(base + off + (uint32_t)(ri * kStep) * rs);
       const uint32_t ai = aoff + (uint32_t)(ri * kStep) * ars;
       if (a.dq) {
+        // u8 codes interleave row pairs: (r, c) at ((r >> 1) A + c) 2 + (r & 1)
         const ProjView& pv = i < NR / 2 ? a.gate : a.up;
-        const long long f = ((long long)br.b * 32 + r0 + ri * kStep) * ars + (col >> a.qbs_shift);
-        am[i] = dq_absmax(pv.code2[(i < NR / 2 ? gq : uq)[ai]], pv.absmax2[f >> a.dq_shift], pv.offset);
+        const uint32_t r = (uint32_t)(r0 + ri * kStep), c = (uint32_t)(col >> a.qbs_shift);
+        const uint32_t qi = ((r >> 1) * ars + c) * 2u + (r & 1u);
+        const long long f = ((long long)br.b * 32 + r) * ars + c;
+        am[i] = dq_absmax(pv.code2[(i < NR / 2 ? gq : uq)[qi]], pv.absmax2[f >> a.dq_shift], pv.offset);
       } else {
         am[i] = abase[ai];
       }

@@ -604,6 +604,10 @@ void launch_gather_rows(const uint8_t* src, const AbsT* src_abs, const int32_t* 
 template <typename AbsT>
 void launch_gather_down(const uint8_t* src, const AbsT* src_abs, const int32_t* blocks, int n, int out_f, int in_f,
                         int qbs, int layout, uint8_t* dst, AbsT* dst_abs, hipStream_t s);
+// u8 absmax codes into the interleaved slot layout (and, when src_packed is
+// non-NULL, the packed bytes as launch_gather_rows does).
+void launch_gather_rows_q8(const uint8_t* src_packed, const uint8_t* src_q, const int32_t* blocks, int src_blocks,
+                           int n, long long bpb, int A, uint8_t* dst_packed, uint8_t* dst_q, hipStream_t s);
 void launch_absmax_dq(const float* absmax, long long n, int dq_block, const float* code2, float offset, uint8_t* q,
                       float* absmax2, hipStream_t s);
 void launch_absmax_undq(const uint8_t* q, long long n, int dq_shift, const float* code2, const float* absmax2,

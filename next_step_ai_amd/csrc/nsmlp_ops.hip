@@ -150,6 +150,19 @@ __global__ void k_gather_rows(const uint8_t* src, const AbsT* src_abs, const int
     dst_abs[i * apb + v] = src_abs[b * apb + v];
 }
 
+// u8 absmax codes of row blocks into the slot layout [n][16][A][2] (A =
+// entries per row): byte (r, c) of block i goes to ((r >> 1) A + c) 2 + (r & 1).
+__global__ void k_gather_rows_q8(const uint8_t* src, const int32_t* blocks, int src_blocks, int A, uint8_t* dst) {
+  const int i = blockIdx.y;
+  const long long b = blocks[i];
+  if (b < 0 || b >= src_blocks) return;
+  const long long apb = 32LL * A;
+  for (long long v = (long long)blockIdx.x * kThreads + threadIdx.x; v < apb; v += (long long)gridDim.x * kThreads) {
+    const long long r = v / A, c = v % A;
+    dst[i * apb + ((r >> 1) * A + c) * 2 + (r & 1)] = src[b * apb + v];
+  }
+}
+
 template <typename AbsT>
 __global__ void k_gather_down(const uint8_t* src, const AbsT* src_abs, const int32_t* blocks, int n, int out_f,
                               int in_f, int qbs, int layout, uint8_t* dst, AbsT* dst_abs) {
@@ -320,8 +333,21 @@ void launch_gather_rows(const uint8_t* src, const AbsT* src_abs, const int32_t* 
 }
 template void launch_gather_rows<float>(const uint8_t*, const float*, const int32_t*, int, int, long long, long long,
                                         uint8_t*, float*, hipStream_t);
-template void launch_gather_rows<uint8_t>(const uint8_t*, const uint8_t*, const int32_t*, int, int, long long,
-                                          long long, uint8_t*, uint8_t*, hipStream_t);
+
+void launch_gather_rows_q8(const uint8_t* src_packed, const uint8_t* src_q, const int32_t* blocks, int src_blocks,
+                           int n, long long bpb, int A, uint8_t* dst_packed, uint8_t* dst_q, hipStream_t s) {
+  const long long apb = 32LL * A;
+  unsigned gx = (unsigned)((apb + kThreads - 1) / kThreads);
+  if (gx > 64) gx = 64;
+  k_gather_rows_q8<<<dim3(gx, n), dim3(kThreads), 0, s>>>(src_q, blocks, src_blocks, A, dst_q);
+  if (src_packed != nullptr) {
+    unsigned gp = (unsigned)((bpb / 16 + kThreads - 1) / kThreads);
+    if (gp > 64) gp = 64;
+    // packed bytes only (absmax count 0)
+    k_gather_rows<uint8_t><<<dim3(gp, n), dim3(kThreads), 0, s>>>(src_packed, nullptr, blocks, src_blocks, bpb, 0,
+                                                                  dst_packed, nullptr);
+  }
+}
 
 template <typename AbsT>
 void launch_gather_down(const uint8_t* src, const AbsT* src_abs, const int32_t* blocks, int n, int out_f, int in_f,

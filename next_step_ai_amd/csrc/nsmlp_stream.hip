@@ -113,6 +113,9 @@ __device__ __forceinline__ float buf_ldf(rsrc_t r, uint32_t voff, uint32_t soff)
 __device__ __forceinline__ uint32_t buf_ldu8(rsrc_t r, uint32_t voff, uint32_t soff) {
   return (uint32_t)__builtin_amdgcn_raw_buffer_load_b8(r, (int)voff, (int)soff, kNontemporal);
 }
+__device__ __forceinline__ uint32_t buf_ldu16(rsrc_t r, uint32_t voff, uint32_t soff) {
+  return (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(r, (int)voff, (int)soff, kNontemporal);
+}
 
 // Replicated pair table, filled by 512 threads in 8 passes of one 16-byte LDS
 // write each: pass ps writes entry e = 32 ps + tid / 16, copies 4 (tid % 16)
@@ -142,17 +145,17 @@ __device__ __forceinline__ void lut_store(uint32_t* lut, const LutCodes& c, int 
 }
 
 struct GuStage {
-  uint4 w[4];    // gate 2p, gate 2p+1, up 2p, up 2p+1: this lane's 32 columns
-  float am[4];   // absmax, or (double-quantised) the absmax2 of the row
-  uint32_t qa[4];  // double-quantised: the u8 absmax code
+  uint4 w[4];      // gate 2p, gate 2p+1, up 2p, up 2p+1: this lane's 32 columns
+  float am[4];     // fp32 absmax of the four rows
+  uint32_t qa[2];  // double-quantised: u8 codes of gate rows 2p | 2p+1 << 8, same for up
 };
 
-// Issue the loads of one item (block reference enc, block id bid, row pair
-// p).  ca: this lane's absmax entry inside a row (its columns / qbs); cb:
-// its byte offset inside a packed row.
+// Issue the loads of one item (block reference enc, row pair p).  ca: this
+// lane's absmax entry inside a row (its columns / qbs); cb: its byte offset
+// inside a packed row.
 template <bool DQ>
-__device__ __forceinline__ void gu_issue(const DecodeArgs& a, uint32_t enc, uint32_t bid, int p, uint32_t cb,
-                                         uint32_t ca, GuStage& st) {
+__device__ __forceinline__ void gu_issue(const DecodeArgs& a, uint32_t enc, int p, uint32_t cb, uint32_t ca,
+                                         GuStage& st) {
   const bool bad = (enc & kBad) != 0;
   const bool dev = (enc & kHostBit) == 0;
   const long long q = bad ? 0 : (long long)(enc & (kHostBit - 1));
@@ -166,24 +169,12 @@ __device__ __forceinline__ void gu_issue(const DecodeArgs& a, uint32_t enc, uint
   st.w[2] = buf_ld16(ru, cb, s0);
   st.w[3] = buf_ld16(ru, cb, s0 + rs);
   if constexpr (DQ) {
+    // codes of rows 2p and 2p+1 at entry ca: one 16-bit read per projection
     const rsrc_t rgq = make_rsrc((dev ? a.gate.qabsmax : a.host_gate.qabsmax) + q * a.gate.abs_blk_stride, na);
     const rsrc_t ruq = make_rsrc((dev ? a.up.qabsmax : a.host_up.qabsmax) + q * a.up.abs_blk_stride, na);
-    const uint32_t as0 = (uint32_t)(2 * p) * ars;
-    st.qa[0] = buf_ldu8(rgq, ca, as0);
-    st.qa[1] = buf_ldu8(rgq, ca, as0 + ars);
-    st.qa[2] = buf_ldu8(ruq, ca, as0);
-    st.qa[3] = buf_ldu8(ruq, ca, as0 + ars);
-    // absmax2 of rows 32 bid + 2p (+1) at this lane's columns (one value per
-    // wave: a 2048-column split never straddles a second-level block)
-    const int n2 = bad ? 0 : a.st_gu_a2bytes;
-    const rsrc_t rg2 = make_rsrc(a.gate.absmax2, n2);
-    const rsrc_t ru2 = make_rsrc(a.up.absmax2, n2);
-    const uint32_t f0 = (32u * bid + 2u * (uint32_t)p) * ars + ca;
-    const uint32_t o0 = (f0 >> a.dq_shift) * 4u, o1 = ((f0 + ars) >> a.dq_shift) * 4u;
-    st.am[0] = buf_ldf(rg2, o0, 0);
-    st.am[1] = buf_ldf(rg2, o1, 0);
-    st.am[2] = buf_ldf(ru2, o0, 0);
-    st.am[3] = buf_ldf(ru2, o1, 0);
+    const uint32_t qo = ((uint32_t)p * ars + ca) * 2u;
+    st.qa[0] = buf_ldu16(rgq, qo, 0);
+    st.qa[1] = buf_ldu16(ruq, qo, 0);
   } else {
     const rsrc_t rga = make_rsrc((dev ? a.gate.absmax : a.host_gate.absmax) + q * a.gate.abs_blk_stride, na);
     const rsrc_t rua = make_rsrc((dev ? a.up.absmax : a.host_up.absmax) + q * a.up.abs_blk_stride, na);
@@ -195,13 +186,16 @@ __device__ __forceinline__ void gu_issue(const DecodeArgs& a, uint32_t enc, uint
   }
 }
 
-// The absmax of row i of a gate/up stage.
+// The absmax of row i of a gate/up stage; a2: the item's absmax2 of the row
+// (double-quantised).
 template <bool DQ>
-__device__ __forceinline__ float gu_absmax(const DecodeArgs& a, const GuStage& st, const float* c2, int i) {
-  if constexpr (DQ)
-    return dq_absmax(c2[(i >= 2 ? 256 : 0) + st.qa[i]], st.am[i], i >= 2 ? a.up.offset : a.gate.offset);
-  else
+__device__ __forceinline__ float gu_absmax(const DecodeArgs& a, const GuStage& st, const float* c2, int i, float a2) {
+  if constexpr (DQ) {
+    const uint32_t q = (st.qa[i >> 1] >> (8 * (i & 1))) & 0xFFu;
+    return dq_absmax(c2[(i >= 2 ? 256 : 0) + q], a2, i >= 2 ? a.up.offset : a.gate.offset);
+  } else {
     return st.am[i];
+  }
 }
 
 // Reduce-scatter of 4 per-lane row sums over the 64 lanes: afterwards every
@@ -313,15 +307,28 @@ __global__ void __launch_bounds__(kThreads8, 2) k_gu_rep(DecodeArgs a) {
       a.st_bid[id0 >> 4] = (int32_t)bid_v;
     }
   }
+  // double-quantised: lane i also holds item i's absmax2 of its four rows at
+  // this wave's split (a 2048-column split never straddles a second-level
+  // block), read once here instead of in the weight stream
+  float a2_v[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  if constexpr (DQ) {
+    const uint32_t ars = (uint32_t)a.gate.abs_row_stride;
+    const uint32_t f0 = (32u * bid_v + 2u * (uint32_t)(id0 & 15)) * ars + (uint32_t)(s * kSplit >> a.qbs_shift);
+    const uint32_t g0 = f0 >> a.dq_shift, g1 = (f0 + ars) >> a.dq_shift;
+    a2_v[0] = a.gate.absmax2[g0];
+    a2_v[1] = a.gate.absmax2[g1];
+    a2_v[2] = a.up.absmax2[g0];
+    a2_v[3] = a.up.absmax2[g1];
+    sched_fence();  // before the weight stream: their wait then drains nothing of it
+  }
   // Stage 0 of every wave goes out before any later stage; the barrier also
   // publishes the code table.
   GuStage st[kGuStages];
-  gu_issue<DQ>(a, R > 0 ? lane_value(enc_v, 0) : kBad, lane_value(bid_v, 0), (wg * NS + q) & 15, cb, ca, st[0]);
+  gu_issue<DQ>(a, R > 0 ? lane_value(enc_v, 0) : kBad, (wg * NS + q) & 15, cb, ca, st[0]);
   lds_barrier();
 #pragma unroll
   for (int i = 1; i < kGuStages; ++i)
-    gu_issue<DQ>(a, i < R ? lane_value(enc_v, i) : kBad, lane_value(bid_v, i < R ? i : 0),
-                 ((i * nwg + wg) * NS + q) & 15, cb, ca, st[i]);
+    gu_issue<DQ>(a, i < R ? lane_value(enc_v, i) : kBad, ((i * nwg + wg) * NS + q) & 15, cb, ca, st[i]);
   sched_fence();
 
   uint32_t adg[4], adu[4];
@@ -338,15 +345,19 @@ __global__ void __launch_bounds__(kThreads8, 2) k_gu_rep(DecodeArgs a) {
       const bool live = r < R;  // uniform over the workgroup
       float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
       if (live) {
-        acc[0] = rep_dot32(st[i].w[0], xp, adg) * gu_absmax<DQ>(a, st[i], c2, 0);
-        acc[1] = rep_dot32(st[i].w[1], xp, adg) * gu_absmax<DQ>(a, st[i], c2, 1);
-        acc[2] = rep_dot32(st[i].w[2], xp, adu) * gu_absmax<DQ>(a, st[i], c2, 2);
-        acc[3] = rep_dot32(st[i].w[3], xp, adu) * gu_absmax<DQ>(a, st[i], c2, 3);
+        float a2[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+        if constexpr (DQ) {
+#pragma unroll
+          for (int m = 0; m < 4; ++m) a2[m] = __uint_as_float(lane_value(__float_as_uint(a2_v[m]), r));
+        }
+        acc[0] = rep_dot32(st[i].w[0], xp, adg) * gu_absmax<DQ>(a, st[i], c2, 0, a2[0]);
+        acc[1] = rep_dot32(st[i].w[1], xp, adg) * gu_absmax<DQ>(a, st[i], c2, 1, a2[1]);
+        acc[2] = rep_dot32(st[i].w[2], xp, adu) * gu_absmax<DQ>(a, st[i], c2, 2, a2[2]);
+        acc[3] = rep_dot32(st[i].w[3], xp, adu) * gu_absmax<DQ>(a, st[i], c2, 3, a2[3]);
       }
       const int rn = r + kGuStages;
       const int rl = rn < R && rn < kMaxItems ? rn : 0;
-      gu_issue<DQ>(a, rn < R ? lane_value(enc_v, rl) : kBad, lane_value(bid_v, rl), ((rn * nwg + wg) * NS + q) & 15,
-                   cb, ca, st[i]);
+      gu_issue<DQ>(a, rn < R ? lane_value(enc_v, rl) : kBad, ((rn * nwg + wg) * NS + q) & 15, cb, ca, st[i]);
       if (live) {
         const float v = reduce4(acc, lane);
         if ((lane & 15) == 0) comb[(r & 1) * (kWaves * 4) + wave * 4 + (lane >> 4)] = v;

@@ -81,21 +81,31 @@ def partition_cached_block_lookup(lookup: torch.Tensor, *, ordered_blocks: torch
     return pos, slots, ordered_blocks[cold_mask], cold_mask
 
 
-def gather_row_blocks(packed: torch.Tensor, absmax: torch.Tensor, blocks: torch.Tensor, in_features: int,
-                      qbs: int) -> tuple[torch.Tensor, torch.Tensor]:
+def gather_row_blocks(packed: torch.Tensor | None, absmax: torch.Tensor, blocks: torch.Tensor, in_features: int,
+                      qbs: int) -> tuple[torch.Tensor | None, torch.Tensor]:
     """Device gather of gate/up row blocks (RT:4530-4578 semantics):
-    returns [n, 32*in/2] u8 and [n, 32*in/qbs] absmax (f32, or the u8 codes
-    of a double-quantised absmax)."""
-    device = require_device(packed, "packed")
+    returns [n, 32*in/2] u8 and [n, 32*in/qbs] f32 absmax, or, for the u8
+    codes of a double-quantised absmax, [n, 16, in/qbs, 2] (rows 2p and 2p+1
+    interleaved, the slot layout).  With u8 codes ``packed`` may be None
+    (codes only)."""
+    device = require_device(absmax, "absmax")
     b = blocks.to(device=device, dtype=torch.int32).contiguous()
     n = int(b.numel())
     q8 = absmax.dtype == torch.uint8
-    out_p = torch.empty((n, BLOCK * int(in_features) // 2), dtype=torch.uint8, device=device)
-    out_a = torch.empty((n, BLOCK * int(in_features) // int(qbs)), dtype=absmax.dtype if q8 else torch.float32,
-                        device=device)
-    src_blocks = int(packed.numel()) // (BLOCK * int(in_features) // 2)
-    _lib.call("nsmlp_gather_row_blocks_q8" if q8 else "nsmlp_gather_row_blocks", ptr(packed), ptr(absmax),
-              src_blocks, ptr(b), n, int(in_features), int(qbs), ptr(out_p), ptr(out_a), stream_handle(device))
+    A = int(in_features) // int(qbs)
+    src_blocks = int(absmax.numel()) // (BLOCK * A)
+    if packed is None and not q8:
+        raise RuntimeError("packed is required with fp32 absmax")
+    out_p = None if packed is None else torch.empty((n, BLOCK * int(in_features) // 2), dtype=torch.uint8,
+                                                    device=device)
+    if q8:
+        out_a = torch.empty((n, BLOCK // 2, A, 2), dtype=torch.uint8, device=device)
+        _lib.call("nsmlp_gather_row_blocks_q8", ptr(packed), ptr(absmax), src_blocks, ptr(b), n, int(in_features),
+                  int(qbs), ptr(out_p), ptr(out_a), stream_handle(device))
+    else:
+        out_a = torch.empty((n, BLOCK * A), dtype=torch.float32, device=device)
+        _lib.call("nsmlp_gather_row_blocks", ptr(packed), ptr(absmax), src_blocks, ptr(b), n, int(in_features),
+                  int(qbs), ptr(out_p), ptr(out_a), stream_handle(device))
     return out_p, out_a
 
 
@@ -183,9 +193,13 @@ class SparseMlpSlotTable:
         all_blocks = torch.arange(NB, dtype=torch.int32, device=device)
         if resident_blocks is None:
             t.gate_packed = gate_packed.view(NB, BLOCK * H // 2)
-            t.gate_absmax = gate_absmax.view(NB, BLOCK * H // qbs)
             t.up_packed = up_packed.view(NB, BLOCK * H // 2)
-            t.up_absmax = up_absmax.view(NB, BLOCK * H // qbs)
+            if t.nested is not None:  # codes in the interleaved slot layout
+                t.gate_absmax = gather_row_blocks(None, gate_absmax, all_blocks, H, qbs)[1]
+                t.up_absmax = gather_row_blocks(None, up_absmax, all_blocks, H, qbs)[1]
+            else:
+                t.gate_absmax = gate_absmax.view(NB, BLOCK * H // qbs)
+                t.up_absmax = up_absmax.view(NB, BLOCK * H // qbs)
             t.down_packed, t.down_absmax = gather_down_columns(down_packed, down_absmax, all_blocks, H, I, qbs)
             t.lookup = None
             t.block_ids = all_blocks.to("cpu", torch.long)
@@ -200,9 +214,14 @@ class SparseMlpSlotTable:
             t.block_ids = res.to("cpu", torch.long)
         if host_copy:
             dp, da = gather_down_columns(down_packed, down_absmax, all_blocks, H, I, qbs)
+            if t.nested is not None:
+                ga_h = gather_row_blocks(None, gate_absmax, all_blocks, H, qbs)[1]
+                ua_h = gather_row_blocks(None, up_absmax, all_blocks, H, qbs)[1]
+            else:
+                ga_h, ua_h = gate_absmax.view(NB, -1), up_absmax.view(NB, -1)
             srcs = {
-                "gate_packed": gate_packed.view(NB, -1), "gate_absmax": gate_absmax.view(NB, -1),
-                "up_packed": up_packed.view(NB, -1), "up_absmax": up_absmax.view(NB, -1),
+                "gate_packed": gate_packed.view(NB, -1), "gate_absmax": ga_h,
+                "up_packed": up_packed.view(NB, -1), "up_absmax": ua_h,
                 "down_packed": dp, "down_absmax": da,
             }
             for name, src in srcs.items():

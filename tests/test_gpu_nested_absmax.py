@@ -50,8 +50,12 @@ def test_q8_gathers_match_reference_slicing(gpu, orc):
     rp, rq = gather_row_blocks(t(gp), t(gq), t(blocks), H, qbs)
     dpk, dqk = gather_down_columns(t(dp), t(dq), t(blocks), H, I, qbs)
     torch.cuda.synchronize()
-    gq2 = gq.reshape(NB, -1)
-    assert rq.dtype == torch.uint8 and np.array_equal(_np(rq), gq2[blocks])
+    gq2 = gq.reshape(NB, 32, H // qbs)[blocks]
+    # slot layout: rows 2p and 2p+1 interleaved, [n, 16, H/qbs, 2]
+    exp_q = np.stack([gq2[:, 0::2, :], gq2[:, 1::2, :]], axis=-1)
+    assert rq.dtype == torch.uint8 and np.array_equal(_np(rq), exp_q)
+    _, rq_only = gather_row_blocks(None, t(gq), t(blocks), H, qbs)
+    assert torch.equal(rq_only, rq)
     assert np.array_equal(_np(rp), gp.reshape(NB, -1)[blocks])
     dq2 = dq.reshape(H, I // qbs)
     assert dqk.dtype == torch.uint8 and np.array_equal(_np(dqk), dq2[:, (blocks * 32) // qbs].T)
