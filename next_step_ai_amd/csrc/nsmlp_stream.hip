@@ -432,7 +432,13 @@ __global__ void __launch_bounds__(kThreads8, 2) k_down_rep(DecodeArgs a) {
   const int tid = threadIdx.x, lane = tid & (kWave - 1);
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int GX = a.st_dn_gx, per = a.st_dn_per;
-  const int gx = (int)blockIdx.x % GX, c = (int)blockIdx.x / GX;
+  // XCD-aware mapping: workgroups go to the 8 XCDs round-robin (b % 8);
+  // chunks 2m and 2m+1 share the 128-byte lines of the absmax codes, so
+  // both are given to workgroups of one XCD (one L2).  The grid size
+  // (H / 64) GX is a multiple of 16 (H a multiple of 2048).
+  const uint32_t xcd = blockIdx.x & 7u, sidx = blockIdx.x >> 3;
+  const uint32_t m = xcd + 8u * (sidx >> 1);
+  const int gx = (int)(m % (uint32_t)GX), c = 2 * (int)(m / (uint32_t)GX) + (int)(sidx & 1u);
   const int nbw_all = (a.k + GX - 1) / GX;
   const int jb0 = gx * nbw_all;
   const int nbw = max(0, min(a.k - jb0, nbw_all));  // blocks of this workgroup
@@ -462,10 +468,11 @@ __global__ void __launch_bounds__(kThreads8, 2) k_down_rep(DecodeArgs a) {
   float c2v = 0.0f, a2v[2] = {0.0f, 0.0f};
   if constexpr (DQ) {
     c2v = a.down.code2[tid & 255];
-    const uint32_t last = (uint32_t)((((long long)a.H * Ad) - 1) >> a.dq_shift);
+    // entries g_lo .. g_lo + st_dn_a2n - 1 (clamped: unconditional loads)
+    const uint32_t last = min((uint32_t)((((long long)a.H * Ad) - 1) >> a.dq_shift), g_lo + a.st_dn_a2n - 1);
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
-      const uint32_t g = min(g_lo + (uint32_t)(tid + h * kThreads8), last);  // clamped: unconditional load
+      const uint32_t g = min(g_lo + (uint32_t)(tid + h * kThreads8), last);
       a2v[h] = a.down.absmax2[g];
     }
   }
