@@ -26,6 +26,12 @@ compress_statistics: u8 codes, one fp32 scale per 256, an offset), the format
 the workload names; --absmax f32 stores the resolved fp32 absmax instead (the
 reference runtime's slot-table format, RT:4621-4625).
 
+--config 3 measures the same layer with half of the blocks in HBM slots and
+the selected blocks' misses (62 of 208) read from pinned host copies over
+the host link; --config 5 decodes 64 tokens through a stack of 126 resident
+layers (x <- x + mlp(x)) and reports the end-to-end decode_tok_s.  Both
+print the same JSON line shape with their own config.
+
 --copy-calibration BYTES runs only a plain device copy of BYTES (the
 reference kernel for the counter calibration) and prints its size.
 """
@@ -46,11 +52,19 @@ METRIC = "sparse-MLP µs/layer + HBM GB/s vs peak, 405B shape top-k 208; decode_
 PEAK_GBS = 8000.0
 MODEL_LAYERS = 126
 # config id -> (hidden, intermediate, basis rank, top-k)
-CONFIGS = {1: (4096, 14336, 64, 64), 2: (16384, 53248, 64, 208)}
+CONFIGS = {1: (4096, 14336, 64, 64), 2: (16384, 53248, 64, 208), 3: (16384, 53248, 64, 208),
+           5: (16384, 53248, 64, 208)}
 WORKLOADS = {
     1: "8B-shaped MLP layer decode: hidden 4096, intermediate 14336, block 32 (448 blocks), top-k 64",
     2: "405B-shaped MLP layer decode: hidden 16384, intermediate 53248, block 32 (1664 blocks), top-k 208",
+    3: "405B-shaped MLP layer decode with partial residency: hidden 16384, intermediate 53248, top-k 208; "
+       "832 of 1664 blocks in HBM slots, 62 of the 208 selected blocks read from pinned host copies",
+    5: "126-layer stack of 405B-shaped MLP layers (hidden 16384, intermediate 53248, top-k 208), all resident; "
+       "64 decode tokens at batch 1, x <- x + mlp(x) per layer",
 }
+STACK_LAYERS = 126
+STACK_TOKENS = 64
+C3_RESIDENT, C3_MISSES = 832, 62
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic_sparse_mlp_decode.json")
 
 
@@ -175,6 +189,160 @@ def copy_calibration(nbytes: int) -> int:
     return 0
 
 
+def base_result(args, value: float, us_per_layer: float, H: int, I: int, R: int, k: int, qbs: int) -> dict:
+    return {
+        "metric": METRIC,
+        "value": round(value, 3),
+        "unit": "tok/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(us_per_layer / 1e3, 6),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "nf4(u8)*f16->f32",
+        "data": "synthetic",
+        "config": {
+            "workload": WORKLOADS[args.config] + f"; NF4 qbs {qbs} with "
+                        + ("double-quantised absmax (u8, fp32 per 256, offset)" if args.absmax == "dq8"
+                           else "fp32 absmax"),
+            "hidden": H, "intermediate": I, "basis_rank": R, "top_k": k, "block": 32, "quant_block": qbs,
+            "absmax": args.absmax,
+        },
+    }
+
+
+def run_partial(args) -> int:
+    """Config 3: half of the blocks resident, 62 of the 208 selected blocks
+    served from pinned host copies (read by the kernels over the host link)."""
+    import numpy as np
+    import torch
+
+    from next_step_ai_amd._runtime import workspace
+    from next_step_ai_amd.router import route_tokens
+    from next_step_ai_amd.slot_table import SparseMlpLayer
+    from next_step_ai_amd.synth import make_synthetic_layer
+
+    device = torch.device("cuda", 0)
+    torch.cuda.set_device(device)
+    H, I, R, k = CONFIGS[3]
+    qbs, NB = 64, I // 32
+    n_layers = min(args.layers, 4)  # each keeps a pinned host copy of all its blocks
+    layers = []
+    for l in range(n_layers):
+        L = make_synthetic_layer(H=H, I=I, R=R, seed=3000 + l, device=device, double_quant=args.absmax == "dq8",
+                                 keep_f32_absmax=args.absmax == "f32")
+        sel = route_tokens(L.x.reshape(1, H), L.routing_dict(k), k, sorted_by_score=False).reshape(-1)
+        sel_np = sel.cpu().numpy().astype(np.int64)
+        rng = np.random.default_rng(3000 + l)
+        hit = sel_np[rng.permutation(k)[: k - C3_MISSES]]
+        others = np.setdiff1d(np.arange(NB), sel_np)
+        resident = np.concatenate([hit, rng.choice(others, size=C3_RESIDENT - hit.size, replace=False)])
+        L.table = L.slot_table(resident_blocks=torch.from_numpy(resident), host_copy=True, drop_reference_down=True)
+        L.mlp = SparseMlpLayer(L.router(), L.table, k)
+        misses = int((L.table.lookup_cpu()[torch.from_numpy(sel_np)] < 0).sum())
+        assert misses == C3_MISSES, misses
+        layers.append(L)
+        print(f"[bench] config 3 layer {l}: {misses} of {k} selected blocks on the host", file=sys.stderr, flush=True)
+    outs = [torch.empty(H, dtype=torch.float16, device=device) for _ in layers]
+    sels = [torch.empty(k, dtype=torch.int32, device=device) for _ in layers]
+    ws = workspace(layers[0].mlp.workspace_bytes(), device)
+    n = len(layers)
+    for i in range(args.warmup):
+        layers[i % n].mlp.forward(layers[i % n].x, out=outs[i % n], sel_out=sels[i % n], ws=ws)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        layers[i % n].mlp.forward(layers[i % n].x, out=outs[i % n], sel_out=sels[i % n], ws=ws)
+    torch.cuda.synchronize()
+    us = (time.perf_counter() - t0) / args.steps * 1e6
+    per_block = algorithmic_bytes(H, I, 1, qbs, args.absmax) - algorithmic_bytes(H, I, 0, qbs, args.absmax)
+    miss_bytes = C3_MISSES * per_block
+    hit_bytes = algorithmic_bytes(H, I, k, qbs, args.absmax) - miss_bytes
+    res = base_result(args, 1e6 / (MODEL_LAYERS * us), us, H, I, R, k, qbs)
+    res["config"].update({"resident_blocks": C3_RESIDENT, "host_misses": C3_MISSES, "rotating_layers": n})
+    res.update({
+        "us_per_layer": round(us, 3),
+        "hbm_hit_bytes_per_layer": hit_bytes,
+        "host_miss_bytes_per_layer": miss_bytes,
+        # the host link carries the misses: their bytes over the whole layer
+        # time is a lower bound of the link rate reached
+        "host_link_gbs_lower_bound": round(miss_bytes / (us * 1e-6) / 1e9, 2),
+        "note": "misses are read by the kernels from pinned host memory (zero-copy); the layer time is "
+                "host-link bound, so the HBM roofline does not apply to this config",
+    })
+    print(json.dumps(res), flush=True)
+    return 0
+
+
+def run_stack(args) -> int:
+    """Config 5: 126 resident layers, 64 decode tokens through all of them."""
+    import torch
+
+    from next_step_ai_amd._runtime import workspace
+    from next_step_ai_amd.slot_table import SparseMlpLayer
+    from next_step_ai_amd.synth import make_synthetic_layer, sub_seed, synth_normal_f16
+
+    device = torch.device("cuda", 0)
+    torch.cuda.set_device(device)
+    H, I, R, k = CONFIGS[5]
+    qbs = 64
+    t_gen = time.perf_counter()
+    mlps = []
+    for l in range(STACK_LAYERS):
+        L = make_synthetic_layer(H=H, I=I, R=R, seed=5000 + l, device=device, double_quant=args.absmax == "dq8",
+                                 keep_f32_absmax=args.absmax == "f32")
+        table = L.slot_table(drop_reference_down=True)
+        mlps.append(SparseMlpLayer(L.router(), table, k))
+        del L
+        if (l + 1) % 16 == 0 or l + 1 == STACK_LAYERS:
+            torch.cuda.synchronize()
+            print(f"[bench] config 5: {l + 1}/{STACK_LAYERS} layers generated "
+                  f"({torch.cuda.memory_allocated(device) / 2**30:.1f} GiB), {time.perf_counter() - t_gen:.0f}s",
+                  file=sys.stderr, flush=True)
+    tokens = [synth_normal_f16(sub_seed(5000 + t, "x"), (H,), 1.0, device) for t in range(STACK_TOKENS + args.warmup)]
+    ws = workspace(mlps[0].workspace_bytes(), device)
+    out = torch.empty(H, dtype=torch.float16, device=device)
+    sel = torch.empty(k, dtype=torch.int32, device=device)
+    xa = torch.empty(H, dtype=torch.float16, device=device)
+    xb = torch.empty(H, dtype=torch.float16, device=device)
+
+    def token(x0):
+        xa.copy_(x0)
+        x, y = xa, xb
+        for m in mlps:
+            m.forward(x, out=out, sel_out=sel, ws=ws)
+            torch.add(x, out, out=y)  # the residual add of the decode loop
+            x, y = y, x
+        return x
+
+    for t in range(args.warmup):
+        token(tokens[STACK_TOKENS + t])
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for t in range(STACK_TOKENS):
+        token(tokens[t])
+    torch.cuda.synchronize()
+    dt = time.perf_counter() - t0
+    tok_s = STACK_TOKENS / dt
+    us_layer = dt / (STACK_TOKENS * STACK_LAYERS) * 1e6
+    layer_bytes = algorithmic_bytes(H, I, k, qbs, args.absmax) + router_bytes(H, R, I // 32)
+    res = base_result(args, tok_s, us_layer, H, I, R, k, qbs)
+    res["steps"] = STACK_TOKENS
+    res["config"].update({"layers": STACK_LAYERS, "tokens": STACK_TOKENS,
+                          "resident_bytes": int(torch.cuda.memory_allocated(device))})
+    res.update({
+        "us_per_layer": round(us_layer, 3),
+        "decode_tok_s_126_layers": round(tok_s, 3),
+        "aggregate_hbm_gbs": round(layer_bytes * STACK_TOKENS * STACK_LAYERS / dt / 1e9, 2),
+        "algorithmic_bytes_per_layer": layer_bytes,
+        "generation_s": round(time.perf_counter() - t_gen - dt, 1),
+    })
+    print(json.dumps(res), flush=True)
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -194,6 +362,10 @@ def main() -> int:
         return 2
     if args.copy_calibration > 0:
         return copy_calibration(args.copy_calibration)
+    if args.config == 3:
+        return run_partial(args)
+    if args.config == 5:
+        return run_stack(args)
 
     import torch
 
