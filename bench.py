@@ -53,12 +53,16 @@ PEAK_GBS = 8000.0
 MODEL_LAYERS = 126
 # config id -> (hidden, intermediate, basis rank, top-k)
 CONFIGS = {1: (4096, 14336, 64, 64), 2: (16384, 53248, 64, 208), 3: (16384, 53248, 64, 208),
-           5: (16384, 53248, 64, 208)}
+           4: (16384, 53248, 64, 208), 5: (16384, 53248, 64, 208)}
+PREFILL_TOKENS = 256
+PEAK_F16_TFLOPS = 2500.0  # dense fp16 MFMA
 WORKLOADS = {
     1: "8B-shaped MLP layer decode: hidden 4096, intermediate 14336, block 32 (448 blocks), top-k 64",
     2: "405B-shaped MLP layer decode: hidden 16384, intermediate 53248, block 32 (1664 blocks), top-k 208",
     3: "405B-shaped MLP layer decode with partial residency: hidden 16384, intermediate 53248, top-k 208; "
        "832 of 1664 blocks in HBM slots, 62 of the 208 selected blocks read from pinned host copies",
+    4: "405B-shaped MLP chunked prefill: 256 tokens, per-token top-208 routing unioned into a block set, "
+       "grouped fp16 MFMA gate/up/down with SiLU fused (hidden 16384, intermediate 53248, block 32)",
     5: "126-layer stack of 405B-shaped MLP layers (hidden 16384, intermediate 53248, top-k 208), all resident; "
        "64 decode tokens at batch 1, x <- x + mlp(x) per layer",
 }
@@ -276,6 +280,73 @@ def run_partial(args) -> int:
     return 0
 
 
+def run_prefill(args) -> int:
+    """Config 4: 256-token chunked prefill through one layer: per-token routing
+    plus the grouped MFMA MLP over the union of the selected blocks."""
+    import torch
+
+    from next_step_ai_amd.synth import make_synthetic_layer, sub_seed, synth_normal_f16
+
+    device = torch.device("cuda", 0)
+    torch.cuda.set_device(device)
+    H, I, R, k = CONFIGS[4]
+    qbs, NB, M = 64, I // 32, PREFILL_TOKENS
+    n_layers = min(args.layers, 3)
+    layers = []
+    for l in range(n_layers):
+        L = make_synthetic_layer(H=H, I=I, R=R, seed=4000 + l, device=device, double_quant=args.absmax == "dq8",
+                                 keep_f32_absmax=args.absmax == "f32")
+        L.table = L.slot_table(drop_reference_down=True)
+        L.xs = synth_normal_f16(sub_seed(4000 + l, "x"), (M, H), 1.0, device)
+        L.sel = L.router().route(L.xs, k)
+        layers.append(L)
+    routers = [L.router() for L in layers]
+    outs = [torch.empty((M, H), dtype=torch.float16, device=device) for _ in layers]
+    n = len(layers)
+    steps = max(1, args.steps // 10)  # a prefill step is ~100x a decode step
+    for i in range(max(1, args.warmup // 10)):
+        L = layers[i % n]
+        L.table.prefill(L.xs, routers[i % n].route(L.xs, k), out=outs[i % n])
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(steps):
+        L = layers[i % n]
+        L.table.prefill(L.xs, routers[i % n].route(L.xs, k), out=outs[i % n])
+    torch.cuda.synchronize()
+    step_us = (time.perf_counter() - t0) / steps * 1e6
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
+    for i in range(steps):
+        L = layers[i % n]
+        ev[i][0].record()
+        L.table.prefill(L.xs, L.sel, out=outs[i % n])
+        ev[i][1].record()
+    torch.cuda.synchronize()
+    mlp_us = statistics.mean(a.elapsed_time(b) for a, b in ev) * 1e3
+    union = [int(torch.unique(L.sel).numel()) for L in layers]
+    per_block = algorithmic_bytes(H, I, 1, qbs, args.absmax) - algorithmic_bytes(H, I, 0, qbs, args.absmax)
+    ubytes = int(statistics.mean(union)) * per_block + 2 * 2 * M * H
+    useful_flop = 2.0 * 3 * M * k * 32 * H
+    res = base_result(args, M / (step_us * 1e-6), step_us, H, I, R, k, qbs)
+    res["unit"] = "tok/s"
+    res["steps"] = steps
+    res["config"].update({"tokens": M, "union_blocks": union, "rotating_layers": n})
+    res.update({
+        "prefill_us_per_layer": round(step_us, 3),
+        "prefill_mlp_us": round(mlp_us, 3),
+        "route_us": round(max(0.0, step_us - mlp_us), 3),
+        "prefill_tok_s_per_layer": round(M / (step_us * 1e-6), 1),
+        "union_bytes": ubytes,
+        "roofline": {"bound": "hbm", "achieved": round(ubytes / (mlp_us * 1e-6) / 1e9, 2), "peak": PEAK_GBS,
+                     "unit": "GB/s", "frac": round(ubytes / (mlp_us * 1e-6) / 1e9 / PEAK_GBS, 4), "traffic": None,
+                     "kernels": "k_pf_mark + k_pf_csr + k_pf_gu + k_pf_down"},
+        "mfma": {"useful_tflops": round(useful_flop / (mlp_us * 1e-6) / 1e12, 2), "peak_tflops": PEAK_F16_TFLOPS,
+                 "frac": round(useful_flop / (mlp_us * 1e-6) / 1e12 / PEAK_F16_TFLOPS, 4),
+                 "useful_flop": useful_flop},
+    })
+    print(json.dumps(res), flush=True)
+    return 0
+
+
 def run_stack(args) -> int:
     """Config 5: 126 resident layers, 64 decode tokens through all of them."""
     import torch
@@ -364,6 +435,8 @@ def main() -> int:
         return copy_calibration(args.copy_calibration)
     if args.config == 3:
         return run_partial(args)
+    if args.config == 4:
+        return run_prefill(args)
     if args.config == 5:
         return run_stack(args)
 

@@ -65,7 +65,10 @@ int nsmlp_version(void);
 /* 1 if device `device` is a gfx950 GPU usable by this library, else 0. */
 int nsmlp_device_supported(int device);
 
-/* Zero the counter region of a workspace; call once after allocating it. */
+/* Zero the counter region of a workspace; call once after allocating it.
+ * The first int32 of a workspace is a status word: the kernels set bit 0 when
+ * a selected block id is out of range, or not resident with no host copy
+ * (such a block contributes zero).  It stays set until the caller clears it. */
 int nsmlp_workspace_init(void* ws, size_t ws_bytes, void* stream);
 
 /* ------------------------------------------------------------------ router
@@ -176,6 +179,20 @@ int nsmlp_decode_layer_f16(const nsmlp_router* router, const nsmlp_slot_table* t
  * out_accum [>= H] f32 receives the fp32 result before rounding (the
  * reference's scratch, TSM:1476-1508).  block_size must be 32.
  */
+/* Chunked prefill over a slot table: M tokens, each with its own k selected
+ * blocks (the multi-token decode branch, RT:4857-4908 + RT:5104-5524 with the
+ * per-row mask of RT:5453: a token's gate/up are masked to its own blocks):
+ *   out[t] = sum over b in sel[t] of Wd_b (silu(Wg_b x_t) * (Wu_b x_t))
+ * x [M][H] fp16 (16-byte aligned), sel [M][k] int32 block ids (e.g. from
+ * nsmlp_route_f16 with rows = M; an id repeated in a row counts once), out
+ * [M][H] fp16.  Grouped per block on MFMA: fp16 operands (the weights as
+ * fp16(code * absmax), as the reference's dequant fallback rounds them,
+ * RT:5439-5447), fp32 accumulation, act rounded to fp16 (RT:5459), the down
+ * sums accumulated in fixed point (independent of scheduling).  M <= 65536. */
+size_t nsmlp_prefill_workspace_bytes(int H, int NB, int M, int k);
+int nsmlp_prefill_slots_f16(const nsmlp_slot_table* table, const void* x, int M, const int32_t* sel, int k, void* out,
+                            void* ws, size_t ws_bytes, void* stream);
+
 size_t nsmlp_single_kernel_workspace_bytes(int H, int top_k);
 int nsmlp_single_kernel_decode_f16(const void* x, const uint8_t* gate_packed, const float* gate_absmax,
                                    const float* gate_code, const uint8_t* up_packed, const float* up_absmax,

@@ -16,7 +16,8 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 BUILD = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libnsmlp.so")
-SOURCES = ["nsmlp_capi.hip", "nsmlp_router.hip", "nsmlp_decode.hip", "nsmlp_stream.hip", "nsmlp_ops.hip"]
+SOURCES = ["nsmlp_capi.hip", "nsmlp_router.hip", "nsmlp_decode.hip", "nsmlp_stream.hip", "nsmlp_ops.hip",
+           "nsmlp_prefill.hip"]
 
 ARCH = "gfx950"
 HIPCC_FLAGS = [

@@ -479,6 +479,61 @@ int nsmlp_decode_layer_f16(const nsmlp_router* router, const nsmlp_slot_table* t
   return run_decode(a, s);
 }
 
+size_t nsmlp_prefill_workspace_bytes(int H, int NB, int M, int k) {
+  if (H <= 0 || NB <= 0 || M <= 0 || k <= 0) return 0;
+  const size_t words = (size_t)(M + 31) / 32, TG = (size_t)(M + 127) / 128, nk = (size_t)M * (size_t)k;
+  size_t off = align_up(kCounterBytes);
+  off += align_up((size_t)NB * words * 4);        // bitmap
+  off += align_up(((size_t)NB + 1) * 4);          // offsets
+  off += align_up((size_t)NB * (TG + 1) * 4);     // group starts
+  off += align_up(nk * 4);                         // tokens
+  off += align_up(nk * 32 * 2);                    // act
+  return off;
+}
+
+int nsmlp_prefill_slots_f16(const nsmlp_slot_table* table, const void* x, int M, const int32_t* sel, int k, void* out,
+                            void* ws, size_t ws_bytes, void* stream) {
+  PrefillArgs p;
+  memset(&p, 0, sizeof(p));
+  int rc = table_to_args(table, p.d);
+  if (rc) return rc;
+  rc = validate_decode_shape(p.d.H, p.d.qbs, k);
+  if (rc) return rc;
+  if (M <= 0 || M > 65536) return set_error(NSMLP_EINVAL, "M=%d out of range [1, 65536]", M);
+  if ((long long)M * p.d.H * 2 >= (1LL << 31) || (long long)M * k * 64 >= (1LL << 31))
+    return set_error(NSMLP_EINVAL, "M=%d too large for one prefill call at H=%d, k=%d (split the tokens)", M, p.d.H, k);
+  if (k > p.d.NB) return set_error(NSMLP_EINVAL, "k=%d exceeds num_blocks=%d", k, p.d.NB);
+  if (!x || !sel || !out) return set_error(NSMLP_EINVAL, "x, sel and out must be non-NULL");
+  if (!aligned16(x)) return set_error(NSMLP_EINVAL, "x must be 16-byte aligned");
+  const size_t need = nsmlp_prefill_workspace_bytes(p.d.H, p.d.NB, M, k);
+  if (ws == nullptr || ws_bytes < need)
+    return set_error(NSMLP_ENOSPC, "prefill workspace needs %zu bytes, got %zu", need, ws_bytes);
+  if (((uintptr_t)ws & (kAlign - 1)) != 0) return set_error(NSMLP_EINVAL, "workspace must be 256-byte aligned");
+  char* base = (char*)ws;
+  p.d.status = (int*)(base + kStatusOff);
+  p.d.qbs_shift = __builtin_ctz((unsigned)p.d.qbs);
+  p.x = (const uint16_t*)x;
+  p.M = M;
+  p.sel = sel;
+  p.k = k;
+  p.out = (uint16_t*)out;
+  p.words = (M + 31) / 32;
+  p.TG = (M + 127) / 128;
+  const size_t nk = (size_t)M * (size_t)k;
+  size_t off = align_up(kCounterBytes);
+  p.bitmap = (uint32_t*)(base + off);
+  off += align_up((size_t)p.d.NB * p.words * 4);
+  p.offsets = (int32_t*)(base + off);
+  off += align_up(((size_t)p.d.NB + 1) * 4);
+  p.grp = (int32_t*)(base + off);
+  off += align_up((size_t)p.d.NB * (p.TG + 1) * 4);
+  p.tokens = (int32_t*)(base + off);
+  off += align_up(nk * 4);
+  p.act = (uint16_t*)(base + off);
+  launch_prefill(p, (hipStream_t)stream);
+  return check_launch("prefill");
+}
+
 size_t nsmlp_single_kernel_workspace_bytes(int H, int top_k) { return decode_ws_layout(H, top_k).total; }
 
 int nsmlp_single_kernel_decode_f16(const void* x, const uint8_t* gate_packed, const float* gate_absmax,

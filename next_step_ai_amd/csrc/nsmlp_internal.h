@@ -325,6 +325,50 @@ __device__ __forceinline__ void st_coherent_i32(int* p, int v) {
 
 __device__ __forceinline__ float silu_mul(float g, float u) { return g / (1.0f + __expf(-g)) * u; }
 
+// ---------------------------------------------------------- buffer loads --
+// Weight streams use raw buffer loads through per-block descriptors: a
+// descriptor whose extent is zero (or an offset past the extent) makes the
+// load return zeros without touching memory, so loads stay unconditional and
+// the compiler's wait counts stay exact (a branch around a load makes it wait
+// for every load in flight).
+// Keeps the compiler from moving instructions across this point (load issue
+// order decides which waits drain the weight stream).
+__device__ __forceinline__ void sched_fence() { __builtin_amdgcn_sched_barrier(0); }
+
+// Raw buffer descriptors (gfx9 family dword format) and nontemporal loads.
+typedef __amdgpu_buffer_rsrc_t rsrc_t;
+constexpr int kRsrcWord3 = 0x00020000;
+constexpr int kNontemporal = 2;
+
+__device__ __forceinline__ rsrc_t make_rsrc(const void* base, int bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, bytes, kRsrcWord3);
+}
+__device__ __forceinline__ uint4 buf_ld16(rsrc_t r, uint32_t voff, uint32_t soff) {
+  const u32x4_t t = __builtin_amdgcn_raw_buffer_load_b128(r, (int)voff, (int)soff, kNontemporal);
+  return make_uint4(t.x, t.y, t.z, t.w);
+}
+__device__ __forceinline__ float buf_ldf(rsrc_t r, uint32_t voff, uint32_t soff) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, (int)voff, (int)soff, kNontemporal));
+}
+__device__ __forceinline__ uint32_t buf_ldu8(rsrc_t r, uint32_t voff, uint32_t soff) {
+  return (uint32_t)__builtin_amdgcn_raw_buffer_load_b8(r, (int)voff, (int)soff, kNontemporal);
+}
+// Cached (temporal) variants, for data that other workgroups read again.
+__device__ __forceinline__ uint4 buf_ld16c(rsrc_t r, uint32_t voff, uint32_t soff) {
+  const u32x4_t t = __builtin_amdgcn_raw_buffer_load_b128(r, (int)voff, (int)soff, 0);
+  return make_uint4(t.x, t.y, t.z, t.w);
+}
+__device__ __forceinline__ int buf_ldic(rsrc_t r, uint32_t voff, uint32_t soff) {
+  return (int)__builtin_amdgcn_raw_buffer_load_b32(r, (int)voff, (int)soff, 0);
+}
+__device__ __forceinline__ float buf_ldfc(rsrc_t r, uint32_t voff, uint32_t soff) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, (int)voff, (int)soff, 0));
+}
+constexpr uint32_t kOffNone = 0x80000000u;  // an offset past every extent: the load returns zeros
+__device__ __forceinline__ uint32_t buf_ldu16(rsrc_t r, uint32_t voff, uint32_t soff) {
+  return (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(r, (int)voff, (int)soff, kNontemporal);
+}
+
 // ------------------------------------------------------------------ top-k --
 // Workgroup top-k of NB fp16 scores.  Keys are fp16 order keys; among equal
 // scores the lower block index ranks higher (the order of the unique key
@@ -542,6 +586,24 @@ __device__ __forceinline__ BlockRef resolve_id(const DecodeArgs& a, int b) {
 __device__ __forceinline__ BlockRef resolve_block(const DecodeArgs& a, int j) {
   return resolve_id(a, a.sel ? a.sel[j] : j);
 }
+
+// Chunked prefill (M tokens, per-token block sets) over a slot table.
+struct PrefillArgs {
+  DecodeArgs d;           // slot table views, H, qbs, NB, code, dq state, status
+  const uint16_t* x;      // [M][H] fp16
+  int M;
+  const int32_t* sel;     // [M][k] block ids
+  int k;
+  uint16_t* out;          // [M][H] fp16
+  uint32_t* bitmap;       // [NB][words]
+  int words;              // ceil(M / 32)
+  int32_t* offsets;       // [NB + 1] CSR offsets
+  int32_t* grp;           // [NB][TG + 1] CSR index of the first token of each 128-token group
+  int TG;                 // token groups
+  int32_t* tokens;        // [M k] token ids per block, ascending
+  uint16_t* act;          // [M k][32] fp16 silu(gate) * up per (block, token) entry
+};
+void launch_prefill(const PrefillArgs& p, hipStream_t s);
 
 void launch_decode_gate_up(const DecodeArgs& a, hipStream_t s);
 void launch_decode_down(const DecodeArgs& a, hipStream_t s);

@@ -91,32 +91,6 @@ __device__ __forceinline__ void lds_barrier() {
   asm volatile("" ::: "memory");
 }
 
-// Keeps the compiler from moving instructions across this point (load issue
-// order decides which waits drain the weight stream).
-__device__ __forceinline__ void sched_fence() { __builtin_amdgcn_sched_barrier(0); }
-
-// Raw buffer descriptors (gfx9 family dword format) and nontemporal loads.
-typedef __amdgpu_buffer_rsrc_t rsrc_t;
-constexpr int kRsrcWord3 = 0x00020000;
-constexpr int kNontemporal = 2;
-
-__device__ __forceinline__ rsrc_t make_rsrc(const void* base, int bytes) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, bytes, kRsrcWord3);
-}
-__device__ __forceinline__ uint4 buf_ld16(rsrc_t r, uint32_t voff, uint32_t soff) {
-  const u32x4_t t = __builtin_amdgcn_raw_buffer_load_b128(r, (int)voff, (int)soff, kNontemporal);
-  return make_uint4(t.x, t.y, t.z, t.w);
-}
-__device__ __forceinline__ float buf_ldf(rsrc_t r, uint32_t voff, uint32_t soff) {
-  return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, (int)voff, (int)soff, kNontemporal));
-}
-__device__ __forceinline__ uint32_t buf_ldu8(rsrc_t r, uint32_t voff, uint32_t soff) {
-  return (uint32_t)__builtin_amdgcn_raw_buffer_load_b8(r, (int)voff, (int)soff, kNontemporal);
-}
-__device__ __forceinline__ uint32_t buf_ldu16(rsrc_t r, uint32_t voff, uint32_t soff) {
-  return (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(r, (int)voff, (int)soff, kNontemporal);
-}
-
 // Replicated pair table, filled by 512 threads in 8 passes of one 16-byte LDS
 // write each: pass ps writes entry e = 32 ps + tid / 16, copies 4 (tid % 16)
 // .. +3 (copies 0..31 decode code_a, 32..63 code_b).  The entry's low half is

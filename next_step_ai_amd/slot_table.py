@@ -281,6 +281,25 @@ class SparseMlpSlotTable:
         return out
 
 
+    def prefill(self, x: torch.Tensor, sel: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
+        """M tokens ``x`` [M, H] with their own selected block ids ``sel``
+        [M, k] (the multi-token branch, RT:4857-4908 + RT:5453): grouped MFMA
+        gate/up/down over the union of the selected blocks; ``out`` [M, H] fp16."""
+        x16 = x.reshape(-1, self.H).to(device=self.device, dtype=torch.float16).contiguous()
+        s = sel.to(device=self.device, dtype=torch.int32).contiguous()
+        M, k = int(x16.shape[0]), int(s.shape[-1])
+        if int(s.numel()) != M * k:
+            raise RuntimeError(f"sel has {int(s.numel())} entries, expected M*k = {M}*{k}")
+        if out is None:
+            out = torch.empty((M, self.H), dtype=torch.float16, device=self.device)
+        nbytes = int(_lib.lib().nsmlp_prefill_workspace_bytes(self.H, self.NB, M, k))
+        ws = workspace(nbytes, self.device)
+        st = self._struct if self._struct is not None else self.as_struct()
+        _lib.call("nsmlp_prefill_slots_f16", ctypes.byref(st), ptr(x16), M, ptr(s), k, ptr(out), ptr(ws), ws.numel(),
+                  stream_handle(self.device))
+        return out
+
+
 class SparseMlpRouter:
     """Device copy of one layer's router (fp16, as the runtime casts it, RT:850-891)."""
 
@@ -298,6 +317,21 @@ class SparseMlpRouter:
         self.NB = int(self.score_w.shape[0])
         self.basis_top_k = self.R if basis_top_k is None else max(1, min(int(basis_top_k), self.R))
         self.legacy_abs = bool(legacy_abs)
+
+    def route(self, x: torch.Tensor, k: int, *, sorted_by_score: bool = False) -> torch.Tensor:
+        """Top-k blocks of every row of ``x`` [M, H]: ``sel`` [M, k] int32
+        (ascending ids, or torch.topk order with ``sorted_by_score``)."""
+        x16 = x.reshape(-1, int(self.enc_w.shape[1])).to(device=self.device, dtype=torch.float16).contiguous()
+        M, H = int(x16.shape[0]), int(x16.shape[1])
+        kk = max(1, min(int(k), self.NB))
+        flags = (_lib.NSMLP_ROUTE_SORTED if sorted_by_score else 0) | (_lib.NSMLP_ROUTE_LEGACY_ABS if self.legacy_abs
+                                                                       else 0)
+        sel = torch.empty((M, kk), dtype=torch.int32, device=self.device)
+        ws = workspace(int(_lib.lib().nsmlp_route_workspace_bytes(M, H, self.R, self.NB, kk)), self.device)
+        _lib.call("nsmlp_route_f16", ptr(x16), M, H, ptr(self.enc_w), ptr(self.enc_b), self.R, self.basis_top_k,
+                  ptr(self.score_w), ptr(self.score_b), ptr(self.dbn), self.NB,
+                  flags, kk, ptr(sel), None, None, ptr(ws), ws.numel(), stream_handle(self.device))
+        return sel
 
     def as_struct(self) -> _lib.Router:
         return _lib.Router(
@@ -339,3 +373,11 @@ class SparseMlpLayer:
         _lib.call("nsmlp_decode_layer_f16", ctypes.byref(self._r), ctypes.byref(self._t), ptr(x16), self.top_k,
                   ptr(sel_out), ptr(out), ptr(ws), ws.numel(), stream_handle(self.device))
         return out, sel_out
+
+    def prefill(self, x: torch.Tensor, out: torch.Tensor | None = None):
+        """M tokens [M, H]: per-token routing (ascending block ids), then the
+        grouped MFMA prefill over the union of the selected blocks.
+        Returns (out [M, H] fp16, sel [M, k] int32)."""
+        x16 = x.reshape(-1, self.table.H).to(device=self.device, dtype=torch.float16).contiguous()
+        sel = self.router.route(x16, self.top_k)
+        return self.table.prefill(x16, sel, out=out), sel
