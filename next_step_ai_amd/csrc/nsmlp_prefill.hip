@@ -16,7 +16,7 @@
 //               every block, act [tokens x 32] times the block's down columns
 //               [32 x 64 rows]; each tile is added into the group's [128][64]
 //               LDS accumulator at its tokens' rows as int64 fixed point
-//               (2^-40), so the sum does not depend on the order the waves
+//               (2^-31), so the sum does not depend on the order the waves
 //               add in; the result is rounded once to fp16.
 //
 // MFMA lane layout (16x16x32 f16, measured): A[i][k] and B[k][j] in lane l
@@ -38,7 +38,7 @@ constexpr int kPfThreads = 512;
 constexpr int kPfWaves = kPfThreads / kWave;
 constexpr int kChunk = 128;      // gate/up columns per wave step
 constexpr int kTokGroup = 128;   // tokens per down workgroup
-constexpr double kFix = 1099511627776.0;  // 2^40: down accumulator scale
+constexpr double kFixInv = 1.0 / 2147483648.0;  // down accumulator: int64 units of 2^-31
 
 __device__ __forceinline__ half8_t mfma_zero_h8() {
   half8_t h;
@@ -61,6 +61,16 @@ __device__ __forceinline__ half8_t deq8(uint32_t word, float am, const float* co
 }
 
 __device__ __forceinline__ half8_t as_h8(uint4 v) { return __builtin_bit_cast(half8_t, v); }
+
+// v * 2^31 truncated toward zero (|v| < 2^23), in fp32/int32 steps: hi =
+// trunc(v * 2^8) carries the bits above 2^-8, the remainder v - hi * 2^-8 is
+// exact and |rem| < 2^-8, so trunc(rem * 2^31) fits 23 bits.
+__device__ __forceinline__ long long to_fix31(float v) {
+  const int hi = (int)(v * 256.0f);
+  const float rem = __builtin_fmaf((float)hi, -0.00390625f, v);
+  const int lo = (int)(rem * 2147483648.0f);
+  return ((long long)hi << 23) + (long long)lo;
+}
 
 __device__ __forceinline__ float4_t mfma16(half8_t a, half8_t b, float4_t c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
@@ -203,7 +213,8 @@ __global__ void __launch_bounds__(kPfThreads, 2) k_pf_gu(PrefillArgs p) {
 #pragma unroll
       for (int nt = 0; nt < 4; ++nt) {
         const uint32_t r = (uint32_t)((nt & 1) * 16 + j);
-        w[st][nt] = buf_ld16(nt < 2 ? rg : ru, live ? r * (uint32_t)rs + (col >> 1) : kOffNone, 0);
+        // cached: the other tile waves of this K split read the same rows
+        w[st][nt] = buf_ld16c(nt < 2 ? rg : ru, live ? r * (uint32_t)rs + (col >> 1) : kOffNone, 0);
         if constexpr (DQ) {
           qa[st][nt] = buf_ldu8(nt < 2 ? rgq : ruq, live ? ((r >> 1) * A + ce) * 2u + (r & 1u) : kOffNone, 0);
           const uint32_t f = (32u * (uint32_t)b + r) * A + ce;
@@ -358,7 +369,8 @@ __global__ void __launch_bounds__(kPfThreads, 2) k_pf_down(PrefillArgs p) {
 #pragma unroll
       for (int nt = 0; nt < 4; ++nt) {
         const uint32_t o = (uint32_t)(o0 + nt * 16 + j);
-        st.w[nt] = __builtin_amdgcn_raw_buffer_load_b32(rw, (int)(o * 16u + 4u * g), 0, kNontemporal);
+        // cached: the other token groups of this row chunk read the same columns
+        st.w[nt] = __builtin_amdgcn_raw_buffer_load_b32(rw, (int)(o * 16u + 4u * g), 0, 0);
         if constexpr (DQ) {
           st.qa[nt] = buf_ldu8(ra, o, 0);
           const uint32_t f = o * Ad + ((32u * (uint32_t)b) >> d.qbs_shift);
@@ -414,8 +426,7 @@ __global__ void __launch_bounds__(kPfThreads, 2) k_pf_down(PrefillArgs p) {
                 const int tl = tk[r] - t0;
 #pragma unroll
                 for (int nt = 0; nt < 4; ++nt) {
-                  const long long fx = (long long)((double)c[nt][r] * kFix);
-                  atomicAdd(&acc_s[tl][nt * 16 + j], (unsigned long long)fx);
+                  atomicAdd(&acc_s[tl][nt * 16 + j], (unsigned long long)to_fix31(c[nt][r]));
                 }
               }
             }
@@ -430,7 +441,7 @@ __global__ void __launch_bounds__(kPfThreads, 2) k_pf_down(PrefillArgs p) {
     const int tl = i >> 6, row = i & 63;
     const int t = t0 + tl;
     if (t >= p.M) continue;
-    float y = (float)((double)(long long)acc_s[tl][row] * (1.0 / kFix));
+    float y = (float)((double)(long long)acc_s[tl][row] * kFixInv);
     if (d.down_bias != nullptr) y += h2f(d.down_bias[o0 + row]);
     p.out[(long long)t * d.H + o0 + row] = f2h(y);
   }
