@@ -185,10 +185,12 @@ int nsmlp_decode_layer_f16(const nsmlp_router* router, const nsmlp_slot_table* t
  *   out[t] = sum over b in sel[t] of Wd_b (silu(Wg_b x_t) * (Wu_b x_t))
  * x [M][H] fp16 (16-byte aligned), sel [M][k] int32 block ids (e.g. from
  * nsmlp_route_f16 with rows = M; an id repeated in a row counts once), out
- * [M][H] fp16.  Grouped per block on MFMA: fp16 operands (the weights as
+ * [M][H] fp16.  Grouped per block on MFMA: fp16 operands (gate/up weights as
  * fp16(code * absmax), as the reference's dequant fallback rounds them,
- * RT:5439-5447), fp32 accumulation, act rounded to fp16 (RT:5459), the down
- * sums accumulated in fixed point (independent of scheduling).  M <= 65536. */
+ * RT:5439-5447; down weights as fp16 codes with the absmax applied to each
+ * block's product in fp32), fp32 accumulation, act rounded to fp16 (RT:5459),
+ * the down sums accumulated in fixed point (independent of scheduling).
+ * M <= 65536 and M*H*2, M*k*64 < 2^31. */
 size_t nsmlp_prefill_workspace_bytes(int H, int NB, int M, int k);
 int nsmlp_prefill_slots_f16(const nsmlp_slot_table* table, const void* x, int M, const int32_t* sel, int k, void* out,
                             void* ws, size_t ws_bytes, void* stream);

@@ -272,6 +272,7 @@ __device__ __forceinline__ float rep_dot32(const uint4 w, const uint32_t* xp, ui
 
 // Nontemporal (streaming) loads for weight data read exactly once.
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
 __device__ __forceinline__ uint4 ld_stream16(const uint8_t* p) {
   const u32x4_t t = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(p));
   return make_uint4(t.x, t.y, t.z, t.w);

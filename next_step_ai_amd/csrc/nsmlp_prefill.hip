@@ -6,15 +6,15 @@
 //
 //   k_pf_mark / k_pf_csr  token lists per block (CSR, ascending token ids),
 //                         from a [NB][M/32] membership bitmap;
-//   k_pf_gu     one workgroup per block: gate and up of the block's tokens,
-//               the token rows gathered as the MFMA A operand and the NF4
-//               rows dequantised in registers to fp16(code * absmax) as the
+//   k_pf_gu     one workgroup per block: gate and up of the block's tokens
+//               as a staged GEMM, the token rows gathered as the MFMA A
+//               operand and the NF4 rows decoded to fp16(code * absmax) as the
 //               B operand (the reference fallback's rounding of the weights,
-//               RT:5439-5447); the 8 waves split K, their sums meet in LDS in
-//               wave order; act = fp16(silu(gate) * up) per (block, token);
+//               RT:5439-5447); act = fp16(silu(gate) * up) per (block, token);
 //   k_pf_down   one workgroup per 64 output rows and 128-token group: for
 //               every block, act [tokens x 32] times the block's down columns
-//               [32 x 64 rows]; each tile is added into the group's [128][64]
+//               [32 x 64 rows] as fp16 codes, the absmax applied to the MFMA
+//               result in fp32; each tile is added into the group's [128][64]
 //               LDS accumulator at its tokens' rows as int64 fixed point
 //               (2^-31), so the sum does not depend on the order the waves
 //               add in; the result is rounded once to fp16.
@@ -47,8 +47,15 @@ __device__ __forceinline__ half8_t mfma_zero_h8() {
   return h;
 }
 
+// Code-pair table: entry e (a packed NF4 byte) holds fp16 code[e >> 4] in
+// the low half (the even element) and fp16 code[e & 15] in the high half.
+__device__ __forceinline__ void cpair_fill(uint32_t* cpair, const float* code, int tid, int nthr) {
+  for (int e = tid; e < 256; e += nthr)
+    cpair[e] = (uint32_t)f2h(code[e >> 4]) | ((uint32_t)f2h(code[e & 15]) << 16);
+}
+
 // 8 consecutive NF4 elements (4 bytes, even element in the high nibble) as
-// fp16(code * absmax).
+// fp16(code * absmax), the reference fallback's rounding of the weights.
 __device__ __forceinline__ half8_t deq8(uint32_t word, float am, const float* code) {
   half8_t h;
 #pragma unroll
@@ -58,6 +65,15 @@ __device__ __forceinline__ half8_t deq8(uint32_t word, float am, const float* co
     h[2 * m + 1] = (_Float16)(code[byte & 15u] * am);
   }
   return h;
+}
+
+// 8 consecutive NF4 elements (4 bytes, even element in the high nibble) as
+// their fp16 code values; the absmax (constant over the 32 columns of an
+// MFMA step for a given weight row) scales the MFMA result instead.
+__device__ __forceinline__ half8_t codes8(uint32_t word, const uint32_t* cpair) {
+  const uint4 v = make_uint4(cpair[word & 0xFFu], cpair[(word >> 8) & 0xFFu], cpair[(word >> 16) & 0xFFu],
+                             cpair[word >> 24]);
+  return __builtin_bit_cast(half8_t, v);
 }
 
 __device__ __forceinline__ half8_t as_h8(uint4 v) { return __builtin_bit_cast(half8_t, v); }
@@ -142,14 +158,38 @@ __global__ void __launch_bounds__(1024) k_pf_csr(PrefillArgs p) {
   }
 }
 
-// Gate/up of one block for all its tokens.  A pass takes up to 8 tiles of
-// 16 tokens; with nte (a power of two >= the tiles) tile groups the 8 waves
-// split K 8 / nte ways: wave w computes tile w % nte over the 128-column
-// chunks ks, ks + KS, ... (ks = w / nte), so every token of the block is done
-// in one pass over its weights; the K-split sums meet in LDS in ks order.
+// Gate/up of one block for all its tokens, as a staged GEMM.  A pass takes
+// up to kGuTok tokens (tiles of 16); K goes in 128-column chunks.  Per chunk
+// the 512 threads load the pass's token rows (16 B pieces, 256 B per row),
+// the block's 64 NF4 rows (8 B pieces, 64 B per row) and their absmax with
+// coalesced loads two chunks ahead, and stage them in LDS (the absmax
+// resolved to fp32 per row and 64 columns).  Wave w takes MFMA step
+// s = w % 4 of every chunk (columns 32 s .. 32 s + 31) for projection
+// w / 4 (gate or up, 2 N-tiles of 16 rows): it decodes its B fragments once
+// per chunk to fp16(code * absmax) and multiplies them with every token
+// tile's A fragment.  The four step partials are summed in LDS in step
+// order at the end of the pass; act = fp16(silu(gate) * up).
+constexpr int kGuChunk = 128;             // columns per chunk
+constexpr int kGuTok = 64;                // tokens per pass
+constexpr int kGuTiles = kGuTok / 16;      // MFMA token tiles per pass
+constexpr int kXPieces = kGuTok * 16 / kPfThreads;  // 16-byte token-row pieces per thread and chunk
+static_assert(kXPieces >= 1 && kGuTok * 16 == kXPieces * kPfThreads, "token pieces must cover the pass");
+static_assert(kGuTok * 64 * 4 <= kGuTok * (kGuChunk * 2 + 16), "gate/up sums must fit the token buffer");
+constexpr int kXRow = kGuChunk * 2 + 16;  // bytes per staged token row (padded)
+constexpr int kWRow = kGuChunk / 2 + 16;  // bytes per staged NF4 row (padded)
+
+struct GuRegs {
+  uint4 x[kXPieces];  // 16-byte pieces of token rows
+  uint2 w;        // 16 nibbles of one weight row
+  float am;       // fp32 absmax, or the absmax2 (double-quantised)
+  uint32_t qa;    // u8 absmax code (double-quantised)
+};
+
 template <bool DQ>
-__global__ void __launch_bounds__(kPfThreads, 2) k_pf_gu(PrefillArgs p) {
-  __shared__ float red[kPfWaves][4][256];  // per wave: N-tile (gate 0-15, 16-31, up 0-15, 16-31), C
+__global__ void __launch_bounds__(kPfThreads, 4) k_pf_gu(PrefillArgs p) {  // 4 waves per SIMD: two workgroups per CU
+  __shared__ __attribute__((aligned(16))) uint8_t xs[2][kGuTok * kXRow];  // token rows, fp16
+  __shared__ __attribute__((aligned(16))) uint8_t wsr[2][64 * kWRow];     // NF4 rows (gate 0-31, up 32-63)
+  __shared__ float ams[2][64][8];                                          // absmax per row and 16 columns
   __shared__ float code_s[16];
   __shared__ float c2_s[2][256];
   const DecodeArgs& d = p.d;
@@ -162,10 +202,8 @@ __global__ void __launch_bounds__(kPfThreads, 2) k_pf_gu(PrefillArgs p) {
   if constexpr (DQ) c2_s[tid >> 8][tid & 255] = (tid < 256 ? d.gate.code2 : d.up.code2)[tid & 255];
   const BlockRef br = resolve_id(d, b);
   if (!br.ok && tid == 0) atomicOr(d.status, 1);
-  __syncthreads();
   const int H = d.H;
-  const int j = lane & 15, g = lane >> 4;
-  const long long rs = d.gate.row_stride;
+  const uint32_t rs = (uint32_t)d.gate.row_stride;
   const uint32_t A = (uint32_t)d.gate.abs_row_stride;
   const int nb = br.ok ? (int)(32 * rs) : 0;
   const rsrc_t rg = make_rsrc((br.dev ? d.gate.packed : d.host_gate.packed) + br.q * d.gate.blk_stride, nb);
@@ -184,94 +222,122 @@ __global__ void __launch_bounds__(kPfThreads, 2) k_pf_gu(PrefillArgs p) {
     rua = make_rsrc((br.dev ? d.up.absmax : d.host_up.absmax) + br.q * d.up.abs_blk_stride, na);
   }
   const rsrc_t rx = make_rsrc(p.x, (int)((long long)p.M * H * 2));
-  const int nchunks = H / kChunk;
-  const int ntiles = (cnt + 15) / 16;
+  const rsrc_t rtok = make_rsrc(p.tokens + beg, cnt * 4);
+  const int nchunks = H / kGuChunk;
+  // this thread's staged weight row (0..31 gate, 32..63 up) and 16-column piece
+  const int wr = tid >> 3, wpart = tid & 7;
+  const bool wup = wr >= 32;
+  const uint32_t wrow = (uint32_t)(wr & 31);
+  // this wave's MFMA step and projection; lane (j, g)
+  const int s = wave & 3, proj = wave >> 2;
+  const int j = lane & 15, g = lane >> 4;
+  __syncthreads();
 
-  for (int pass0 = 0; pass0 < ntiles; pass0 += kPfWaves) {
-    const int ntp = min(kPfWaves, ntiles - pass0);
-    const int nte = ntp <= 1 ? 1 : ntp <= 2 ? 2 : ntp <= 4 ? 4 : 8;
-    const int KS = kPfWaves / nte;
-    const int tile = wave % nte, ks = wave / nte;
-    const int e_row = (pass0 + tile) * 16 + j;  // this lane's A row (token entry)
-    const bool tv = br.ok && tile < ntp && e_row < cnt;
-    const int tok = tv ? p.tokens[beg + e_row] : 0;
-    const bool wlive = br.ok && tile < ntp;
-    float4_t acc[4];
+  for (int t0 = 0; t0 < cnt; t0 += kGuTok) {
+    const int T = min(kGuTok, cnt - t0);
+    const int ntiles = (T + 15) >> 4;
+    int xtok[kXPieces];
 #pragma unroll
-    for (int nt = 0; nt < 4; ++nt) acc[nt] = float4_t{0.0f, 0.0f, 0.0f, 0.0f};
-
-    // two-stage pipeline over this wave's chunks ks, ks + KS, ...; every load
-    // is unconditional (a chunk past the end, an idle tile or an invalid block
-    // reads zeros through an out-of-extent offset)
-    uint4 w[2][4], xv[2][4];
-    float am[2][4];
-    uint32_t qa[2][4];
-    auto issue = [&](int st, int c) {
-      const bool live = c < nchunks && wlive;
-      const uint32_t col = (uint32_t)(live ? c : 0) * kChunk + 32u * g;
-      const uint32_t ce = col >> d.qbs_shift;
-#pragma unroll
-      for (int nt = 0; nt < 4; ++nt) {
-        const uint32_t r = (uint32_t)((nt & 1) * 16 + j);
-        // cached: the other tile waves of this K split read the same rows
-        w[st][nt] = buf_ld16c(nt < 2 ? rg : ru, live ? r * (uint32_t)rs + (col >> 1) : kOffNone, 0);
-        if constexpr (DQ) {
-          qa[st][nt] = buf_ldu8(nt < 2 ? rgq : ruq, live ? ((r >> 1) * A + ce) * 2u + (r & 1u) : kOffNone, 0);
-          const uint32_t f = (32u * (uint32_t)b + r) * A + ce;
-          am[st][nt] = buf_ldfc(nt < 2 ? rg2 : ru2, live ? (f >> d.dq_shift) * 4u : kOffNone, 0);
-        } else {
-          qa[st][nt] = 0;
-          am[st][nt] = buf_ldf(nt < 2 ? rga : rua, live ? (r * A + ce) * 4u : kOffNone, 0);
-        }
-      }
-      const uint32_t xo = (live && tv) ? ((uint32_t)tok * (uint32_t)H + col) * 2u : kOffNone;
-#pragma unroll
-      for (int v = 0; v < 4; ++v) xv[st][v] = buf_ld16c(rx, xo, 16u * v);
-    };
-    issue(0, ks);
-    issue(1, ks + KS);
-    for (int c0 = ks; c0 < nchunks; c0 += 2 * KS) {
-#pragma unroll
-      for (int st = 0; st < 2; ++st) {
-        const int c = c0 + st * KS;
-        if (c < nchunks && wlive) {
-          float amv[4];
-#pragma unroll
-          for (int nt = 0; nt < 4; ++nt) {
-            if constexpr (DQ)
-              amv[nt] = dq_absmax(c2_s[nt < 2 ? 0 : 1][qa[st][nt]], am[st][nt], nt < 2 ? d.gate.offset : d.up.offset);
-            else
-              amv[nt] = am[st][nt];
-          }
-#pragma unroll
-          for (int s = 0; s < 4; ++s) {
-            const half8_t af = as_h8(xv[st][s]);
-#pragma unroll
-            for (int nt = 0; nt < 4; ++nt) {
-              const uint32_t word = s == 0 ? w[st][nt].x : s == 1 ? w[st][nt].y : s == 2 ? w[st][nt].z : w[st][nt].w;
-              acc[nt] = mfma16(af, deq8(word, amv[nt], code_s), acc[nt]);
-            }
-          }
-        }
-        issue(st, c + 2 * KS);
-      }
+    for (int h = 0; h < kXPieces; ++h) {
+      const int tt = (tid + h * kPfThreads) >> 4;
+      xtok[h] = tt < T ? buf_ldic(rtok, (uint32_t)(t0 + tt) * 4u, 0) : -1;
     }
+    auto load = [&](GuRegs& R, int c) {
+      const bool live = c < nchunks;
+      const uint32_t col0 = (uint32_t)(live ? c : 0) * kGuChunk;
 #pragma unroll
-    for (int nt = 0; nt < 4; ++nt)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) red[wave][nt][(4 * g + r) * 16 + j] = acc[nt][r];
-    __syncthreads();
-    for (int o = tid; o < ntp * 16 * 32; o += kPfThreads) {
-      const int t = o >> 9, i = (o >> 5) & 15, row = o & 31;
-      const int e = (pass0 + t) * 16 + i;
-      if (e >= cnt) continue;
-      const int ng = row >> 4, jj = row & 15;
-      float gs = 0.0f, us = 0.0f;
-      for (int q = 0; q < KS; ++q) {
-        gs += red[t + nte * q][ng][i * 16 + jj];
-        us += red[t + nte * q][2 + ng][i * 16 + jj];
+      for (int h = 0; h < kXPieces; ++h) {
+        const uint32_t part = (uint32_t)((tid + h * kPfThreads) & 15);
+        const uint32_t xo = (live && xtok[h] >= 0) ? ((uint32_t)xtok[h] * (uint32_t)H + col0 + part * 8u) * 2u
+                                                   : kOffNone;
+        R.x[h] = buf_ld16c(rx, xo, 0);
       }
-      p.act[(long long)(beg + e) * 32 + row] = br.ok ? f2h(silu_mul(gs, us)) : (uint16_t)0;
+      const uint32_t col = col0 + 16u * (uint32_t)wpart;
+      const uint32_t ce = col >> d.qbs_shift;
+      const u32x2_t wv = __builtin_amdgcn_raw_buffer_load_b64(wup ? ru : rg, (int)(live ? wrow * rs + (col >> 1)
+                                                                                         : kOffNone), 0, 0);
+      R.w = make_uint2(wv.x, wv.y);
+      if constexpr (DQ) {
+        R.qa = buf_ldu8(wup ? ruq : rgq, live ? ((wrow >> 1) * A + ce) * 2u + (wrow & 1u) : kOffNone, 0);
+        const uint32_t f = (32u * (uint32_t)b + wrow) * A + ce;
+        R.am = buf_ldfc(wup ? ru2 : rg2, live ? (f >> d.dq_shift) * 4u : kOffNone, 0);
+      } else {
+        R.qa = 0;
+        R.am = buf_ldf(wup ? rua : rga, live ? (wrow * A + ce) * 4u : kOffNone, 0);
+      }
+    };
+    auto store = [&](int bi, const GuRegs& R) {
+#pragma unroll
+      for (int h = 0; h < kXPieces; ++h) {
+        const int piece = tid + h * kPfThreads;
+        *reinterpret_cast<uint4*>(&xs[bi][(piece >> 4) * kXRow + (piece & 15) * 16]) = R.x[h];
+      }
+      *reinterpret_cast<uint2*>(&wsr[bi][wr * kWRow + wpart * 8]) = R.w;
+      float am = R.am;
+      if constexpr (DQ) am = dq_absmax(c2_s[wup ? 1 : 0][R.qa], R.am, wup ? d.up.offset : d.gate.offset);
+      ams[bi][wr][wpart] = am;  // the absmax of this thread's 16 columns
+    };
+    float4_t acc[kGuTiles][2];
+#pragma unroll
+    for (int tt = 0; tt < kGuTiles; ++tt) acc[tt][0] = acc[tt][1] = float4_t{0.0f, 0.0f, 0.0f, 0.0f};
+    GuRegs R[2];
+    load(R[0], 0);
+    load(R[1], 1);
+    store(0, R[0]);
+    load(R[0], 2);
+    __syncthreads();
+    // chunk c computes from buffer c & 1 while the next chunk goes into the
+    // other buffer; unrolled by two so the register stages are named
+    auto step = [&](int c, int bi, GuRegs& Rn) {
+      half8_t bf[2];
+#pragma unroll
+      for (int q = 0; q < 2; ++q) {
+        const int row = proj * 32 + q * 16 + j;
+        const uint32_t word = *reinterpret_cast<const uint32_t*>(&wsr[bi][row * kWRow + 16 * s + 4 * g]);
+        bf[q] = deq8(word, ams[bi][row][2 * s + (g >> 1)], code_s);
+      }
+#pragma unroll
+      for (int tt = 0; tt < kGuTiles; ++tt) {
+        if (tt < ntiles) {
+          const half8_t af = as_h8(*reinterpret_cast<const uint4*>(&xs[bi][(tt * 16 + j) * kXRow + (32 * s + 8 * g) * 2]));
+          acc[tt][0] = mfma16(af, bf[0], acc[tt][0]);
+          acc[tt][1] = mfma16(af, bf[1], acc[tt][1]);
+        }
+      }
+      if (c + 1 < nchunks) {
+        store(bi ^ 1, Rn);
+        load(Rn, c + 3);
+      }
+      __syncthreads();
+    };
+    for (int c = 0; c < nchunks; c += 2) {
+      step(c, 0, R[1]);
+      if (c + 1 < nchunks) step(c + 1, 1, R[0]);
+    }
+    // step partials summed in step order into [kGuTok tok][64 rows] fp32
+    // (rows: gate 0-31, up 32-63), reusing the token staging buffer
+    float* cs = reinterpret_cast<float*>(&xs[0][0]);
+    for (int ss = 0; ss < 4; ++ss) {
+      if (s == ss) {
+#pragma unroll
+        for (int tt = 0; tt < kGuTiles; ++tt) {
+          if (tt < ntiles) {
+#pragma unroll
+            for (int q = 0; q < 2; ++q)
+#pragma unroll
+              for (int r = 0; r < 4; ++r) {
+                float* dst = &cs[(tt * 16 + 4 * g + r) * 64 + proj * 32 + q * 16 + j];
+                *dst = ss == 0 ? acc[tt][q][r] : *dst + acc[tt][q][r];
+              }
+          }
+        }
+      }
+      __syncthreads();
+    }
+    for (int o = tid; o < T * 32; o += kPfThreads) {
+      const int ti = o >> 5, row = o & 31;
+      const float gs = cs[ti * 64 + row], us = cs[ti * 64 + 32 + row];
+      p.act[(long long)(beg + t0 + ti) * 32 + row] = br.ok ? f2h(silu_mul(gs, us)) : (uint16_t)0;
     }
     __syncthreads();
   }
@@ -292,11 +358,15 @@ struct DnPf {
   int b;
 };
 
+constexpr int kPfA2Max = 1024;  // absmax2 entries of a 64-row chunk staged in LDS
+constexpr int kDnDepth = 2;     // blocks in flight per wave
+
 template <bool DQ>
 __global__ void __launch_bounds__(kPfThreads, 2) k_pf_down(PrefillArgs p) {
   __shared__ unsigned long long acc_s[kTokGroup][64];
-  __shared__ float code_s[16];
+  __shared__ uint32_t cpair[256];
   __shared__ float c2_s[256];
+  __shared__ float a2_s[DQ ? kPfA2Max : 1];
   const DecodeArgs& d = p.d;
   const int tid = threadIdx.x, lane = tid & (kWave - 1);
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -314,13 +384,21 @@ __global__ void __launch_bounds__(kPfThreads, 2) k_pf_down(PrefillArgs p) {
   }
   const int o0 = rc * 64, t0 = tg * kTokGroup;
   for (int i = tid; i < kTokGroup * 64; i += kPfThreads) (&acc_s[0][0])[i] = 0ull;
-  if (tid < 16) code_s[tid] = d.code[tid];
+  cpair_fill(cpair, d.code, tid, kPfThreads);
+  const uint32_t Ad = (uint32_t)(d.NB * 32) >> d.qbs_shift;
+  // double-quantised: the absmax2 entries of rows o0 .. o0 + 63 (from g_lo on)
+  // in LDS when they fit, else read per block
+  const uint32_t g_lo = DQ ? ((uint32_t)o0 * Ad) >> d.dq_shift : 0u;
+  const bool a2_lds = DQ && (((64u * Ad - 1u) >> d.dq_shift) + 2u) <= (uint32_t)kPfA2Max;
   if constexpr (DQ) {
     if (tid < 256) c2_s[tid] = d.down.code2[tid];
+    if (a2_lds) {
+      const uint32_t last = (uint32_t)((((long long)d.H * Ad) - 1) >> d.dq_shift);
+      for (int i = tid; i < kPfA2Max; i += kPfThreads) a2_s[i] = d.down.absmax2[min(g_lo + (uint32_t)i, last)];
+    }
   }
   __syncthreads();
   const int j = lane & 15, g = lane >> 4;
-  const uint32_t Ad = (uint32_t)(d.NB * 32) >> d.qbs_shift;
   const int NB = d.NB;
   const int nbw = NB > wave ? (NB - wave + kPfWaves - 1) / kPfWaves : 0;  // this wave's blocks
   const long long nk = (long long)p.M * p.k;
@@ -374,7 +452,7 @@ __global__ void __launch_bounds__(kPfThreads, 2) k_pf_down(PrefillArgs p) {
         if constexpr (DQ) {
           st.qa[nt] = buf_ldu8(ra, o, 0);
           const uint32_t f = o * Ad + ((32u * (uint32_t)b) >> d.qbs_shift);
-          st.am[nt] = buf_ldfc(r_a2, ok ? (f >> d.dq_shift) * 4u : kOffNone, 0);
+          st.am[nt] = buf_ldfc(r_a2, (ok && !a2_lds) ? (f >> d.dq_shift) * 4u : kOffNone, 0);
         } else {
           st.qa[nt] = 0;
           st.am[nt] = buf_ldf(ra, o * 4u, 0);
@@ -389,19 +467,29 @@ __global__ void __launch_bounds__(kPfThreads, 2) k_pf_down(PrefillArgs p) {
         st.tok[r] = er < st.s1 ? tv : -1;
       }
     };
-    DnPf st[2];
-    issue(st[0], 0);
-    issue(st[1], 1);
-    for (int m0 = 0; m0 < nseg; m0 += 2) {
+    DnPf st[kDnDepth];
 #pragma unroll
-      for (int ss = 0; ss < 2; ++ss) {
+    for (int i = 0; i < kDnDepth; ++i) issue(st[i], i);
+    for (int m0 = 0; m0 < nseg; m0 += kDnDepth) {
+#pragma unroll
+      for (int ss = 0; ss < kDnDepth; ++ss) {
         DnPf& cur = st[ss];
         if (cur.s0 < cur.s1) {
           half8_t bf[4];
+          float am[4];  // absmax of output row j of N-tile nt for this block
 #pragma unroll
           for (int nt = 0; nt < 4; ++nt) {
-            const float a = DQ ? dq_absmax(c2_s[cur.qa[nt]], cur.am[nt], d.down.offset) : cur.am[nt];
-            bf[nt] = deq8(cur.w[nt], a, code_s);
+            float a = cur.am[nt];
+            if constexpr (DQ) {
+              float a2 = cur.am[nt];
+              if (a2_lds) {
+                const uint32_t o = (uint32_t)(o0 + nt * 16 + j);
+                a2 = a2_s[((o * Ad + ((32u * (uint32_t)cur.b) >> d.qbs_shift)) >> d.dq_shift) - g_lo];
+              }
+              a = dq_absmax(c2_s[cur.qa[nt]], a2, d.down.offset);
+            }
+            bf[nt] = codes8(cur.w[nt], cpair);
+            am[nt] = a;
           }
           for (int e0 = cur.s0; e0 < cur.s1; e0 += 16) {
             uint4 av = cur.act;
@@ -426,13 +514,13 @@ __global__ void __launch_bounds__(kPfThreads, 2) k_pf_down(PrefillArgs p) {
                 const int tl = tk[r] - t0;
 #pragma unroll
                 for (int nt = 0; nt < 4; ++nt) {
-                  atomicAdd(&acc_s[tl][nt * 16 + j], (unsigned long long)to_fix31(c[nt][r]));
+                  atomicAdd(&acc_s[tl][nt * 16 + j], (unsigned long long)to_fix31(c[nt][r] * am[nt]));
                 }
               }
             }
           }
         }
-        issue(cur, m0 + ss + 2);
+        issue(cur, m0 + ss + kDnDepth);
       }
     }
   }
