@@ -379,44 +379,47 @@ __device__ __forceinline__ uint32_t buf_ldu16(rsrc_t r, uint32_t voff, uint32_t 
 // scan gives each thread the counts above T (gt) and equal to T (eq) before
 // its range, so an ordered compaction can place every selected index.
 struct TopkLds {
-  unsigned hist[256];
-  int wsum[16];
-  unsigned digit, above;
+  unsigned hist[2][256];  // one histogram per pass, both cleared up front
+  unsigned wsum[16];
 };
 
-__device__ __forceinline__ int wave_incl_scan(int v, int lane) {
+__device__ __forceinline__ unsigned wave_incl_scan(unsigned v, int lane) {
 #pragma unroll
   for (int d = 1; d < kWave; d <<= 1) {
-    int o = __shfl_up(v, d, kWave);
+    const unsigned o = __shfl_up(v, d, kWave);
     if (lane >= d) v += o;
   }
   return v;
 }
 
-// Wave 0: the digit (from the top) holding the remaining-th largest entry.
-__device__ __forceinline__ void topk_find_digit(TopkLds& L, unsigned remaining, int lane) {
+// Run by every wave on its own (no barrier after it): the digit (from the
+// top) holding the remaining-th largest entry of hist, and the count of
+// entries in higher digits, in every lane.
+__device__ __forceinline__ void topk_find_digit(const unsigned* hist, unsigned remaining, int lane, unsigned& digit,
+                                                unsigned& above) {
   // lane l holds digits 255 - 4l .. 252 - 4l (plain registers: no array, so
   // nothing is placed in scratch memory)
-  const unsigned c0 = L.hist[255 - 4 * lane], c1 = L.hist[254 - 4 * lane];
-  const unsigned c2 = L.hist[253 - 4 * lane], c3 = L.hist[252 - 4 * lane];
+  const unsigned c0 = hist[255 - 4 * lane], c1 = hist[254 - 4 * lane];
+  const unsigned c2 = hist[253 - 4 * lane], c3 = hist[252 - 4 * lane];
   const unsigned local = c0 + c1 + c2 + c3;
-  const unsigned incl = (unsigned)wave_incl_scan((int)local, lane);
+  const unsigned incl = wave_incl_scan(local, lane);
   const unsigned excl = incl - local;
-  if (excl < remaining && remaining <= incl) {
-    unsigned b = 3, cum = excl + c0 + c1 + c2;
-    if (excl + c0 >= remaining) {
-      b = 0;
-      cum = excl;
-    } else if (excl + c0 + c1 >= remaining) {
-      b = 1;
-      cum = excl + c0;
-    } else if (excl + c0 + c1 + c2 >= remaining) {
-      b = 2;
-      cum = excl + c0 + c1;
-    }
-    L.digit = 255u - 4u * lane - b;
-    L.above = cum;
+  const bool mine = excl < remaining && remaining <= incl;
+  unsigned b = 3, cum = excl + c0 + c1 + c2;
+  if (excl + c0 >= remaining) {
+    b = 0;
+    cum = excl;
+  } else if (excl + c0 + c1 >= remaining) {
+    b = 1;
+    cum = excl + c0;
+  } else if (excl + c0 + c1 + c2 >= remaining) {
+    b = 2;
+    cum = excl + c0 + c1;
   }
+  const unsigned long long m = __ballot(mine);
+  const int src = m ? __ffsll((long long)m) - 1 : 0;
+  digit = (unsigned)__shfl((int)(255u - 4u * lane - b), src, kWave);
+  above = (unsigned)__shfl((int)cum, src, kWave);
 }
 
 template <int NTHR, int KPT>
@@ -425,41 +428,48 @@ __device__ __forceinline__ void topk_threshold(const uint32_t (&key)[KPT], int i
   const int tid = threadIdx.x, lane = tid % kWave, wave = tid / kWave;
   T = 0;
   unsigned remaining = (unsigned)k;
+  for (int i = tid; i < 2 * 256; i += NTHR) (&L.hist[0][0])[i] = 0;
+  __syncthreads();
   for (int pass = 0; pass < 2; ++pass) {
-    for (int i = tid; i < 256; i += NTHR) L.hist[i] = 0;
-    __syncthreads();
+    // Scores clamped at zero are common (about half at the 405B shape) and
+    // share one bin: they are counted per wave and added once, instead of
+    // contending on one LDS counter.
+    constexpr uint32_t kZeroKey = 0x8000u;  // order key of +0.0
+    unsigned nzero = 0;
 #pragma unroll
     for (int m = 0; m < KPT; ++m) {
       if (i0 + m >= NB) continue;
-      if (pass == 0)
-        atomicAdd(&L.hist[key[m] >> 8], 1u);
-      else if ((key[m] >> 8) == (T >> 8))
-        atomicAdd(&L.hist[key[m] & 0xFFu], 1u);
+      if (key[m] == kZeroKey) {
+        nzero += pass == 0 || (T >> 8) == (kZeroKey >> 8);
+      } else if (pass == 0) {
+        atomicAdd(&L.hist[0][key[m] >> 8], 1u);
+      } else if ((key[m] >> 8) == (T >> 8)) {
+        atomicAdd(&L.hist[1][key[m] & 0xFFu], 1u);
+      }
     }
+    nzero = wave_sum(nzero);
+    if (lane == 0 && nzero != 0)
+      atomicAdd(&L.hist[pass][pass == 0 ? (kZeroKey >> 8) : (kZeroKey & 0xFFu)], nzero);
     __syncthreads();
-    if (wave == 0) topk_find_digit(L, remaining, lane);
-    __syncthreads();
-    T |= L.digit << (pass == 0 ? 8 : 0);
-    remaining -= L.above;
-    __syncthreads();
+    unsigned digit, above;
+    topk_find_digit(L.hist[pass], remaining, lane, digit, above);
+    T |= digit << (pass == 0 ? 8 : 0);
+    remaining -= above;
   }
   need = remaining;
-  int cnt = 0;
+  // counts of keys above T (high half) and equal to T (low half) before this
+  // thread's keys; both stay below 2^16 since NB <= 65535
+  unsigned cnt = 0;
 #pragma unroll
   for (int m = 0; m < KPT; ++m)
-    if (i0 + m < NB) cnt += key[m] > T ? (1 << 16) : (key[m] == T ? 1 : 0);
-  const int incl = wave_incl_scan(cnt, lane);
+    if (i0 + m < NB) cnt += key[m] > T ? (1u << 16) : (key[m] == T ? 1u : 0u);
+  const unsigned incl = wave_incl_scan(cnt, lane);
   if (lane == kWave - 1) L.wsum[wave] = incl;
   __syncthreads();
-  if (wave == 0) {
-    int v = lane < NTHR / kWave ? L.wsum[lane] : 0;
-    int vi = wave_incl_scan(v, lane);
-    if (lane < NTHR / kWave) L.wsum[lane] = vi - v;
-  }
-  __syncthreads();
-  const int before = L.wsum[wave] + incl - cnt;
-  gt = (unsigned)before >> 16;
-  eq = (unsigned)before & 0xFFFFu;
+  unsigned before = incl - cnt;
+  for (int w = 0; w < wave; ++w) before += L.wsum[w];
+  gt = before >> 16;
+  eq = before & 0xFFFFu;
 }
 
 // Position of a key in ascending block order among the selected, or -1; gt /
