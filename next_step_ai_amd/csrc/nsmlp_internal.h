@@ -65,46 +65,43 @@ __device__ __forceinline__ void exact_merge(Exact3& e, const Exact3& o) {
   e.a2 += o.a2;
 }
 
-// Exact conversion of a double that is a multiple of 2^-48 (|v| < 2^78) to
-// fixed point with LSB 2^-48.
-__device__ __forceinline__ __int128 dbl_to_fix48(double v) {
-  uint64_t bits = (uint64_t)__double_as_longlong(v);
-  uint64_t ex = (bits >> 52) & 0x7FFull;
-  if (ex == 0) return 0;
-  __int128 m = (__int128)((bits & 0xFFFFFFFFFFFFFull) | (1ull << 52));
-  int s = (int)ex - 1075 + 48;
-  __int128 r = s >= 0 ? (m << s) : (m >> (-s));
-  return (bits >> 63) ? -r : r;
-}
-
-// Round v * 2^-48 to the nearest fp16 (ties to even); overflow -> inf.
-__device__ __forceinline__ uint16_t fix48_to_f16(__int128 v) {
-  uint16_t sign = v < 0 ? 0x8000u : 0u;
-  unsigned __int128 M = v < 0 ? (unsigned __int128)(-v) : (unsigned __int128)v;
-  if (M == 0) return sign;
-  uint64_t hi = (uint64_t)(M >> 64), lo = (uint64_t)M;
-  int msb = hi ? 127 - __clzll((long long)hi) : 63 - __clzll((long long)lo);
-  int X = msb - 48;
-  if (X > 15) return sign | 0x7C00u;
-  int q = X >= -14 ? X - 10 : -24;
-  int shift = q + 48;  // in [24, 53]
-  unsigned __int128 R = M >> shift;
-  unsigned __int128 rem = M - (R << shift);
-  unsigned __int128 half = (unsigned __int128)1 << (shift - 1);
-  if (rem > half || (rem == half && (R & 1))) R += 1;
-  if (q == -24) return sign | (uint16_t)R;
-  if (R == 2048) {
-    R = 1024;
+// Round the exact sum a2 + a1 + a0 of an Exact3 to the nearest fp16 (ties to
+// even; overflow -> inf; zero -> +0).  Valid for sums of up to 2^16 + 1
+// products of two fp16 values: then |a1| < 2^27.1 (each part at most 2^11)
+// and |a0| < 17 (each part at most 2^-12), so
+//   * |a2| >= 2^30 means |sum| > 65520: inf with the sign of a2;
+//   * otherwise hi = a2 + a1 is exact (a multiple of 2^-11 below 2^30.2);
+//   * s + err = hi + a0 exactly (TwoSum), |err| <= half an ulp of s.
+// s is then rounded to fp16 by scaling its fp16 ulp to 1 (exact): the
+// fraction of the scaled s decides, and only an exact half is settled by
+// the sign of err (any other fraction is at least one ulp of s from a half,
+// more than |err|).  A sum just below a power of two whose s rounded up to
+// it rounds to that power, as s does.
+__host__ __device__ inline uint16_t exact_to_f16(const Exact3& e) {
+  const double a2 = e.a2, a1 = e.a1, a0 = e.a0;
+  if (fabs(a2) >= 1073741824.0) return a2 < 0.0 ? (uint16_t)0xFC00u : (uint16_t)0x7C00u;
+  const double hi = a2 + a1;
+  const double s = hi + a0;
+  const double bb = s - hi;
+  const double err = (hi - (s - bb)) + (a0 - bb);
+  if (s == 0.0) return 0;
+  const uint16_t sign = s < 0.0 ? (uint16_t)0x8000u : (uint16_t)0u;
+  const double as = fabs(s), ae = s < 0.0 ? -err : err;
+  int ex = 0;
+  (void)frexp(as, &ex);  // as in [2^(ex-1), 2^ex)
+  int q = ex - 1 >= -14 ? ex - 11 : -24;  // fp16 ulp exponent of as
+  const double R = ldexp(as, -q);
+  const double Ri = floor(R), frac = R - Ri;
+  uint32_t Rn = (uint32_t)Ri;
+  if (frac > 0.5 || (frac == 0.5 && (ae > 0.0 || (ae == 0.0 && (Rn & 1u))))) Rn += 1;
+  if (q == -24) return sign | (uint16_t)Rn;  // subnormal (1024: the smallest normal)
+  if (Rn == 2048u) {
+    Rn = 1024u;
     q += 1;
   }
-  int ef = q + 25;
+  const int ef = q + 25;
   if (ef >= 31) return sign | 0x7C00u;
-  return sign | (uint16_t)(ef << 10) | (uint16_t)(R - 1024);
-}
-
-__device__ __forceinline__ uint16_t exact_to_f16(const Exact3& e) {
-  __int128 v = dbl_to_fix48(e.a0) + dbl_to_fix48(e.a1) + dbl_to_fix48(e.a2);
-  return fix48_to_f16(v);
+  return sign | (uint16_t)(ef << 10) | (uint16_t)(Rn - 1024u);
 }
 
 // --------------------------------------------------------- wave helpers --

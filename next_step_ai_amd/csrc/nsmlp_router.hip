@@ -31,6 +31,10 @@ __global__ void __launch_bounds__(kLatThreads) k_latent(RouteArgs a) {
   const int tid = threadIdx.x;
   const uint16_t* __restrict__ x = a.x + (long long)row * a.H;
   const uint16_t* __restrict__ w = a.enc_w + (long long)r * a.H;
+  // the bias goes out with the first loads (an unconditional load: x[0]
+  // stands in when there is no bias), not after the dot product
+  const bool has_b = a.enc_b != nullptr;
+  const uint16_t eb = (has_b ? a.enc_b : x)[has_b ? r : 0];
   Exact3 acc = exact_zero();
   if (kVec) {
 #pragma unroll 8
@@ -48,7 +52,7 @@ __global__ void __launch_bounds__(kLatThreads) k_latent(RouteArgs a) {
   } else {
     for (int c = tid; c < a.H; c += kLatThreads) exact_add(acc, (double)(h2f(x[c]) * h2f(w[c])));
   }
-  if (tid == 0 && a.enc_b != nullptr) exact_add(acc, (double)h2f(a.enc_b[r]));
+  if (tid == 0 && has_b) exact_add(acc, (double)h2f(eb));
   acc = wave_sum_exact(acc);
   __shared__ double red[kLatThreads / kWave][3];
   const int wave = tid / kWave, lane = tid % kWave;
@@ -58,10 +62,14 @@ __global__ void __launch_bounds__(kLatThreads) k_latent(RouteArgs a) {
     red[wave][2] = acc.a2;
   }
   __syncthreads();
-  if (tid == 0) {
-    Exact3 t = exact_zero();
-    for (int wv = 0; wv < kLatThreads / kWave; ++wv) exact_merge(t, Exact3{red[wv][0], red[wv][1], red[wv][2]});
-    a.lat16[(long long)row * a.R + r] = exact_to_f16(t);
+  if (wave == 0) {
+    // the 16 wave sums meet in one wave (exact: any order gives the same sum)
+    constexpr int kW = kLatThreads / kWave;
+    Exact3 t = lane < kW ? Exact3{red[lane][0], red[lane][1], red[lane][2]} : exact_zero();
+#pragma unroll
+    for (int m = kW / 2; m >= 1; m >>= 1)
+      exact_merge(t, Exact3{__shfl_xor(t.a0, m, kWave), __shfl_xor(t.a1, m, kWave), __shfl_xor(t.a2, m, kWave)});
+    if (lane == 0) a.lat16[(long long)row * a.R + r] = exact_to_f16(t);
   }
 }
 
@@ -80,6 +88,11 @@ __global__ void __launch_bounds__(kScoreThreads) k_scores(RouteArgs a) {
   const int part = tid % kScoreLanes;
   const int jj = j < a.NB ? j : a.NB - 1;  // all lanes take part in the merge
   const uint16_t* __restrict__ w = a.score_w + (long long)jj * a.R;
+  // bias and down_block_norm go out with the first loads (unconditional:
+  // score_w stands in for an absent array), not after the dot products
+  const bool has_b = !a.legacy_abs && a.score_b != nullptr, has_n = a.dbn != nullptr;
+  const uint16_t sb = (has_b ? a.score_b : a.score_w)[has_b ? jj : 0];
+  const uint16_t sn = (has_n ? a.dbn : a.score_w)[has_n ? jj : 0];
   constexpr int kPre = 16;  // prefetched terms per lane (R <= 128)
   uint16_t wv[kPre];
 #pragma unroll
@@ -125,10 +138,10 @@ __global__ void __launch_bounds__(kScoreThreads) k_scores(RouteArgs a) {
   for (int m = 1; m < kScoreLanes; m <<= 1)
     exact_merge(acc, Exact3{__shfl_xor(acc.a0, m, kWave), __shfl_xor(acc.a1, m, kWave), __shfl_xor(acc.a2, m, kWave)});
   if (part != 0 || j >= a.NB) return;
-  if (!a.legacy_abs && a.score_b != nullptr) exact_add(acc, (double)h2f(a.score_b[j]));
+  if (has_b) exact_add(acc, (double)h2f(sb));
   uint16_t sc = exact_to_f16(acc);
   if (!a.legacy_abs && (sc & 0x8000u)) sc = 0;  // clamp_min(0) (RT:4331)
-  if (a.dbn != nullptr) sc = f2h(h2f(sc) * h2f(a.dbn[j]));  // fp16 x fp16 is exact in fp32
+  if (has_n) sc = f2h(h2f(sc) * h2f(sn));  // fp16 x fp16 is exact in fp32
   a.scores[(long long)row * a.NB + j] = sc;
   if (a.scores_out != nullptr) a.scores_out[(long long)row * a.NB + j] = sc;
 }
