@@ -195,6 +195,40 @@ size_t nsmlp_prefill_workspace_bytes(int H, int NB, int M, int k);
 int nsmlp_prefill_slots_f16(const nsmlp_slot_table* table, const void* x, int M, const int32_t* sel, int k, void* out,
                             void* ws, size_t ws_bytes, void* stream);
 
+/* ------------------------------------------------ hot-block cache (device)
+ * Promotion of missed blocks into the table's fixed-capacity slots, as
+ * stream-ordered kernels with no host round trip.  Replaces the host-side
+ * promotion of RT:2809-3018 (the down bank's fixed-capacity update, applied
+ * here to whole blocks: gate/up rows and down columns share a slot) with the
+ * slot plan of RT:2576-2617: the novel entries of blocks (valid ids not
+ * resident, first occurrence, in order; at most `capacity`) take the free
+ * slots from active_count on, then the slots of lowest score (ties: lowest
+ * slot); a promoted block scores fp32(base + (i + 1) * 1e-3), base = max
+ * active score + 1 (fp64), i its novel index; active_count grows by the free
+ * slots used.  With NSMLP_CACHE_GROW_ONLY only free slots are used (the gate/up
+ * hot cache, which only grows).  The lookup entries of evicted blocks become
+ * -1.  The promoted blocks are copied from the table's host copies into the
+ * table's slots (written in place), after the work already queued on the
+ * stream.  slot_out (nullable): [n] slot given to each entry, -1 otherwise. */
+typedef struct nsmlp_cache_state {
+  int capacity;           /* slots: the table's n_slots (<= 8192) */
+  int32_t* lookup;        /* [NB] the table's lookup, updated in place */
+  int32_t* slot_block;    /* [capacity] block held by each slot, -1 = none */
+  float* slot_score;      /* [capacity] replacement scores */
+  int32_t* active_count;  /* [1] slots in use (device) */
+} nsmlp_cache_state;
+#define NSMLP_CACHE_GROW_ONLY 1
+size_t nsmlp_cache_workspace_bytes(int n);
+int nsmlp_cache_promote(const nsmlp_slot_table* table, const nsmlp_cache_state* cache, const int32_t* blocks, int n,
+                        int flags, int32_t* slot_out, void* ws, size_t ws_bytes, void* stream);
+/* Calibration hit counts (replaces RT:2205-2243 without the host copy):
+ * counts[b] += row_weights[r] (1 when NULL) for every entry b of row r of
+ * blocks [rows][k] with 0 <= b < NB, added in row order and entry order as
+ * a row-by-row index_add_ adds them.  The reference's recency weights are
+ * ((r + 1) / rows) ** power in fp32. */
+int nsmlp_cache_record_f32(float* counts, int NB, const int32_t* blocks, int rows, int k, const float* row_weights,
+                           void* stream);
+
 size_t nsmlp_single_kernel_workspace_bytes(int H, int top_k);
 int nsmlp_single_kernel_decode_f16(const void* x, const uint8_t* gate_packed, const float* gate_absmax,
                                    const float* gate_code, const uint8_t* up_packed, const float* up_absmax,

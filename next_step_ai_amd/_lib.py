@@ -27,6 +27,7 @@ NSMLP_ROUTE_SORTED = 1
 NSMLP_ROUTE_LEGACY_ABS = 2
 NSMLP_DOWN_BLOCK_MAJOR = 0
 NSMLP_DOWN_GATHERED = 1
+NSMLP_CACHE_GROW_ONLY = 1
 
 
 class SlotTable(ctypes.Structure):
@@ -61,6 +62,12 @@ class Router(ctypes.Structure):
     ]
 
 
+class CacheState(ctypes.Structure):
+    """Mirror of ``nsmlp_cache_state``."""
+
+    _fields_ = [("capacity", I32), ("lookup", P), ("slot_block", P), ("slot_score", P), ("active_count", P)]
+
+
 # name -> (restype, argtypes)
 SIGNATURES: dict[str, tuple] = {
     "nsmlp_last_error": (ctypes.c_char_p, []),
@@ -89,6 +96,9 @@ SIGNATURES: dict[str, tuple] = {
     "nsmlp_gather_down_columns_q8": (I32, [P, P, P, I32, I32, I32, I32, I32, P, P, P]),
     "nsmlp_absmax_dq_quantize": (I32, [P, I64, I32, P, F32, P, P, P]),
     "nsmlp_absmax_dq_dequantize": (I32, [P, I64, I32, P, P, F32, P, P]),
+    "nsmlp_cache_workspace_bytes": (SZ, [I32]),
+    "nsmlp_cache_promote": (I32, [ctypes.POINTER(SlotTable), ctypes.POINTER(CacheState), P, I32, I32, P, P, SZ, P]),
+    "nsmlp_cache_record_f32": (I32, [P, I32, P, I32, I32, P, P]),
     "nsmlp_host_device_pointer": (I32, [P, ctypes.POINTER(P)]),
     "nsmlp_synth_normal_f16": (I32, [U64, I64, F32, P, P]),
     "nsmlp_synth_normal_f32": (I32, [U64, I64, F32, P, P]),

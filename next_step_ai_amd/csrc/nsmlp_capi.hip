@@ -803,4 +803,87 @@ int nsmlp_nf4_quantize_f32(const float* w, long long n, int qbs, uint8_t* packed
   return check_launch("nf4 quantize");
 }
 
+size_t nsmlp_cache_workspace_bytes(int n) {
+  if (n < 0) n = 0;
+  return align_up((size_t)n * 4) * 3 + align_up(4);
+}
+
+int nsmlp_cache_promote(const nsmlp_slot_table* table, const nsmlp_cache_state* cache, const int32_t* blocks, int n,
+                        int flags, int32_t* slot_out, void* ws, size_t ws_bytes, void* stream) {
+  if (table == nullptr || cache == nullptr) return set_error(NSMLP_EINVAL, "table and cache must be non-NULL");
+  DecodeArgs a;
+  int rc = table_to_args(table, a);
+  if (rc != NSMLP_OK) return rc;
+  if (n < 0 || n > 65535) return set_error(NSMLP_EINVAL, "n = %d out of range [0, 65535]", n);
+  if (n > 0 && blocks == nullptr) return set_error(NSMLP_EINVAL, "blocks must be non-NULL");
+  if ((flags & ~NSMLP_CACHE_GROW_ONLY) != 0) return set_error(NSMLP_EINVAL, "unknown flags 0x%x", flags);
+  const int cap = cache->capacity;
+  if (cap < 1 || cap > kMaxCacheSlots)
+    return set_error(NSMLP_EINVAL, "cache capacity %d out of range [1, %d]", cap, kMaxCacheSlots);
+  if (cap != table->n_slots)
+    return set_error(NSMLP_EINVAL, "cache capacity %d differs from the table's n_slots %d", cap, table->n_slots);
+  if (cache->lookup == nullptr || (const int32_t*)cache->lookup != table->lookup)
+    return set_error(NSMLP_EINVAL, "the cache's lookup must be the table's (non-NULL) lookup");
+  if (cache->slot_block == nullptr || cache->slot_score == nullptr || cache->active_count == nullptr)
+    return set_error(NSMLP_EINVAL, "slot_block, slot_score and active_count must be non-NULL");
+  if (table->host_gate_packed == nullptr)
+    return set_error(NSMLP_EINVAL, "promotion copies blocks from the table's host copies, which are absent");
+  if (n > 0 && (ws == nullptr || ws_bytes < nsmlp_cache_workspace_bytes(n)))
+    return set_error(NSMLP_ENOSPC, "workspace of %zu bytes < %zu", ws_bytes, nsmlp_cache_workspace_bytes(n));
+  if (n == 0) return NSMLP_OK;
+  CacheArgs c;
+  memset(&c, 0, sizeof(c));
+  c.NB = a.NB;
+  c.capacity = cap;
+  c.n = n;
+  c.grow_only = (flags & NSMLP_CACHE_GROW_ONLY) ? 1 : 0;
+  c.lookup = cache->lookup;
+  c.slot_block = cache->slot_block;
+  c.slot_score = cache->slot_score;
+  c.active = cache->active_count;
+  c.blocks = blocks;
+  c.plan_out = slot_out;
+  uint8_t* w = (uint8_t*)ws;
+  const size_t ln = align_up((size_t)n * 4);
+  c.novel = (int32_t*)w;
+  c.copy_block = (int32_t*)(w + ln);
+  c.copy_slot = (int32_t*)(w + 2 * ln);
+  c.n_copy = (int32_t*)(w + 3 * ln);
+  const bool dq = table->dq_block > 0;
+  const long long H = table->H, A = H / table->qbs;
+  const void* src[6] = {table->host_gate_packed,
+                        dq ? (const void*)table->host_gate_qabsmax : (const void*)table->host_gate_absmax,
+                        table->host_up_packed,
+                        dq ? (const void*)table->host_up_qabsmax : (const void*)table->host_up_absmax,
+                        table->host_down_packed,
+                        dq ? (const void*)table->host_down_qabsmax : (const void*)table->host_down_absmax};
+  const void* dst[6] = {table->gate_packed, dq ? (const void*)table->gate_qabsmax : (const void*)table->gate_absmax,
+                        table->up_packed, dq ? (const void*)table->up_qabsmax : (const void*)table->up_absmax,
+                        table->down_packed,
+                        dq ? (const void*)table->down_qabsmax : (const void*)table->down_absmax};
+  const long long bytes[6] = {16 * H, dq ? 32 * A : 128 * A, 16 * H, dq ? 32 * A : 128 * A, 16 * H, dq ? H : 4 * H};
+  for (int i = 0; i < 6; ++i) {
+    if (src[i] == nullptr || dst[i] == nullptr)
+      return set_error(NSMLP_EINVAL, "slot and host-copy arrays must all be non-NULL");
+    if (!aligned16(src[i]) || !aligned16(dst[i]) || bytes[i] % 16 != 0)
+      return set_error(NSMLP_EINVAL, "slot and host-copy arrays must be 16-byte aligned");
+    c.src[i] = (const uint8_t*)src[i];
+    c.dst[i] = (uint8_t*)const_cast<void*>(dst[i]);  // the table's slots are written in place
+    c.bytes[i] = bytes[i];
+  }
+  launch_cache_promote(c, (hipStream_t)stream);
+  return check_launch("nsmlp_cache_promote");
+}
+
+int nsmlp_cache_record_f32(float* counts, int NB, const int32_t* blocks, int rows, int k, const float* row_weights,
+                           void* stream) {
+  if (counts == nullptr || NB <= 0) return set_error(NSMLP_EINVAL, "counts must be non-NULL and NB >= 1");
+  if (rows < 0 || k < 0 || (long long)rows * k >= (1LL << 31))
+    return set_error(NSMLP_EINVAL, "rows %d x k %d out of range", rows, k);
+  if ((long long)rows * k == 0) return NSMLP_OK;
+  if (blocks == nullptr) return set_error(NSMLP_EINVAL, "blocks must be non-NULL");
+  launch_cache_record(counts, NB, blocks, rows, k, row_weights, (hipStream_t)stream);
+  return check_launch("nsmlp_cache_record_f32");
+}
+
 }  // extern "C"

@@ -112,6 +112,12 @@ __device__ __forceinline__ T wave_sum(T v) {
   return v;
 }
 
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int m = kWave / 2; m >= 1; m >>= 1) v = fmaxf(v, __shfl_xor(v, m, kWave));
+  return v;
+}
+
 __device__ __forceinline__ Exact3 wave_sum_exact(Exact3 e) {
 #pragma unroll
   for (int m = kWave / 2; m >= 1; m >>= 1) {
@@ -612,6 +618,32 @@ struct PrefillArgs {
   uint16_t* act;          // [M k][32] fp16 silu(gate) * up per (block, token) entry
 };
 void launch_prefill(const PrefillArgs& p, hipStream_t s);
+
+// Hot-block cache maintenance (fixed-capacity promotion and calibration
+// counts) over a slot table with pinned host copies.
+constexpr int kMaxCacheSlots = 8192;  // capacity limit (eviction order staged in LDS)
+struct CacheArgs {
+  int NB;
+  int capacity;
+  int n;          // entries of blocks
+  int grow_only;  // 1: free slots only, no eviction
+  int32_t* lookup;      // [NB] block -> slot or -1
+  int32_t* slot_block;  // [capacity] slot -> block or -1
+  float* slot_score;    // [capacity]
+  int32_t* active;      // [1]
+  const int32_t* blocks;  // [n] candidate blocks (a token's selection)
+  int32_t* plan_out;      // [n] slot given to each entry or -1; nullable
+  int32_t* novel;         // workspace [n]
+  int32_t* copy_block;    // workspace [min(n, capacity)]
+  int32_t* copy_slot;     // workspace [min(n, capacity)]
+  int32_t* n_copy;        // workspace [1]
+  const uint8_t* src[6];  // host copies by block id: gate packed, gate absmax, up packed, up absmax,
+  uint8_t* dst[6];        //   down packed, down absmax; slots by slot index
+  long long bytes[6];     // bytes per block of each array (multiples of 16)
+};
+void launch_cache_promote(const CacheArgs& c, hipStream_t s);
+void launch_cache_record(float* counts, int NB, const int32_t* blocks, int rows, int k, const float* w,
+                         hipStream_t s);
 
 void launch_decode_gate_up(const DecodeArgs& a, hipStream_t s);
 void launch_decode_down(const DecodeArgs& a, hipStream_t s);

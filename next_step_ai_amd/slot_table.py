@@ -170,14 +170,16 @@ class SparseMlpSlotTable:
     @classmethod
     def from_reference(cls, *, gate_packed: torch.Tensor, gate_absmax, up_packed: torch.Tensor, up_absmax,
                        down_packed: torch.Tensor, down_absmax, H: int, I: int, qbs: int = 64,
-                       resident_blocks: torch.Tensor | None = None, host_copy: bool = False) -> "SparseMlpSlotTable":
+                       resident_blocks: torch.Tensor | None = None, host_copy: bool = False,
+                       capacity: int | None = None) -> "SparseMlpSlotTable":
         """Build from the reference layouts on the device: gate/up ``[I*H/2]``
         u8 + ``[I*H/qbs]`` absmax, down ``[H*I/2]`` u8 + ``[H*I/qbs]`` absmax.
         The absmax are fp32 tensors, or all three ``NestedAbsmax`` (the
         double-quantised state, kept as u8 codes).  ``resident_blocks``
         (default: all) go to HBM slots in the given order; with ``host_copy``
         every block is also kept in pinned host memory and non-resident
-        blocks are served from there."""
+        blocks are served from there.  ``capacity`` (>= the resident count)
+        adds empty slots after the resident ones, for promotions."""
         device = require_device(gate_packed, "gate_packed")
         t = cls(H=H, I=I, qbs=qbs, device=device)
         nested = [isinstance(x, NestedAbsmax) for x in (gate_absmax, up_absmax, down_absmax)]
@@ -208,6 +210,15 @@ class SparseMlpSlotTable:
             t.gate_packed, t.gate_absmax = gather_row_blocks(gate_packed, gate_absmax, res, H, qbs)
             t.up_packed, t.up_absmax = gather_row_blocks(up_packed, up_absmax, res, H, qbs)
             t.down_packed, t.down_absmax = gather_down_columns(down_packed, down_absmax, res, H, I, qbs)
+            n_res = int(res.numel())
+            if capacity is not None and int(capacity) > n_res:
+                def grow(a):
+                    g = torch.zeros((int(capacity),) + tuple(a.shape[1:]), dtype=a.dtype, device=device)
+                    g[:n_res] = a
+                    return g
+                t.gate_packed, t.gate_absmax = grow(t.gate_packed), grow(t.gate_absmax)
+                t.up_packed, t.up_absmax = grow(t.up_packed), grow(t.up_absmax)
+                t.down_packed, t.down_absmax = grow(t.down_packed), grow(t.down_absmax)
             lookup = torch.full((NB,), -1, dtype=torch.int32)
             lookup[res.to("cpu", torch.long)] = torch.arange(int(res.numel()), dtype=torch.int32)
             t.lookup = lookup.to(device)
@@ -342,15 +353,96 @@ class SparseMlpRouter:
         )
 
 
+def recency_weights(rows: int, power: float) -> torch.Tensor:
+    """The calibration weight of each row, ((r + 1) / rows) ** power in fp32
+    on the CPU (RT:2224-2228)."""
+    pos = torch.arange(1, int(rows) + 1, dtype=torch.float32)
+    return torch.pow(pos / float(max(int(rows), 1)), float(power))
+
+
+def record_hot_cache_calibration_blocks(counts: torch.Tensor, active_blocks: torch.Tensor, *,
+                                        recency_power: float = 1.0) -> torch.Tensor:
+    """Calibration hit counts on the device (RT:2205-2243 without the host
+    copy): ``counts`` [NB] fp32 += the row's recency weight for every block id
+    of each row of ``active_blocks`` [rows, k] (ids outside [0, NB) skipped),
+    added row by row as ``index_add_`` adds them.  Returns ``counts``."""
+    device = require_device(counts, "counts")
+    if counts.dtype != torch.float32 or not counts.is_contiguous():
+        raise RuntimeError("counts must be a contiguous float32 tensor")
+    blocks = active_blocks.to(device=device, dtype=torch.int32).contiguous()
+    k = int(blocks.shape[-1]) if blocks.ndim > 0 else 1
+    rows = int(blocks.numel()) // max(k, 1)
+    if rows == 0:
+        return counts
+    w = recency_weights(rows, recency_power).to(device)
+    _lib.call("nsmlp_cache_record_f32", ptr(counts), int(counts.numel()), ptr(blocks), rows, k, ptr(w),
+              stream_handle(device))
+    return counts
+
+
+class HotBlockCache:
+    """Device-side replacement policy of a slot table: the promotion of
+    missed blocks (RT:2809-3018) with the fixed-capacity slot plan of
+    RT:2576-2617, run on the table's stream with no host round trip.  The
+    table needs its host copies (``host_copy=True``); the promoted blocks are
+    copied from them into the slots.  ``grow_only`` uses free slots only (the
+    reference's gate/up hot cache, which never evicts)."""
+
+    def __init__(self, table: SparseMlpSlotTable, *, scores: torch.Tensor | None = None,
+                 active_count: int | None = None, grow_only: bool = False):
+        if not table.host:
+            raise RuntimeError("promotion copies blocks from the table's host copies (build it with host_copy=True)")
+        device = table.device
+        cap = table.n_slots
+        if table.lookup is None:  # all blocks resident in order: make the identity lookup explicit
+            table.lookup = torch.arange(table.NB, dtype=torch.int32, device=device)
+            table.as_struct()
+        self.table = table
+        self.grow_only = bool(grow_only)
+        blocks = table.block_ids.to(torch.int32)
+        self.slot_block = torch.full((cap,), -1, dtype=torch.int32)
+        self.slot_block[:int(blocks.numel())] = blocks[:cap]
+        self.slot_block = self.slot_block.to(device)
+        self.slot_score = (torch.zeros(cap, dtype=torch.float32) if scores is None
+                           else scores.to(torch.float32).reshape(-1)[:cap].clone()).to(device).contiguous()
+        n_active = int(blocks.numel()) if active_count is None else int(active_count)
+        self.active = torch.tensor([max(0, min(n_active, cap))], dtype=torch.int32, device=device)
+        self._state = _lib.CacheState(capacity=cap, lookup=ptr(table.lookup), slot_block=ptr(self.slot_block),
+                                      slot_score=ptr(self.slot_score), active_count=ptr(self.active))
+
+    def promote(self, blocks: torch.Tensor, *, return_slots: bool = False) -> torch.Tensor | None:
+        """Promote the non-resident entries of ``blocks`` (a token's selected
+        block ids); optionally return the slot given to each entry (-1: none)."""
+        device = self.table.device
+        b = blocks.reshape(-1).to(device=device, dtype=torch.int32).contiguous()
+        n = int(b.numel())
+        slots = torch.empty(n, dtype=torch.int32, device=device) if return_slots else None
+        ws = workspace(int(_lib.lib().nsmlp_cache_workspace_bytes(n)), device)
+        st = self.table._struct if self.table._struct is not None else self.table.as_struct()
+        _lib.call("nsmlp_cache_promote", ctypes.byref(st), ctypes.byref(self._state), ptr(b), n,
+                  _lib.NSMLP_CACHE_GROW_ONLY if self.grow_only else 0, ptr(slots), ptr(ws), ws.numel(),
+                  stream_handle(device))
+        return slots
+
+    def state_cpu(self):
+        """(slot block ids, slot scores, active count, lookup) on the CPU."""
+        return (self.slot_block.to("cpu", torch.long), self.slot_score.to("cpu"), int(self.active.item()),
+                self.table.lookup.to("cpu"))
+
+
 class SparseMlpLayer:
     """Router + slot table: one call per decode token and layer, no host
     round trip (the decode branch of RT:5833-5923)."""
 
-    def __init__(self, router: SparseMlpRouter, table: SparseMlpSlotTable, top_k: int):
+    def __init__(self, router: SparseMlpRouter, table: SparseMlpSlotTable, top_k: int,
+                 cache: HotBlockCache | None = None):
         if router.NB != table.NB:
             raise RuntimeError(f"router num_blocks {router.NB} != table num_blocks {table.NB}")
+        if cache is not None and cache.table is not table:
+            raise RuntimeError("the cache belongs to another slot table")
         self.router = router
         self.table = table
+        self.cache = cache
         self.top_k = max(1, min(int(top_k), table.NB))
         self._r = router.as_struct()
         self._t = table.as_struct()
@@ -372,6 +464,8 @@ class SparseMlpLayer:
             ws = workspace(self.workspace_bytes(), self.device)
         _lib.call("nsmlp_decode_layer_f16", ctypes.byref(self._r), ctypes.byref(self._t), ptr(x16), self.top_k,
                   ptr(sel_out), ptr(out), ptr(ws), ws.numel(), stream_handle(self.device))
+        if self.cache is not None:  # the blocks that missed take slots for the next tokens
+            self.cache.promote(sel_out)
         return out, sel_out
 
     def prefill(self, x: torch.Tensor, out: torch.Tensor | None = None):

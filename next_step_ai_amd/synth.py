@@ -88,7 +88,8 @@ class SyntheticLayer:
         }
 
     def slot_table(self, resident_blocks: torch.Tensor | None = None, host_copy: bool = False,
-                   drop_reference_down: bool = False, absmax: str = "auto") -> SparseMlpSlotTable:
+                   drop_reference_down: bool = False, absmax: str = "auto",
+                   capacity: int | None = None) -> SparseMlpSlotTable:
         """``absmax``: "auto" (the nested state when the layer has one),
         "dq" (nested) or "f32" (fp32 absmax)."""
         if self.down_packed is None:
@@ -105,7 +106,7 @@ class SyntheticLayer:
         t = SparseMlpSlotTable.from_reference(
             gate_packed=self.gate_packed, gate_absmax=ga, up_packed=self.up_packed, up_absmax=ua,
             down_packed=self.down_packed, down_absmax=da, H=self.H, I=self.I, qbs=self.qbs,
-            resident_blocks=resident_blocks, host_copy=host_copy)
+            resident_blocks=resident_blocks, host_copy=host_copy, capacity=capacity)
         if drop_reference_down:
             self.down_packed = None
             self.down_absmax = None

@@ -18,6 +18,10 @@ Pinning status (what checks each function, see tests/test_oracle_*.py):
   active_layout          torch.unique / reference test expectations
   gather_* (slot/gather) reference tests test_down_proj_col_cache.py /
                          test_prewarm_col_cache.py expectations
+  plan / promote_blocks  reference test test_throughput_contract.py:308-321
+                         expectations; the argmin rule by brute force
+  calibration_counts     reference test test_throughput_contract.py:261-287
+                         (recency order) and a closed form per block
   nf4 quantize/dequant   closed-form invariants (round trip, nearest code);
                          bitsandbytes itself is absent: parity unpinned
   double quant           closed-form invariants; bitsandbytes absent: parity unpinned
@@ -297,6 +301,66 @@ def plan_fixed_capacity_bank_update(existing_block_ids, existing_scores, active_
         scores[s] = np.float32(base + float(i + 1) * 1e-3)
         slots.append(s)
     return np.array(slots, dtype=np.int64), ids, scores, active
+
+
+def promote_blocks(lookup, slot_block, slot_score, active_count, blocks, *, grow_only=False):
+    """One promotion of a token's selected ``blocks`` into a fixed-capacity
+    bank, as the reference's down-bank promotion takes it (RT:2908-3018):
+    the novel blocks are the valid ids not in ``lookup`` (first occurrence, in
+    order), planned by ``plan_fixed_capacity_bank_update``; an evicted
+    block's lookup entry becomes -1 and a promoted block's its slot.  With
+    ``grow_only`` only the free slots are used (the gate/up hot cache, which
+    grows and never evicts, RT:2809-2906).  Returns (lookup, slot_block,
+    slot_score, active_count, slot per entry of blocks or -1)."""
+    lookup = np.array(lookup, dtype=np.int64).copy()
+    NB = lookup.size
+    cap = len(slot_block)
+    novel, seen = [], set()
+    for b in [int(v) for v in np.asarray(blocks).reshape(-1)]:
+        if 0 <= b < NB and lookup[b] < 0 and b not in seen:
+            novel.append(b)
+            seen.add(b)
+    active = max(0, min(int(active_count), cap))
+    if grow_only:
+        novel = novel[:cap - active]
+    slots, ids, scores, active_new = plan_fixed_capacity_bank_update(slot_block, slot_score, active, cap, novel)
+    old_ids = np.array(slot_block, dtype=np.int64)
+    for b, s in zip(novel, slots.tolist()):
+        o = int(old_ids[s])
+        if 0 <= o < NB and lookup[o] == s:
+            lookup[o] = -1
+        lookup[b] = s
+    slot_of = {b: s for b, s in zip(novel, slots.tolist())}
+    per_entry, given = [], set()
+    for b in [int(v) for v in np.asarray(blocks).reshape(-1)]:
+        if b in slot_of and b not in given:
+            per_entry.append(slot_of[b])
+            given.add(b)
+        else:
+            per_entry.append(-1)
+    return lookup, ids, scores, active_new, np.array(per_entry, dtype=np.int64)
+
+
+def calibration_counts(counts, active_blocks, num_blocks, recency_power):
+    """Restates _record_hot_cache_calibration_blocks (RT:2205-2243): rows of
+    active_blocks [N, k]; row r weighs ((r + 1) / N) ** power (fp32); every
+    valid id of the row adds the weight to its count, row by row (fp32 adds
+    in entry order, as index_add_ on the CPU)."""
+    counts = np.array(counts, dtype=np.float32).copy()
+    rows = np.asarray(active_blocks, dtype=np.int64)
+    rows = rows.reshape(-1, rows.shape[-1] if rows.ndim > 0 else 1)
+    n = rows.shape[0]
+    # the weights as the reference computes them: torch.pow in fp32 on the CPU
+    # (numpy's float32 power can differ from it in the last place)
+    import torch
+
+    pos = torch.arange(1, n + 1, dtype=torch.float32)
+    w = torch.pow(pos / float(max(n, 1)), float(recency_power)).numpy()
+    for r in range(n):
+        for b in rows[r].tolist():
+            if 0 <= b < num_blocks:
+                counts[b] = np.float32(counts[b] + w[r])
+    return counts
 
 
 # ------------------------------------------------------------------ NF4 ---

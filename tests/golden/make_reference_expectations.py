@@ -38,6 +38,11 @@ def main():
             "expected_active_count": 3, "expected_slots": [2, 1], "expected_block_ids": [10, 21, 20],
             "expected_scores_above": {"1": 5.0, "2": 5.0},
         },
+        "calibration_recency": {
+            "source": "tests/test_throughput_contract.py:261-287",
+            "num_blocks": 8, "recency_power": 2.0, "active_blocks": [[1, 1], [2, 2], [3, 3]],
+            "expected_order_desc": [3, 2, 1],
+        },
         "down_column_gather": down_columns_case(),
         "hot_cold_partition": {
             "source": "tests/test_prewarm_col_cache.py:66-72, 133-139, 169-190, 227-240 (hot iff lookup >= 0)",
