@@ -264,6 +264,21 @@ def run_partial(args) -> int:
     per_block = algorithmic_bytes(H, I, 1, qbs, args.absmax) - algorithmic_bytes(H, I, 0, qbs, args.absmax)
     miss_bytes = C3_MISSES * per_block
     hit_bytes = algorithmic_bytes(H, I, k, qbs, args.absmax) - miss_bytes
+    # device-side promotion of the misses into the table (fixed-capacity plan
+    # + copies from the host copies), once per layer after the timed loop
+    from next_step_ai_amd.slot_table import HotBlockCache
+
+    prom = []
+    for j, L in enumerate(layers):
+        cache = HotBlockCache(L.table)
+        ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        ev0.record()
+        slots = cache.promote(sels[j], return_slots=True)
+        ev1.record()
+        torch.cuda.synchronize()
+        assert int((slots >= 0).sum()) == C3_MISSES
+        prom.append(ev0.elapsed_time(ev1) * 1e3)
+    promote_us = statistics.median(prom)
     res = base_result(args, 1e6 / (MODEL_LAYERS * us), us, H, I, R, k, qbs)
     res["config"].update({"resident_blocks": C3_RESIDENT, "host_misses": C3_MISSES, "rotating_layers": n})
     res.update({
@@ -273,6 +288,10 @@ def run_partial(args) -> int:
         # the host link carries the misses: their bytes over the whole layer
         # time is a lower bound of the link rate reached
         "host_link_gbs_lower_bound": round(miss_bytes / (us * 1e-6) / 1e9, 2),
+        # promoting the token's misses into the slots (plan + copies of the
+        # blocks from pinned host memory), HIP events, median over the layers
+        "promote_us": round(promote_us, 1),
+        "promote_host_gbs": round(miss_bytes / (promote_us * 1e-6) / 1e9, 2),
         "note": "misses are read by the kernels from pinned host memory (zero-copy); the layer time is "
                 "host-link bound, so the HBM roofline does not apply to this config",
     })

@@ -21,7 +21,8 @@
 // promoted score is above every score in the bank before the plan, so the
 // argmin never returns a slot promoted by the same plan, and the evicted
 // slots are the old slots in ascending (score, slot) order (argmin returns
-// the first of equal minima).  k_cache_plan computes that order by ranking.
+// the first of equal minima).  k_cache_plan computes that order with a
+// bitonic sort of (score, slot) keys.
 #include <mutex>
 
 #include "nsmlp_internal.h"
@@ -31,17 +32,32 @@ namespace nsmlp {
 namespace {
 
 constexpr int kPlanThreads = 1024;
+constexpr int kPlanStage = 4096;  // entries staged in LDS for the duplicate checks
 
+// fp32 score -> unsigned key with the same order (+0 and -0 equal, as the
+// reference's argmin compares them)
+__device__ __forceinline__ uint32_t score_order_key(float v) {
+  const uint32_t u = v == 0.0f ? 0u : __float_as_uint(v);
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+// k_cache_plan's dynamic LDS: the (score key << 32 | slot) sort keys of the
+// old active slots, padded to a power of two (<= kMaxCacheSlots entries).
 __global__ void __launch_bounds__(kPlanThreads) k_cache_plan(CacheArgs c) {
-  extern __shared__ float score_s[];  // [capacity]
+  extern __shared__ __attribute__((aligned(16))) unsigned long long key_s[];
   __shared__ int wsum[kPlanThreads / kWave];
-  __shared__ int n_novel_s;
+  __shared__ float wmax[kPlanThreads / kWave];
+  __shared__ __attribute__((aligned(16))) int32_t blk_s[kPlanStage];  // the first entries (duplicate checks)
   const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid >> 6;
   const int cap = c.capacity;
   int active = *c.active;
   active = active < 0 ? 0 : (active > cap ? cap : active);
-  for (int s = tid; s < cap; s += kPlanThreads) score_s[s] = c.slot_score[s];
-  if (tid == 0) n_novel_s = 0;
+  for (int i = tid; i < min(c.n, kPlanStage); i += kPlanThreads) blk_s[i] = c.blocks[i];
+  // base score: max over the active slots (fp32 max, exact), plus 1 in fp64
+  float mx = -INFINITY;
+  for (int s = tid; s < active; s += kPlanThreads) mx = fmaxf(mx, c.slot_score[s]);
+  mx = wave_max(mx);
+  if (lane == 0) wmax[wave] = mx;
   __syncthreads();
   // novel positions, compacted in selection order (chunks of 1024 entries)
   int carry = 0;
@@ -52,7 +68,19 @@ __global__ void __launch_bounds__(kPlanThreads) k_cache_plan(CacheArgs c) {
     if (i < c.n) {
       b = c.blocks[i];
       novel = b >= 0 && b < c.NB && c.lookup[b] < 0;
-      for (int j = 0; novel && j < i; ++j) novel = c.blocks[j] != b;
+      if (novel) {  // first occurrence: no earlier equal entry (independent reads, no early exit)
+        const int js = min(i, kPlanStage), j4 = js & ~3;
+        const int4* b4 = reinterpret_cast<const int4*>(blk_s);
+        bool dup = false;
+#pragma unroll 8
+        for (int j = 0; j < j4; j += 4) {
+          const int4 v = b4[j >> 2];
+          dup |= (v.x == b) | (v.y == b) | (v.z == b) | (v.w == b);
+        }
+        for (int j = j4; j < js; ++j) dup |= blk_s[j] == b;
+        for (int j = js; j < i; ++j) dup |= c.blocks[j] == b;
+        novel = !dup;
+      }
     }
     const unsigned long long m = __ballot(novel);
     const int before = __popcll(m & ((1ull << lane) - 1ull));
@@ -71,26 +99,31 @@ __global__ void __launch_bounds__(kPlanThreads) k_cache_plan(CacheArgs c) {
   const int n_free = cap - active;
   const int n_take = c.grow_only ? min(n_novel, n_free) : min(n_novel, cap);
   const int n_evict = max(0, n_take - n_free);
-  // base score: max over the active slots (fp32 max, exact), plus 1 in fp64
-  float mx = -INFINITY;
-  for (int s = tid; s < active; s += kPlanThreads) mx = fmaxf(mx, score_s[s]);
-  mx = wave_max(mx);
-  __shared__ float wmax[kPlanThreads / kWave];
-  if (lane == 0) wmax[wave] = mx;
-  // eviction order: old slot s has rank #{t < active : (score_t, t) < (score_s, s)}
-  __shared__ int evict_s[kMaxCacheSlots];
+  // eviction order: the old active slots sorted by (score, slot), a bitonic
+  // sort of 64-bit keys in LDS over the next power of two (padding sorts last)
   if (n_evict > 0) {
-    for (int s = tid; s < active; s += kPlanThreads) {
-      const float v = score_s[s];
-      int rank = 0;
-      for (int t = 0; t < active; ++t) {
-        const float u = score_s[t];
-        rank += (u < v) || (u == v && t < s);
+    int np2 = 1;
+    while (np2 < active) np2 <<= 1;
+    for (int i = tid; i < np2; i += kPlanThreads)
+      key_s[i] = i < active ? ((unsigned long long)score_order_key(c.slot_score[i]) << 32) | (unsigned)i : ~0ull;
+    __syncthreads();
+    for (int kk = 2; kk <= np2; kk <<= 1) {
+      for (int jj = kk >> 1; jj > 0; jj >>= 1) {
+        for (int i = tid; i < np2; i += kPlanThreads) {
+          const int l = i ^ jj;
+          if (l > i) {
+            const unsigned long long x = key_s[i], y = key_s[l];
+            const bool up = (i & kk) == 0;
+            if (up ? (x > y) : (x < y)) {
+              key_s[i] = y;
+              key_s[l] = x;
+            }
+          }
+        }
+        __syncthreads();
       }
-      if (rank < n_evict) evict_s[rank] = s;
     }
   }
-  __syncthreads();
   double base = 1.0;
   if (active > 0) {
     float m2 = -INFINITY;
@@ -101,7 +134,7 @@ __global__ void __launch_bounds__(kPlanThreads) k_cache_plan(CacheArgs c) {
   // ones are not, so every write below has one writer
   for (int q = tid; q < n_take; q += kPlanThreads) {
     const int b = c.novel[q];
-    const int s = q < n_free ? active + q : evict_s[q - n_free];
+    const int s = q < n_free ? active + q : (int)(key_s[q - n_free] & 0xFFFFFFFFull);
     const int old = c.slot_block[s];
     if (old >= 0 && old < c.NB && c.lookup[old] == s) c.lookup[old] = -1;
     c.lookup[b] = s;
@@ -113,7 +146,8 @@ __global__ void __launch_bounds__(kPlanThreads) k_cache_plan(CacheArgs c) {
   if (c.plan_out != nullptr) {
     for (int i = tid; i < c.n; i += kPlanThreads) {
       const int q = c.plan_out[i];
-      if (q >= 0) c.plan_out[i] = q < n_take ? (q < n_free ? active + q : evict_s[q - n_free]) : -1;
+      if (q >= 0)
+        c.plan_out[i] = q < n_take ? (q < n_free ? active + q : (int)(key_s[q - n_free] & 0xFFFFFFFFull)) : -1;
     }
   }
   if (tid == 0) {
@@ -181,9 +215,12 @@ void launch_cache_promote(const CacheArgs& c, hipStream_t s) {
   static std::once_flag once;
   std::call_once(once, [] {
     (void)hipFuncSetAttribute(reinterpret_cast<const void*>(k_cache_plan),
-                              hipFuncAttributeMaxDynamicSharedMemorySize, (int)(kMaxCacheSlots * sizeof(float)));
+                              hipFuncAttributeMaxDynamicSharedMemorySize,
+                              (int)(kMaxCacheSlots * sizeof(unsigned long long)));
   });
-  k_cache_plan<<<dim3(1), dim3(kPlanThreads), (size_t)c.capacity * sizeof(float), s>>>(c);
+  size_t np2 = 1;
+  while (np2 < (size_t)c.capacity) np2 <<= 1;
+  k_cache_plan<<<dim3(1), dim3(kPlanThreads), np2 * sizeof(unsigned long long), s>>>(c);
   long long total = 0;
   for (int a = 0; a < 6; ++a) total += c.bytes[a];
   const unsigned parts = (unsigned)((total + kCopyPart - 1) / kCopyPart);

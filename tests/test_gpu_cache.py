@@ -53,6 +53,30 @@ def test_promotion_state_matches_oracle(gpu, orc, absmax, grow_only):
         assert np.array_equal(_np(slots), per), step
 
 
+def test_promotion_large_capacity_matches_oracle(gpu, orc):
+    """3000 slots: the eviction order spans several sort keys per thread."""
+    from next_step_ai_amd.slot_table import HotBlockCache
+    from next_step_ai_amd.synth import make_synthetic_layer
+
+    L = make_synthetic_layer(H=512, I=32 * 4096, R=16, seed=66, device=gpu)
+    rng = np.random.default_rng(66)
+    res = rng.choice(L.NB, size=3000, replace=False)
+    t = L.slot_table(resident_blocks=torch.from_numpy(res), host_copy=True)
+    scores = torch.from_numpy(rng.integers(0, 50, size=3000).astype(np.float32))  # ties
+    cache = HotBlockCache(t, scores=scores)
+    lookup, sb, sc, act = _np(t.lookup).astype(np.int64), _np(cache.slot_block).astype(np.int64), _np(
+        cache.slot_score), 3000
+    for step in range(6):
+        sel = np.sort(rng.choice(L.NB, size=700, replace=False)).astype(np.int32)
+        slots = cache.promote(torch.from_numpy(sel), return_slots=True)
+        lookup, sb, sc, act, per = orc.promote_blocks(lookup, sb, sc, act, sel)
+        torch.cuda.synchronize()
+        d_sb, d_sc, d_act, d_lookup = cache.state_cpu()
+        assert d_act == act and np.array_equal(d_lookup.numpy(), lookup), step
+        assert np.array_equal(d_sb.numpy(), sb) and np.array_equal(_np(slots), per), step
+        assert np.array_equal(d_sc.numpy().view(np.uint32), np.asarray(sc, np.float32).view(np.uint32)), step
+
+
 @pytest.mark.parametrize("absmax", ["f32", "dq"])
 def test_promoted_slots_hold_the_blocks(gpu, absmax):
     from next_step_ai_amd.slot_table import HotBlockCache
