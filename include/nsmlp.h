@@ -218,7 +218,7 @@ typedef struct nsmlp_cache_state {
   int32_t* active_count;  /* [1] slots in use (device) */
 } nsmlp_cache_state;
 #define NSMLP_CACHE_GROW_ONLY 1
-size_t nsmlp_cache_workspace_bytes(int n);
+size_t nsmlp_cache_workspace_bytes(int n);  /* starts with the counter region, as every workspace */
 int nsmlp_cache_promote(const nsmlp_slot_table* table, const nsmlp_cache_state* cache, const int32_t* blocks, int n,
                         int flags, int32_t* slot_out, void* ws, size_t ws_bytes, void* stream);
 /* Calibration hit counts (replaces RT:2205-2243 without the host copy):

@@ -805,7 +805,9 @@ int nsmlp_nf4_quantize_f32(const float* w, long long n, int qbs, uint8_t* packed
 
 size_t nsmlp_cache_workspace_bytes(int n) {
   if (n < 0) n = 0;
-  return align_up((size_t)n * 4) * 3 + align_up(4);
+  // the counter region first (left untouched: the workspace may be shared
+  // with the decode entry points), then the novel and copy lists
+  return align_up(kCounterBytes) + align_up((size_t)n * 4) * 3 + align_up(4);
 }
 
 int nsmlp_cache_promote(const nsmlp_slot_table* table, const nsmlp_cache_state* cache, const int32_t* blocks, int n,
@@ -843,7 +845,8 @@ int nsmlp_cache_promote(const nsmlp_slot_table* table, const nsmlp_cache_state* 
   c.active = cache->active_count;
   c.blocks = blocks;
   c.plan_out = slot_out;
-  uint8_t* w = (uint8_t*)ws;
+  if (((uintptr_t)ws & (kAlign - 1)) != 0) return set_error(NSMLP_EINVAL, "workspace must be 256-byte aligned");
+  uint8_t* w = (uint8_t*)ws + align_up(kCounterBytes);
   const size_t ln = align_up((size_t)n * 4);
   c.novel = (int32_t*)w;
   c.copy_block = (int32_t*)(w + ln);

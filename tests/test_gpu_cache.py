@@ -121,6 +121,25 @@ def test_layer_forward_promotes_misses(gpu):
     assert torch.equal(sel2, sel) and torch.equal(out2, out_full)
 
 
+def test_promotion_keeps_the_shared_workspace_counters(gpu):
+    """The promotion shares the stream's workspace with the decode: the
+    generic decode path (hidden 256) relies on its zeroed counters."""
+    from next_step_ai_amd.slot_table import HotBlockCache, SparseMlpLayer
+    from next_step_ai_amd.synth import make_synthetic_layer
+
+    H, I, R, k = 256, 2048, 8, 16
+    L = make_synthetic_layer(H=H, I=I, R=R, seed=67, device=gpu)
+    out_full, sel = L.layer(k).forward(L.x)
+    rng = np.random.default_rng(67)
+    t = L.slot_table(resident_blocks=torch.from_numpy(rng.choice(L.NB, size=20, replace=False)), host_copy=True,
+                     capacity=40)
+    layer = SparseMlpLayer(L.router(), t, k, cache=HotBlockCache(t))
+    for _ in range(3):
+        out, sel2 = layer.forward(L.x)
+        torch.cuda.synchronize()
+        assert torch.equal(sel2, sel) and torch.equal(out, out_full)
+
+
 def test_calibration_counts_match_oracle(gpu, orc):
     import json
     import os
