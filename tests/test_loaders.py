@@ -1,0 +1,174 @@
+"""On-disk formats (CPU): bitsandbytes NF4 safetensors written in the
+published quant-state layout and read back, and the routing artifact as
+the reference's writer builds it (RT:779-991 semantics).  bitsandbytes is
+absent, so the quant-state layout is pinned only by its published form
+(parity unpinned at that boundary)."""
+import json
+
+import numpy as np
+import pytest
+import torch
+
+
+def _nf4(orc, out_f, in_f, seed, nested):
+    from next_step_ai_amd.loaders import Nf4Param
+    from next_step_ai_amd.nested_absmax import NestedAbsmax
+
+    rng = np.random.default_rng(seed)
+    w = (rng.standard_normal(out_f * in_f) * 0.02).astype(np.float32)
+    packed, absmax = orc.nf4_quantize(w, qbs=64)
+    code = torch.from_numpy(orc.nf4_code().astype(np.float32))
+    if nested:
+        q, a2, off = orc.double_quant(absmax, dq_block=256)
+        am = NestedAbsmax(q=torch.from_numpy(q), absmax2=torch.from_numpy(a2),
+                          code2=torch.from_numpy(orc.dynamic_map_signed().astype(np.float32)), offset=float(off),
+                          blocksize=256)
+    else:
+        am = torch.from_numpy(absmax)
+    return Nf4Param(packed=torch.from_numpy(packed), absmax=am, code=code, blocksize=64, shape=(out_f, in_f),
+                    dtype="float16")
+
+
+@pytest.mark.parametrize("nested", [False, True])
+def test_nf4_safetensors_round_trip(tmp_path, orc, nested):
+    from next_step_ai_amd.loaders import SafetensorShards, load_nf4_param, write_nf4_safetensors
+
+    p = _nf4(orc, 96, 128, 1, nested)
+    write_nf4_safetensors(tmp_path / "m.safetensors", {"model.layers.0.mlp.gate_proj.weight": p})
+    s = SafetensorShards(tmp_path)
+    assert "model.layers.0.mlp.gate_proj.weight.quant_state.bitsandbytes__nf4" in s.names()
+    r = load_nf4_param(s, "model.layers.0.mlp.gate_proj.weight")
+    assert r.shape == (96, 128) and r.blocksize == 64 and r.nested == nested
+    assert torch.equal(r.packed, p.packed) and torch.equal(r.code, p.code)
+    if nested:
+        assert torch.equal(r.absmax.q, p.absmax.q) and torch.equal(r.absmax.absmax2, p.absmax.absmax2)
+        assert torch.equal(r.absmax.code2, p.absmax.code2) and r.absmax.offset == np.float32(p.absmax.offset)
+        assert r.absmax.blocksize == 256
+    else:
+        assert torch.equal(r.absmax, p.absmax)
+
+
+def test_quant_state_blob_in_the_published_form(tmp_path, orc):
+    """A file whose quant state is packed by hand, key by key, as
+    bitsandbytes' QuantState.as_dict(packed=True) lays it out."""
+    from safetensors.torch import save_file
+
+    from next_step_ai_amd.loaders import SafetensorShards, load_nf4_param
+
+    p = _nf4(orc, 32, 64, 2, True)
+    meta = {"quant_type": "nf4", "absmax_dtype": None, "blocksize": 64, "dtype": "bfloat16", "shape": [32, 64],
+            "nested_blocksize": 256, "nested_dtype": "float32", "nested_offset": p.absmax.offset}
+    meta.pop("absmax_dtype")
+    blob = torch.tensor(list(json.dumps(meta).encode("utf-8")), dtype=torch.uint8)
+    name = "w.weight"
+    save_file({name: p.packed.reshape(-1, 1), f"{name}.absmax": p.absmax.q, f"{name}.quant_map": p.code,
+               f"{name}.nested_absmax": p.absmax.absmax2, f"{name}.nested_quant_map": p.absmax.code2,
+               f"{name}.quant_state.bitsandbytes__nf4": blob}, str(tmp_path / "a.safetensors"))
+    r = load_nf4_param(SafetensorShards(tmp_path / "a.safetensors"), name)
+    assert r.dtype == "bfloat16" and r.shape == (32, 64) and r.nested
+    assert torch.equal(r.absmax.q, p.absmax.q)
+
+
+def test_nf4_loader_errors(tmp_path, orc):
+    from safetensors.torch import save_file
+
+    from next_step_ai_amd.loaders import SafetensorShards, load_nf4_param
+
+    p = _nf4(orc, 32, 64, 3, False)
+    fp4 = torch.tensor(list(json.dumps({"quant_type": "fp4", "blocksize": 64, "dtype": "float16",
+                                        "shape": [32, 64]}).encode()), dtype=torch.uint8)
+    good = torch.tensor(list(json.dumps({"quant_type": "nf4", "blocksize": 64, "dtype": "float16",
+                                         "shape": [32, 64]}).encode()), dtype=torch.uint8)
+    t = {"a.weight": p.packed.reshape(-1, 1), "a.weight.absmax": p.absmax, "a.weight.quant_map": p.code,
+         "a.weight.quant_state.bitsandbytes__fp4": fp4,
+         "b.weight": p.packed[:-3].reshape(-1, 1), "b.weight.absmax": p.absmax,
+         "b.weight.quant_map": p.code, "b.weight.quant_state.bitsandbytes__nf4": good,
+         "c.weight": p.packed.reshape(-1, 1), "c.weight.absmax": p.absmax,
+         "c.weight.quant_state.bitsandbytes__nf4": good,
+         "d.weight": torch.zeros(4)}
+    save_file({k: v.clone().contiguous() for k, v in t.items()}, str(tmp_path / "e.safetensors"))
+    s = SafetensorShards(tmp_path / "e.safetensors")
+    with pytest.raises(RuntimeError, match="fp4"):
+        load_nf4_param(s, "a.weight")
+    with pytest.raises(RuntimeError, match="packed weight"):
+        load_nf4_param(s, "b.weight")
+    with pytest.raises(RuntimeError, match="quant_map"):
+        load_nf4_param(s, "c.weight")
+    with pytest.raises(RuntimeError, match="quant state"):
+        load_nf4_param(s, "d.weight")
+    with pytest.raises(KeyError):
+        load_nf4_param(s, "missing.weight")
+
+
+def _artifact(H, I, R, layers, *, with_bias=True):
+    g = torch.Generator().manual_seed(5)
+    NB = I // 32
+    states = {}
+    for l in layers:
+        st = {"encoder_weight": torch.randn(R, H, generator=g) * 0.02, "encoder_bias": torch.randn(R, generator=g),
+              "score_weight": torch.randn(NB, R, generator=g), "scale": torch.tensor(1.5),
+              "block_importance": torch.rand(NB, generator=g), "samples": torch.tensor(100.0),
+              "rank_effective": torch.tensor(float(R - 2)), "explained_variance_ratio": torch.tensor(0.8)}
+        if with_bias:
+            st["score_bias"] = torch.randn(NB, generator=g)
+        states[str(l)] = st
+    return {"model_name": "m", "config": {"artifact_target": "intermediate_block_scores",
+                                          "block_domain": "intermediate", "basis_rank": R, "basis_top_k": R,
+                                          "top_k_by_layer": {"1": 5}, "basis_top_k_by_layer": {},
+                                          "block_size": 32, "num_blocks": NB},
+            "layer_selection": list(layers), "layer_states": states, "stats": {}}
+
+
+def test_routing_artifact_layers(tmp_path):
+    from next_step_ai_amd.loaders import load_routing_artifact
+
+    H, I, R = 64, 2048, 8
+    pay = _artifact(H, I, R, [0, 1])
+    pay["layer_states"]["2"] = {"encoder_weight": torch.zeros(R, H), "encoder_bias": torch.zeros(R),
+                                "decoder_blocks": torch.zeros(2, 2), "artifact_target": "output_reconstruction",
+                                "block_domain": "output"}
+    torch.save(pay, tmp_path / "basis.pt")
+    r = load_routing_artifact(tmp_path / "basis.pt", hidden_size=H, intermediate_size=I)
+    assert sorted(r) == [0, 1]  # the output-domain layer belongs to another mode
+    st0 = pay["layer_states"]["0"]
+    assert r[0]["enc_w"].dtype == torch.float16 and torch.equal(r[0]["enc_w"], st0["encoder_weight"].half())
+    assert torch.equal(r[0]["route_score_bias"], st0["score_bias"].half())
+    assert torch.equal(r[0]["dec_norm_t"], st0["score_weight"].half().t().abs())
+    assert r[0]["num_blocks"] == 64 and r[0]["block_size"] == 32 and r[0]["scale"] == 1.5
+    assert r[0]["top_k"] == max(1, round(64 * 0.02)) and r[1]["top_k"] == 5  # default and per-layer override
+    assert r[0]["basis_top_k"] == R - 2 and r[0]["rank_effective"] == R - 2  # clamped to rank_effective
+    assert load_routing_artifact(tmp_path / "basis.pt", hidden_size=H, intermediate_size=I, sparse_top_k=9,
+                                 sparse_basis_top_k=3)[0]["top_k"] == 9
+
+
+def test_routing_artifact_errors(tmp_path):
+    from next_step_ai_amd.loaders import load_routing_artifact
+
+    H, I, R = 64, 2048, 8
+    torch.save(_artifact(H, I, R, [0]), tmp_path / "a.pt")
+    with pytest.raises(RuntimeError, match="expected hidden_size=32"):
+        load_routing_artifact(tmp_path / "a.pt", hidden_size=32, intermediate_size=I)
+    with pytest.raises(RuntimeError, match="expected 32"):
+        load_routing_artifact(tmp_path / "a.pt", hidden_size=H, intermediate_size=1024)
+    bad = _artifact(H, I, R, [0])
+    bad["layer_states"]["0"]["score_bias"] = torch.zeros(7)
+    torch.save(bad, tmp_path / "b.pt")
+    with pytest.raises(RuntimeError, match="score_bias has 7 values"):
+        load_routing_artifact(tmp_path / "b.pt", hidden_size=H, intermediate_size=I)
+
+
+class _Opaque:
+    """Not on torch's safe-load allowlist."""
+
+    def __init__(self):
+        self.v = 1
+
+
+def test_routing_artifact_needing_code_is_refused(tmp_path):
+    from next_step_ai_amd.loaders import load_routing_artifact
+
+    pay = _artifact(64, 2048, 8, [0])
+    pay["extra"] = _Opaque()
+    torch.save(pay, tmp_path / "u.pt")
+    with pytest.raises(RuntimeError, match="cannot be loaded safely"):
+        load_routing_artifact(tmp_path / "u.pt", hidden_size=64, intermediate_size=2048)
