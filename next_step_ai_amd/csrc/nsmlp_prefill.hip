@@ -92,6 +92,16 @@ __device__ __forceinline__ float4_t mfma16(half8_t a, half8_t b, float4_t c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
 }
 
+// Wait states between MFMAs and VALU reads of their results, beyond what the
+// compiler inserts: reads of a 16x16x32 result that follow its MFMA closely
+// have returned values that changed from run to run in the last elements
+// (written last), so MFMA results are read only after this drain.
+__device__ __forceinline__ void mfma_drain() {
+  __builtin_amdgcn_sched_barrier(0);
+  asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory");
+  __builtin_amdgcn_sched_barrier(0);
+}
+
 }  // namespace
 
 
@@ -508,6 +518,7 @@ __global__ void __launch_bounds__(kPfThreads, 2) k_pf_down(PrefillArgs p) {
             float4_t c[4];
 #pragma unroll
             for (int nt = 0; nt < 4; ++nt) c[nt] = mfma16(af, bf[nt], float4_t{0.0f, 0.0f, 0.0f, 0.0f});
+            mfma_drain();
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
               if (tk[r] >= 0) {
