@@ -29,8 +29,9 @@ reference runtime's slot-table format, RT:4621-4625).
 --config 3 measures the same layer with half of the blocks in HBM slots and
 the selected blocks' misses (62 of 208) read from pinned host copies over
 the host link; --config 5 decodes 64 tokens through a stack of 126 resident
-layers (x <- x + mlp(x)) and reports the end-to-end decode_tok_s.  Both
-print the same JSON line shape with their own config.
+layers (x <- x + mlp(x)) and reports the end-to-end decode_tok_s; --config 6
+times the NF4 LM head (vocabulary 128256 x hidden 16384) for one token.
+Each prints the same JSON line shape with its own config.
 
 --copy-calibration BYTES runs only a plain device copy of BYTES (the
 reference kernel for the counter calibration) and prints its size.
@@ -53,7 +54,8 @@ PEAK_GBS = 8000.0
 MODEL_LAYERS = 126
 # config id -> (hidden, intermediate, basis rank, top-k)
 CONFIGS = {1: (4096, 14336, 64, 64), 2: (16384, 53248, 64, 208), 3: (16384, 53248, 64, 208),
-           4: (16384, 53248, 64, 208), 5: (16384, 53248, 64, 208)}
+           4: (16384, 53248, 64, 208), 5: (16384, 53248, 64, 208), 6: (16384, 53248, 64, 208)}
+LM_VOCAB = 128256
 PREFILL_TOKENS = 256
 PEAK_F16_TFLOPS = 2500.0  # dense fp16 MFMA
 WORKLOADS = {
@@ -65,6 +67,8 @@ WORKLOADS = {
        "grouped fp16 MFMA gate/up/down with SiLU fused (hidden 16384, intermediate 53248, block 32)",
     5: "126-layer stack of 405B-shaped MLP layers (hidden 16384, intermediate 53248, top-k 208), all resident; "
        "64 decode tokens at batch 1, x <- x + mlp(x) per layer",
+    6: "405B NF4 LM head decode: logits over vocabulary 128256 from hidden 16384 (dense NF4 GEMV, "
+       "every input block active), one token",
 }
 STACK_LAYERS = 126
 STACK_TOKENS = 64
@@ -433,6 +437,83 @@ def run_stack(args) -> int:
     return 0
 
 
+def lm_head_bytes(V: int, H: int, qbs: int, absmax: str, dq_block: int = 256) -> int:
+    """Bytes one LM-head pass must move: packed NF4 (V H / 2), absmax (fp32,
+    or u8 codes plus one fp32 scale per dq_block codes and the 256-entry
+    second-level table), x (fp16) and the fp16 logits."""
+    n_abs = V * H // qbs
+    ab = 4 * n_abs if absmax == "f32" else n_abs + 4 * ((n_abs + dq_block - 1) // dq_block) + 4 * 256
+    return V * H // 2 + ab + 2 * H + 2 * V + 4 * 16
+
+
+def run_lm_head(args) -> int:
+    """Config 6: the 405B NF4 LM head for one decode token."""
+    import numpy as np
+    import torch
+
+    from next_step_ai_amd.lm_head import dense_linear_nf4
+    from next_step_ai_amd.nested_absmax import NestedAbsmax
+    from next_step_ai_amd._runtime import nf4_code
+    from next_step_ai_amd.synth import synth_nf4, synth_normal_f16
+
+    device = torch.device("cuda", 0)
+    torch.cuda.set_device(device)
+    V, H, qbs = LM_VOCAB, 16384, 64
+    packed, absmax = synth_nf4(6001, V * H, qbs, 0.02, device)
+    if args.absmax == "dq8":
+        absmax = NestedAbsmax.quantize(absmax)
+    code = nf4_code(device)
+    xs = [synth_normal_f16(6100 + t, (1, H), 1.0, device) for t in range(4)]
+    for i in range(args.warmup):
+        dense_linear_nf4(xs[i % 4], packed, absmax, code, V, H, qbs)
+    torch.cuda.synchronize()
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(args.steps)]
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        ev[i][0].record()
+        dense_linear_nf4(xs[i % 4], packed, absmax, code, V, H, qbs)
+        ev[i][1].record()
+    torch.cuda.synchronize()
+    wall_us = (time.perf_counter() - t0) / args.steps * 1e6
+    us = statistics.mean(a.elapsed_time(b) for a, b in ev) * 1e3
+    nbytes = lm_head_bytes(V, H, qbs, args.absmax)
+    gbs = nbytes / (us * 1e-6) / 1e9
+    res = base_result(args, 1e6 / wall_us, wall_us, H, 0, 0, 0, qbs)
+    res["metric"] = "NF4 LM head µs/token + HBM GB/s vs peak, vocabulary 128256 x hidden 16384"
+    res["config"] = {"workload": WORKLOADS[6] + f"; NF4 qbs {qbs} with "
+                     + ("double-quantised absmax (u8, fp32 per 256, offset)" if args.absmax == "dq8"
+                        else "fp32 absmax"),
+                     "vocab": V, "hidden": H, "quant_block": qbs, "absmax": args.absmax, "rows": 1}
+    res.update({
+        "lm_head_us": round(us, 3),
+        "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": PEAK_GBS, "unit": "GB/s",
+                     "frac": round(gbs / PEAK_GBS, 4), "traffic": None, "algorithmic_bytes": nbytes,
+                     "kernel": "k_rows_rep"},
+    })
+    if not args.no_cpu_baseline:
+        from oracle import oracle as orc
+
+        sample = 2048
+        pk = packed.view(V, H // 2)[:sample].cpu().numpy()
+        am = (absmax.resolve() if isinstance(absmax, NestedAbsmax) else absmax).view(V, H // qbs)[:sample].cpu().numpy()
+        xh = xs[0].cpu().view(torch.int16).numpy().view(np.uint16)
+        orc.set_num_threads(host_threads())
+        times = []
+        for _ in range(max(1, args.cpu_runs)):
+            c0 = time.perf_counter()
+            orc.dense_linear_nf4(xh, pk, am, sample, H, qbs)
+            times.append(time.perf_counter() - c0)
+        full_s = statistics.median(times) * V / sample
+        res["cpu_baseline"] = {"value": round(1.0 / full_s, 4), "unit": "tok/s", "cores": host_threads(),
+                               "kind": "port",
+                               "sample": f"oracle NF4 dequant + fp64 GEMV over the first {sample} of {V} vocabulary "
+                                         f"rows, median of {max(1, args.cpu_runs)}, scaled by {V}/{sample}; "
+                                         f"{cpu_model()}",
+                               "us_per_token": round(full_s * 1e6, 1)}
+    print(json.dumps(res), flush=True)
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -458,6 +539,8 @@ def main() -> int:
         return run_prefill(args)
     if args.config == 5:
         return run_stack(args)
+    if args.config == 6:
+        return run_lm_head(args)
 
     import torch
 

@@ -272,14 +272,46 @@ int nsmlp_output_linear_nf4_f16(const void* x, int rows, int in_dim, const int32
 
 /* Replaces TSM:1303-1337 (triton_sparse_input_linear_4bit) with row-major
  * NF4 semantics (RT:5651-5675 passes the gathered down weight [H][A*32] with
- * quant block 32, i.e. absmax [H][A]):
- *   out[t][o] = sum_{s in active_idx[t]} sum_j W[o][s*32 + j] x[t][s*32 + j] + bias[o]
+ * quant block 32, i.e. absmax [H][A]; runtime/lm_head.py:461-473 passes the
+ * LM head with blocks of 256 columns, all active):
+ *   out[t][o] = sum_{s in active_idx[t]} sum_{j < B} W[o][s*B + j] x[t][s*B + j] + bias[o]
+ * B = block_size, a multiple of 32; entries < 0 or past in_features skipped.
  * W [out_features][in_features] NF4 (absmax per qbs elements),
  * x [rows][in_features], out [rows][out_features] fp16.
  */
 int nsmlp_input_linear_nf4_f16(const void* x, int rows, int in_features, const int32_t* active_idx, int kk,
                                const uint8_t* packed, const float* absmax, const float* code, int qbs,
                                int out_features, const void* bias, int block_size, void* out, void* stream);
+
+/* Dense NF4 matrix (no bias, version >= 102): the LM head the reference keeps on the GPU
+ * (runtime/lm_head.py:267-350 materialises it, bitsandbytes' flat layout:
+ * packed [out][in/2], high nibble first, absmax over qbs consecutive
+ * elements of the flat row-major weight).  dq_block > 0 (power of two):
+ * absmax is double-quantised, absmax = code2[qabsmax[i]] * absmax2[i /
+ * dq_block] + offset (two fp32 roundings), and the fp32 absmax is ignored. */
+typedef struct nsmlp_nf4_matrix {
+  int out_features;
+  int in_features;       /* multiple of 32, <= 16384 */
+  int qbs;               /* power of two >= 32 dividing in_features */
+  const uint8_t* packed; /* [out][in/2], 16-byte aligned */
+  const float* absmax;   /* [out*in/qbs] f32 (dq_block == 0) */
+  const float* code;     /* [16] NF4 code book (device) */
+  int dq_block;
+  const uint8_t* qabsmax; /* [out*in/qbs] u8 */
+  const float* absmax2;   /* [ceil(out*in/qbs / dq_block)] f32 */
+  const float* code2;     /* [256] f32 */
+  float offset;
+} nsmlp_nf4_matrix;
+
+/* Replaces runtime/lm_head.py:450-474 (_lm_head_forward: the NF4 LM head
+ * through triton_sparse_input_linear_4bit with every input block active):
+ *   out[t][o] = sum_c W[o][c] x[t][c],  t < rows
+ * x [rows][in] fp16 (16-byte aligned), out [rows][out] fp16, out_f32
+ * [rows][out] (nullable) the same sums before the fp16 rounding.  One pass
+ * over the weight per two rows.  in_features > 16384: use
+ * nsmlp_input_linear_nf4_f16 with every block active. */
+int nsmlp_dense_linear_nf4_f16(const nsmlp_nf4_matrix* w, const void* x, int rows, void* out, float* out_f32,
+                               void* stream);
 
 /* silu(gate) * up elementwise in fp32, rounded to fp16 (TSM:1577-1578). */
 int nsmlp_silu_mul_f16(const void* gate, const void* up, void* out, long long n, void* stream);

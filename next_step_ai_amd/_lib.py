@@ -62,6 +62,15 @@ class Router(ctypes.Structure):
     ]
 
 
+class Nf4Matrix(ctypes.Structure):
+    """Mirror of ``nsmlp_nf4_matrix``."""
+
+    _fields_ = [
+        ("out_features", I32), ("in_features", I32), ("qbs", I32), ("packed", P), ("absmax", P), ("code", P),
+        ("dq_block", I32), ("qabsmax", P), ("absmax2", P), ("code2", P), ("offset", F32),
+    ]
+
+
 class CacheState(ctypes.Structure):
     """Mirror of ``nsmlp_cache_state``."""
 
@@ -89,6 +98,7 @@ SIGNATURES: dict[str, tuple] = {
     "nsmlp_output_linear_workspace_bytes": (SZ, [I32, I32, I32]),
     "nsmlp_output_linear_nf4_f16": (I32, [P, I32, I32, P, I32, I32, P, P, P, P, I32, P, I32, P, P, SZ, P]),
     "nsmlp_input_linear_nf4_f16": (I32, [P, I32, I32, P, I32, P, P, P, I32, I32, P, I32, P, P]),
+    "nsmlp_dense_linear_nf4_f16": (I32, [ctypes.POINTER(Nf4Matrix), P, I32, P, P, P]),
     "nsmlp_silu_mul_f16": (I32, [P, P, P, I64, P]),
     "nsmlp_gather_row_blocks": (I32, [P, P, I32, P, I32, I32, I32, P, P, P]),
     "nsmlp_gather_down_columns": (I32, [P, P, P, I32, I32, I32, I32, I32, P, P, P]),

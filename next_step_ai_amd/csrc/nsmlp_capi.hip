@@ -366,7 +366,7 @@ extern "C" {
 
 const char* nsmlp_last_error(void) { return g_err; }
 
-int nsmlp_version(void) { return 101; }
+int nsmlp_version(void) { return 102; }
 
 int nsmlp_device_supported(int device) {
   hipDeviceProp_t prop;
@@ -669,10 +669,12 @@ int nsmlp_output_linear_nf4_f16(const void* x, int rows, int in_dim, const int32
 int nsmlp_input_linear_nf4_f16(const void* x, int rows, int in_features, const int32_t* active_idx, int kk,
                                const uint8_t* packed, const float* absmax, const float* code, int qbs,
                                int out_features, const void* bias, int block_size, void* out, void* stream) {
-  if (block_size != 32) return set_error(NSMLP_EINVAL, "block_size must be 32 (got %d)", block_size);
+  if (block_size <= 0 || block_size % 32 != 0)
+    return set_error(NSMLP_EINVAL, "block_size must be a multiple of 32 (got %d)", block_size);
   if (rows <= 0 || kk <= 0 || out_features <= 0) return set_error(NSMLP_EINVAL, "rows, kk, out_features must be > 0");
-  if (in_features <= 0 || in_features % 32 != 0)
-    return set_error(NSMLP_EINVAL, "in_features %d must be a multiple of 32", in_features);
+  if (in_features <= 0 || in_features % block_size != 0)
+    return set_error(NSMLP_EINVAL, "in_features %d must be a multiple of block_size %d", in_features, block_size);
+  if ((long long)kk * (block_size / 32) > INT32_MAX / 2) return set_error(NSMLP_EINVAL, "kk * block_size too large");
   if (qbs <= 0 || qbs % 32 != 0 || in_features % qbs != 0)
     return set_error(NSMLP_EINVAL, "quant block size %d must be a multiple of 32 dividing %d", qbs, in_features);
   if (!x || !active_idx || !packed || !absmax || !code || !out) return set_error(NSMLP_EINVAL, "NULL tensor argument");
@@ -691,8 +693,66 @@ int nsmlp_input_linear_nf4_f16(const void* x, int rows, int in_features, const i
   l.qbs = qbs;
   l.bias = (const uint16_t*)bias;
   l.out = (uint16_t*)out;
+  l.bm = block_size / 32;
   launch_input_linear(l, (hipStream_t)stream);
   return check_launch("input linear");
+}
+
+int nsmlp_dense_linear_nf4_f16(const nsmlp_nf4_matrix* w, const void* x, int rows, void* out, float* out_f32,
+                               void* stream) {
+  if (!w) return set_error(NSMLP_EINVAL, "NULL matrix");
+  const int in = w->in_features, O = w->out_features, qbs = w->qbs;
+  if (rows < 0 || O <= 0) return set_error(NSMLP_EINVAL, "rows must be >= 0 and out_features > 0");
+  if (in <= 0 || in % 32 != 0 || in > 16384)
+    return set_error(NSMLP_EINVAL,
+                     "in_features %d must be a multiple of 32 up to 16384 (nsmlp_input_linear_nf4_f16 takes any)", in);
+  if (qbs < 32 || (qbs & (qbs - 1)) != 0 || in % qbs != 0)
+    return set_error(NSMLP_EINVAL, "quant block size %d must be a power of two >= 32 dividing %d", qbs, in);
+  const bool dq = w->dq_block > 0;
+  if (w->dq_block < 0 || (dq && (w->dq_block & (w->dq_block - 1)) != 0))
+    return set_error(NSMLP_EINVAL, "dq_block %d must be 0 or a power of two", w->dq_block);
+  const long long pbytes = (long long)O * (in / 2);
+  const long long nabs = (long long)O * (in / qbs);
+  if (pbytes >= (1LL << 31) || nabs * 4 >= (1LL << 31))
+    return set_error(NSMLP_EINVAL, "matrix of %d x %d exceeds 2 GiB of packed weight", O, in);
+  if (rows == 0) return NSMLP_OK;
+  if (!x || !out || !w->packed || !w->code) return set_error(NSMLP_EINVAL, "NULL tensor argument");
+  if (dq ? (!w->qabsmax || !w->absmax2 || !w->code2) : !w->absmax)
+    return set_error(NSMLP_EINVAL, "NULL absmax argument");
+  if (!aligned16(w->packed) || !aligned16(x)) return set_error(NSMLP_EINVAL, "packed weight and x must be 16-byte aligned");
+  RowsArgs a;
+  memset(&a, 0, sizeof(a));
+  a.in = in;
+  a.out = O;
+  a.qbs_shift = __builtin_ctz((unsigned)qbs);
+  a.packed = w->packed;
+  a.rs = in / 2;
+  a.p_bytes = (int)pbytes;
+  a.ars = in / qbs;
+  a.dq = dq ? 1 : 0;
+  if (dq) {
+    a.qabsmax = w->qabsmax;
+    a.a_bytes = (int)nabs;
+    a.absmax2 = w->absmax2;
+    a.dq_shift = __builtin_ctz((unsigned)w->dq_block);
+    a.a2_bytes = (int)(((nabs + w->dq_block - 1) >> a.dq_shift) * 4);
+    a.code2 = w->code2;
+    a.offset = w->offset;
+  } else {
+    a.absmax = w->absmax;
+    a.a_bytes = (int)(nabs * 4);
+  }
+  a.code = w->code;
+  const int cus = device_cus();
+  for (int t = 0; t < rows; t += 2) {
+    const int nt = rows - t >= 2 ? 2 : 1;
+    if (!plan_rows(a, nt, cus)) return set_error(NSMLP_EINVAL, "dense linear geometry not supported");
+    a.x = (const uint16_t*)x + (long long)t * in;
+    a.y = (uint16_t*)out + (long long)t * O;
+    a.out_f32 = out_f32 ? out_f32 + (long long)t * O : nullptr;
+    launch_rows(a, nt, (hipStream_t)stream);
+  }
+  return check_launch("dense linear");
 }
 
 int nsmlp_silu_mul_f16(const void* gate, const void* up, void* out, long long n, void* stream) {

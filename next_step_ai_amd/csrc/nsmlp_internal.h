@@ -619,6 +619,32 @@ struct PrefillArgs {
 };
 void launch_prefill(const PrefillArgs& p, hipStream_t s);
 
+// Dense NF4 rows (the LM head): y[t][o] = sum_i W[o][i] x[t][i] over a
+// row-major [out][in] NF4 matrix, in % 32 == 0, in <= 16384.
+struct RowsArgs {
+  const uint16_t* x;  // [nt][in] fp16
+  int in, out;
+  int qbs_shift;
+  const uint8_t* packed;  // [out][in/2]
+  int rs;                 // bytes per row (in / 2)
+  int p_bytes;            // out * rs (buffer extent)
+  int ars;                // absmax per row (in / qbs)
+  const float* absmax;    // [out][in/qbs] f32 (dq = 0)
+  const uint8_t* qabsmax; // [out][in/qbs] u8 codes (dq = 1)
+  int a_bytes;            // extent of the absmax array
+  const float* absmax2;   // per dq block of the flat absmax index
+  int a2_bytes;
+  const float* code2;     // [256]
+  float offset;
+  int dq, dq_shift;
+  const float* code;      // [16]
+  uint16_t* y;            // [nt][out] fp16
+  float* out_f32;         // [nt][out] or NULL
+  int splits, rounds, wgs;
+};
+bool plan_rows(RowsArgs& a, int nt, int cus);  // nt tokens per pass (1 or 2)
+void launch_rows(const RowsArgs& a, int nt, hipStream_t s);
+
 // Hot-block cache maintenance (fixed-capacity promotion and calibration
 // counts) over a slot table with pinned host copies.
 constexpr int kMaxCacheSlots = 8192;  // capacity limit (eviction order staged in LDS)
@@ -694,6 +720,7 @@ struct LinearArgs {
   uint16_t* out;
   int cs, splits;             // output linear column split
   float* part;                // [rows*kk][splits][32]
+  int bm;                     // input linear: 32-column slots per active block
 };
 
 void launch_output_linear(const LinearArgs& a, hipStream_t s);

@@ -91,11 +91,15 @@ __global__ void __launch_bounds__(kThreads) k_in_linear(LinearArgs a) {
   const long long row_bytes = a.in_dim / 2;
   const long long row_abs = a.in_dim / a.qbs;
   float acc = 0.0f;
-  for (int ib = 0; ib < a.kk; ib += kInBatch) {
+  // active block e / bm contributes its 32-column slot e % bm
+  const int n = a.kk * a.bm;
+  for (int ib = 0; ib < n; ib += kInBatch) {
     __syncthreads();
     if (tid < kInBatch) {
-      int sl = ib + tid < a.kk ? a.active_idx[(long long)t * a.kk + ib + tid] : -1;
-      slots[tid] = (sl >= 0 && (long long)sl * 32 < a.in_dim) ? sl : -1;
+      const int e = ib + tid;
+      const int blk = e < n ? a.active_idx[(long long)t * a.kk + e / a.bm] : -1;
+      const long long sl = (long long)blk * a.bm + e % a.bm;
+      slots[tid] = (blk >= 0 && sl * 32 < a.in_dim) ? (int)sl : -1;
     }
     __syncthreads();
     for (int e = tid; e < kInBatch * 32; e += kThreads) {

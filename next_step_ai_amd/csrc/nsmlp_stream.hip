@@ -574,6 +574,137 @@ __global__ void __launch_bounds__(256) k_fin_rep(DecodeArgs a) {
   a.out[o] = f2h(y);
 }
 
+// Dense NF4 rows (the LM head: all rows of a row-major [out][in] NF4
+// matrix times NT token vectors).  The structure of k_gu_rep without the
+// block selection: an item is 4 consecutive rows; in a round every wave
+// decodes one item over its 2048-column split (16 packed bytes per lane and
+// row) through the replicated byte-pair table, dots it with each token's
+// split (fp16 pairs in registers), scales each row sum by its absmax, and
+// the split sums meet in LDS behind one LDS-only barrier per round.  S =
+// ceil(in / 2048) splits, 8 / S items per workgroup round; lanes past the
+// last column load zeros, waves past the last item group stay idle.
+struct RwStage {
+  uint4 w[4];
+  float am[4];     // fp32 absmax, or the absmax2 (double-quantised)
+  uint32_t qa[4];  // u8 absmax code (double-quantised)
+};
+
+// item < 0: zeros (idle wave or past the last round); colok: the lane's 32
+// columns lie inside the row.
+template <bool DQ>
+__device__ __forceinline__ void rw_issue(const RowsArgs& a, int item, bool colok, uint32_t cb, uint32_t ca,
+                                         RwStage& st) {
+  const rsrc_t rp = make_rsrc(a.packed, a.p_bytes);
+  const bool lane_ok = colok && item >= 0;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int row = 4 * item + i;  // uniform over the wave: its offset goes in soffset
+    const bool live = lane_ok && row < a.out;
+    st.w[i] = buf_ld16(rp, live ? cb : kOffNone, live ? (uint32_t)row * (uint32_t)a.rs : 0u);
+    const uint32_t ai = (uint32_t)row * (uint32_t)a.ars + ca;  // flat absmax index
+    if constexpr (DQ) {
+      st.qa[i] = buf_ldu8(make_rsrc(a.qabsmax, a.a_bytes), live ? ai : kOffNone, 0);
+      st.am[i] = buf_ldfc(make_rsrc(a.absmax2, a.a2_bytes), live ? (ai >> a.dq_shift) * 4u : kOffNone, 0);
+    } else {
+      st.qa[i] = 0;
+      st.am[i] = buf_ldf(make_rsrc(a.absmax, a.a_bytes), live ? ca * 4u : kOffNone,
+                         live ? (uint32_t)row * (uint32_t)a.ars * 4u : 0u);
+    }
+  }
+}
+
+constexpr int kRwStages = 2;
+
+// One token fits 128 VGPRs (two workgroups per CU); two tokens take one.
+template <int NT>
+constexpr int rows_wgs_per_cu() {
+  return NT == 1 ? 2 : 1;
+}
+
+template <bool DQ, int NT>
+__global__ void __launch_bounds__(kThreads8, 2 * rows_wgs_per_cu<NT>()) k_rows_rep(RowsArgs a) {
+  extern __shared__ __attribute__((aligned(16))) uint32_t lds[];
+  float* comb = reinterpret_cast<float*>(lds + kLutWords);     // [2][8][4 NT]
+  float* c2 = comb + 2 * kWaves * 4 * NT;                      // [256] (DQ)
+  const int tid = threadIdx.x, lane = tid & (kWave - 1);
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int S = a.splits, NS = kWaves / S;
+  const int s = wave % S, q = wave / S;
+  const bool idle = q >= NS;
+  const int nwg = (int)gridDim.x, wg = (int)blockIdx.x;
+  const uint32_t col = (uint32_t)(s * kSplit + lane * 32);
+  const bool colok = (int)col < a.in;
+  const uint32_t cb = col >> 1, ca = col >> a.qbs_shift;
+  LutCodes codes;
+  lut_codes_load(a.code, a.code, tid, codes);
+  float c2v = 0.0f;
+  if constexpr (DQ) c2v = a.code2[tid & 255];
+  uint32_t xp[NT][16];
+#pragma unroll
+  for (int t = 0; t < NT; ++t) {
+    const uint4* xv = reinterpret_cast<const uint4*>(a.x + (long long)t * a.in + (colok ? col : 0u));
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const uint4 u = colok ? xv[v] : make_uint4(0u, 0u, 0u, 0u);
+      xp[t][4 * v] = u.x;
+      xp[t][4 * v + 1] = u.y;
+      xp[t][4 * v + 2] = u.z;
+      xp[t][4 * v + 3] = u.w;
+    }
+  }
+  RwStage st[kRwStages];
+#pragma unroll
+  for (int i = 0; i < kRwStages; ++i)
+    rw_issue<DQ>(a, !idle && i < a.rounds ? (i * nwg + wg) * NS + q : -1, colok, cb, ca, st[i]);
+  sched_fence();
+  lut_store(lds, codes, tid);
+  if constexpr (DQ) {
+    if (tid < 256) c2[tid] = c2v;
+  }
+  lds_barrier();
+  uint32_t ad[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) ad[i] = (uint32_t)lane * 4u;
+  for (int r0 = 0; r0 < a.rounds; r0 += kRwStages) {
+#pragma unroll
+    for (int i = 0; i < kRwStages; ++i) {
+      const int r = r0 + i;
+      const bool live = r < a.rounds;  // uniform over the workgroup
+      const int item = (r * nwg + wg) * NS + q;
+      float acc[NT][4];
+      if (live) {
+#pragma unroll
+        for (int m = 0; m < 4; ++m) {
+          float am = st[i].am[m];
+          if constexpr (DQ) am = dq_absmax(c2[st[i].qa[m]], st[i].am[m], a.offset);
+#pragma unroll
+          for (int t = 0; t < NT; ++t) acc[t][m] = rep_dot32(st[i].w[m], xp[t], ad) * am;
+        }
+      }
+      const int rn = r + kRwStages;
+      rw_issue<DQ>(a, !idle && rn < a.rounds ? (rn * nwg + wg) * NS + q : -1, colok, cb, ca, st[i]);
+      if (live) {
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+          const float v = reduce4(acc[t], lane);
+          if ((lane & 15) == 0) comb[((r & 1) * kWaves + wave) * 4 * NT + 4 * t + (lane >> 4)] = v;
+        }
+        lds_barrier();
+        if (!idle && s == 0 && lane < 4 * NT) {
+          // row 4 item + lane % 4 of token lane / 4: splits added in order
+          const int t = lane >> 2, m = lane & 3, row = 4 * item + m;
+          float y = 0.0f;
+          for (int sp = 0; sp < S; ++sp) y += comb[((r & 1) * kWaves + q * S + sp) * 4 * NT + 4 * t + m];
+          if (row < a.out) {
+            if (a.out_f32 != nullptr) a.out_f32[(long long)t * a.out + row] = y;
+            a.y[(long long)t * a.out + row] = f2h(y);
+          }
+        }
+      }
+    }
+  }
+}
+
 int env_or(const char* name, int dflt) {
   const char* v = getenv(name);
   return (v != nullptr && *v != 0) ? atoi(v) : dflt;
@@ -692,6 +823,31 @@ void launch_decode_streaming(const DecodeArgs& a, hipStream_t s) {
   else
     k_down_rep<false><<<gd, bd, kDnLds, s>>>(a);
   if (a.st_dn_gx > 1) hipLaunchKernelGGL(k_fin_rep, dim3(a.H / 256), dim3(256), 0, s, a);
+}
+
+bool plan_rows(RowsArgs& a, int nt, int cus) {
+  if (a.in <= 0 || a.in % 32 != 0 || a.in > kWaves * kSplit || a.out <= 0 || cus <= 0 || nt < 1 || nt > 2)
+    return false;
+  const int S = (a.in + kSplit - 1) / kSplit, NS = kWaves / S;
+  const long long items = (a.out + 3) / 4;
+  const long long per_round = (long long)(nt == 1 ? rows_wgs_per_cu<1>() : rows_wgs_per_cu<2>()) * cus * NS;
+  const long long R = (items + per_round - 1) / per_round;
+  a.splits = S;
+  a.rounds = (int)R;
+  a.wgs = (int)((items + R * NS - 1) / (R * NS));
+  return true;
+}
+
+void launch_rows(const RowsArgs& a, int nt, hipStream_t s) {
+  using Fn = void (*)(RowsArgs);
+  static const Fn fns[2][2] = {{k_rows_rep<false, 1>, k_rows_rep<false, 2>}, {k_rows_rep<true, 1>, k_rows_rep<true, 2>}};
+  const size_t lds = (size_t)kRepLutBytes + 2 * kWaves * 4 * 2 * sizeof(float) + 256 * sizeof(float);
+  static std::once_flag once;
+  std::call_once(once, [lds] {
+    for (int d = 0; d < 2; ++d)
+      for (int t = 0; t < 2; ++t) set_lds_limit(fns[d][t], lds);
+  });
+  fns[a.dq ? 1 : 0][nt == 2 ? 1 : 0]<<<dim3(a.wgs), dim3(kThreads8), lds, s>>>(a);
 }
 
 }  // namespace nsmlp

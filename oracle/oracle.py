@@ -26,6 +26,8 @@ Pinning status (what checks each function, see tests/test_oracle_*.py):
                          bitsandbytes itself is absent: parity unpinned
   double quant           closed-form invariants; bitsandbytes absent: parity unpinned
   sparse_mlp             dense-MLP closed form (all blocks), numpy fp64
+  dense_linear_nf4       hand-packed known answers (codes -1/0/+1, power-of-
+                         two absmax, integer x: exact sums), ragged shapes
 """
 from __future__ import annotations
 
@@ -461,6 +463,19 @@ def sparse_mlp(x16, active_local, gate_packed, gate_absmax, up_packed, up_absmax
     if rc != 0:
         raise ValueError("unsupported shape")
     return ye, yf
+
+
+def dense_linear_nf4(x16, packed, absmax, out_features, in_features, qbs, code=None):
+    """The NF4 LM head (runtime/lm_head.py:450-474: triton_sparse_input_linear_4bit
+    with every block active over the row-major [V, H] weight):
+    y[t][o] = sum_c fp32(code[nib(o, c)] * absmax[(o*H + c) // qbs]) * x[t][c],
+    element o*H + c in the high nibble of its byte when even (TSM:499-507,
+    with the row-major element index the LM-head meta holds, lm_head.py:221-241).
+    x16: fp16 bits [rows, H].  Returns the fp64 sums [rows, V]."""
+    x = f16_bits_to_f32(np.asarray(x16, dtype=np.uint16).reshape(-1, int(in_features))).astype(np.float64)
+    w = nf4_dequant(packed, absmax, int(out_features) * int(in_features), int(qbs), code)
+    w = w.reshape(int(out_features), int(in_features)).astype(np.float64)
+    return x @ w.T
 
 
 def rel_l2(a, b) -> float:
