@@ -30,7 +30,8 @@ reference runtime's slot-table format, RT:4621-4625).
 the selected blocks' misses (62 of 208) read from pinned host copies over
 the host link; --config 5 decodes 64 tokens through a stack of 126 resident
 layers (x <- x + mlp(x)) and reports the end-to-end decode_tok_s; --config 6
-times the NF4 LM head (vocabulary 128256 x hidden 16384) for one token.
+times the NF4 LM head (vocabulary 128256 x hidden 16384) for one token;
+--graph replays each config-5 token as one captured HIP graph.
 Each prints the same JSON line shape with its own config.
 
 --copy-calibration BYTES runs only a plain device copy of BYTES (the
@@ -411,6 +412,11 @@ def run_stack(args) -> int:
             x, y = y, x
         return x
 
+    if args.graph:  # the whole token as one captured graph
+        from next_step_ai_amd.decode_graph import StackGraph
+
+        g = StackGraph(mlps)
+        token = g.run  # noqa: F811
     for t in range(args.warmup):
         token(tokens[STACK_TOKENS + t])
     torch.cuda.synchronize()
@@ -424,7 +430,7 @@ def run_stack(args) -> int:
     layer_bytes = algorithmic_bytes(H, I, k, qbs, args.absmax) + router_bytes(H, R, I // 32)
     res = base_result(args, tok_s, us_layer, H, I, R, k, qbs)
     res["steps"] = STACK_TOKENS
-    res["config"].update({"layers": STACK_LAYERS, "tokens": STACK_TOKENS,
+    res["config"].update({"layers": STACK_LAYERS, "tokens": STACK_TOKENS, "graph": bool(args.graph),
                           "resident_bytes": int(torch.cuda.memory_allocated(device))})
     res.update({
         "us_per_layer": round(us_layer, 3),
@@ -524,6 +530,8 @@ def main() -> int:
     ap.add_argument("--cpu-runs", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="BYTES")
+    ap.add_argument("--graph", action="store_true",
+                    help="config 5: replay each token as one captured graph instead of eager launches")
     ap.add_argument("--absmax", choices=("dq8", "f32"), default="dq8",
                     help="absmax storage: double-quantised u8 (default) or resolved fp32")
     args = ap.parse_args()

@@ -1,0 +1,98 @@
+"""Graph-captured decode (LayerGraph, StackGraph) against eager launches.
+
+Bar: bit-identical outputs and selections on every replay, with eager work and
+synchronisations between the replays (the decode kernels are deterministic,
+so a replay must reproduce the eager launch exactly); with a hot-block cache
+the promotion runs inside the graph and the cache state after each token
+equals the eager one.
+"""
+import numpy as np
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+
+
+def _inputs(gpu, H, n, seed):
+    from next_step_ai_amd.synth import synth_normal_f16
+
+    return [synth_normal_f16(seed * 100 + t, (H,), 1.0, gpu) for t in range(n)]
+
+
+@pytest.mark.parametrize("H,I,R,k", [(1024, 4096, 16, 40), (4096, 14336, 64, 64)])
+def test_layer_graph_replays_match_eager(gpu, H, I, R, k):
+    from next_step_ai_amd.decode_graph import LayerGraph
+    from next_step_ai_amd.synth import make_synthetic_layer
+
+    print(f"layer graph H={H} I={I} k={k}", flush=True)
+    L = make_synthetic_layer(H=H, I=I, R=R, seed=71, device=gpu, double_quant=True)
+    layer = L.layer(k)
+    g = LayerGraph(layer)
+    other = make_synthetic_layer(H=H, I=I, R=R, seed=72, device=gpu).layer(k)
+    for t, x in enumerate(_inputs(gpu, H, 4, 71)):
+        ref_out, ref_sel = layer.forward(x)
+        ref_out, ref_sel = ref_out.clone(), ref_sel.clone()
+        other.forward(x)  # eager work on the same stream between replays
+        out, sel = g.run(x)
+        torch.cuda.synchronize()
+        assert torch.equal(sel, ref_sel), f"token {t}: selection differs"
+        assert torch.equal(out, ref_out), f"token {t}: output differs"
+        g.run(x * 0.5)  # another replay in between
+        torch.cuda.synchronize()
+        out2, sel2 = g.run(x)
+        torch.cuda.synchronize()
+        assert torch.equal(out2, ref_out) and torch.equal(sel2, ref_sel)
+
+
+def test_stack_graph_matches_eager_token_loop(gpu):
+    from next_step_ai_amd.decode_graph import StackGraph
+    from next_step_ai_amd.synth import make_synthetic_layer
+
+    H, I, R, k, n_layers = 2048, 8192, 16, 64, 5
+    print(f"stack graph H={H} layers={n_layers}", flush=True)
+    layers = [make_synthetic_layer(H=H, I=I, R=R, seed=80 + l, device=gpu).layer(k) for l in range(n_layers)]
+    g = StackGraph(layers)
+    for t, x0 in enumerate(_inputs(gpu, H, 3, 80)):
+        x = x0.clone()
+        sels = []
+        for m in layers:
+            out, sel = m.forward(x)
+            sels.append(sel.clone())
+            x = x + out
+        ref = x.clone()
+        y = g.run(x0)
+        torch.cuda.synchronize()
+        assert torch.equal(y, ref), f"token {t}: stack output differs"
+        for l in range(n_layers):
+            assert torch.equal(g.sels[l], sels[l]), f"token {t}: layer {l} selection differs"
+
+
+def test_layer_graph_with_hot_cache_promotion(gpu):
+    """Partial residency with a fixed-capacity cache: the captured graph runs
+    the decode and the promotion of its misses; two identical tables, one
+    eager and one replayed, stay identical token after token."""
+    from next_step_ai_amd.decode_graph import LayerGraph
+    from next_step_ai_amd.slot_table import HotBlockCache, SparseMlpLayer
+    from next_step_ai_amd.synth import make_synthetic_layer
+
+    H, I, R, k = 2048, 8192, 16, 48
+    print("layer graph with cache", flush=True)
+    L = make_synthetic_layer(H=H, I=I, R=R, seed=91, device=gpu)
+    rng = np.random.default_rng(91)
+    resident = torch.from_numpy(rng.choice(L.NB, size=64, replace=False))
+    layers = []
+    for _ in range(2):
+        t = L.slot_table(resident_blocks=resident, host_copy=True, capacity=96)
+        layers.append(SparseMlpLayer(L.router(), t, k, cache=HotBlockCache(t)))
+    eager, captured = layers
+    g = LayerGraph(captured)  # its warm-up decodes a zero token
+    eager.forward(torch.zeros(H, dtype=torch.float16, device=gpu))
+    for t, x in enumerate(_inputs(gpu, H, 6, 91)):
+        ref_out, ref_sel = eager.forward(x)
+        out, sel = g.run(x)
+        torch.cuda.synchronize()
+        assert torch.equal(sel, ref_sel) and torch.equal(out, ref_out), f"token {t}: output differs"
+        for a, b in zip(eager.cache.state_cpu()[:2], captured.cache.state_cpu()[:2]):
+            assert torch.equal(a, b), f"token {t}: cache state differs"
+        assert eager.cache.state_cpu()[2] == captured.cache.state_cpu()[2]
+        assert torch.equal(eager.table.lookup, captured.table.lookup)
