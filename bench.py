@@ -407,8 +407,11 @@ def run_stack(args) -> int:
         xa.copy_(x0)
         x, y = xa, xb
         for m in mlps:
-            m.forward(x, out=out, sel_out=sel, ws=ws)
-            torch.add(x, out, out=y)  # the residual add of the decode loop
+            if args.unfused_residual:
+                m.forward(x, out=out, sel_out=sel, ws=ws)
+                torch.add(x, out, out=y)  # the residual add of the decode loop
+            else:  # the same add fused into the down kernel's output
+                m.forward(x, out=y, sel_out=sel, ws=ws, residual=x)
             x, y = y, x
         return x
 
@@ -431,6 +434,7 @@ def run_stack(args) -> int:
     res = base_result(args, tok_s, us_layer, H, I, R, k, qbs)
     res["steps"] = STACK_TOKENS
     res["config"].update({"layers": STACK_LAYERS, "tokens": STACK_TOKENS, "graph": bool(args.graph),
+                          "residual": "separate add" if args.unfused_residual and not args.graph else "fused",
                           "resident_bytes": int(torch.cuda.memory_allocated(device))})
     res.update({
         "us_per_layer": round(us_layer, 3),
@@ -530,6 +534,8 @@ def main() -> int:
     ap.add_argument("--cpu-runs", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="BYTES")
+    ap.add_argument("--unfused-residual", action="store_true",
+                    help="config 5: the residual add as its own launch instead of in the down kernel")
     ap.add_argument("--graph", action="store_true",
                     help="config 5: replay each token as one captured graph instead of eager launches")
     ap.add_argument("--absmax", choices=("dq8", "f32"), default="dq8",

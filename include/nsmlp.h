@@ -171,6 +171,14 @@ size_t nsmlp_layer_workspace_bytes(int H, int R, int NB, int k);
 int nsmlp_decode_layer_f16(const nsmlp_router* router, const nsmlp_slot_table* table, const void* x, int k,
                            int32_t* sel_out, void* out, void* ws, size_t ws_bytes, void* stream);
 
+/* The same layer call with the decode loop's residual add fused into the
+ * output (version >= 102; RT:7774, hidden = residual + mlp_out):
+ * out[o] = fp16(residual[o] + fp16(mlp(x)[o])), the fp16 add torch does.
+ * residual [H] fp16; out may alias residual or x (in-place hidden update). */
+int nsmlp_decode_layer_add_f16(const nsmlp_router* router, const nsmlp_slot_table* table, const void* x,
+                               const void* residual, int k, int32_t* sel_out, void* out, void* ws, size_t ws_bytes,
+                               void* stream);
+
 /* --------------------------------------- reference-signature entry points
  * Replaces TSM:1378-1509 (triton_sparse_mlp_decode_4bit_single_kernel_sm75):
  * x [H] fp16; gathered gate/up packed [top_k][32][H/2] u8 with absmax

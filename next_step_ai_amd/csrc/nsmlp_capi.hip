@@ -430,8 +430,9 @@ size_t nsmlp_layer_workspace_bytes(int H, int R, int NB, int k) {
   return r + align_up((size_t)k * sizeof(int32_t));
 }
 
-int nsmlp_decode_layer_f16(const nsmlp_router* router, const nsmlp_slot_table* table, const void* x, int k,
-                           int32_t* sel_out, void* out, void* ws, size_t ws_bytes, void* stream) {
+static int decode_layer(const nsmlp_router* router, const nsmlp_slot_table* table, const void* x,
+                        const void* residual, int k, int32_t* sel_out, void* out, void* ws, size_t ws_bytes,
+                        void* stream) {
   if (router == nullptr) return set_error(NSMLP_EINVAL, "router is NULL");
   DecodeArgs a;
   int rc = table_to_args(table, a);
@@ -451,6 +452,7 @@ int nsmlp_decode_layer_f16(const nsmlp_router* router, const nsmlp_slot_table* t
   a.x = (const uint16_t*)x;
   a.k = k;
   a.out = (uint16_t*)out;
+  a.residual = (const uint16_t*)residual;
   rc = fill_decode_ws(a, ws, ws_bytes);
   if (rc) return rc;
   fill_decode_tiling(a);
@@ -477,6 +479,18 @@ int nsmlp_decode_layer_f16(const nsmlp_router* router, const nsmlp_slot_table* t
   if (rc) return rc;
   a.sel = sel;
   return run_decode(a, s);
+}
+
+int nsmlp_decode_layer_f16(const nsmlp_router* router, const nsmlp_slot_table* table, const void* x, int k,
+                           int32_t* sel_out, void* out, void* ws, size_t ws_bytes, void* stream) {
+  return decode_layer(router, table, x, nullptr, k, sel_out, out, ws, ws_bytes, stream);
+}
+
+int nsmlp_decode_layer_add_f16(const nsmlp_router* router, const nsmlp_slot_table* table, const void* x,
+                               const void* residual, int k, int32_t* sel_out, void* out, void* ws, size_t ws_bytes,
+                               void* stream) {
+  if (residual == nullptr) return set_error(NSMLP_EINVAL, "residual must be non-NULL");
+  return decode_layer(router, table, x, residual, k, sel_out, out, ws, ws_bytes, stream);
 }
 
 size_t nsmlp_prefill_workspace_bytes(int H, int NB, int M, int k) {

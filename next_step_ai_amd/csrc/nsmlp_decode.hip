@@ -238,9 +238,7 @@ __device__ __forceinline__ void down_task(const DecodeArgs& a, DecodeSmem& sm, u
   if (live) {
     float y = 0.0f;
     for (int t = 0; t < a.groups; ++t) y += ld_coherent(a.outpart + (long long)t * a.H + o);
-    if (a.out_f32 != nullptr) a.out_f32[o] = y;
-    if (a.down_bias != nullptr) y += h2f(a.down_bias[o]);
-    a.out[o] = f2h(y);
+    a.out[o] = decode_out(a, o, y);
   }
   if (tid == 0) atomicExch(&a.row_count[rc], 0);
 }

@@ -536,6 +536,7 @@ struct DecodeArgs {
   int skip_negative;          // sel[j] < 0 means "no block" (not an error)
   uint16_t* out;         // [H] fp16
   float* out_f32;        // [H] fp32 result before rounding, or nullptr
+  const uint16_t* residual;  // [H] fp16 added to the rounded output, or nullptr
   // workspace
   float* part;           // [k][splits][64]
   uint32_t* act;         // [k][16] fp16 pairs of silu(gate)*up, scaled by 2^act_exp
@@ -570,6 +571,17 @@ struct DecodeArgs {
   int st_gu_a2bytes;     // extent of gate/up absmax2 (bytes)
   int st_dn_a2n;         // down absmax2 entries staged per 64-row chunk
 };
+
+// Output row o of a decode: the MLP sum y (+ bias) rounded once to fp16;
+// with a residual, fp16(residual[o] + that value), the decode loop's fp16 add
+// (hidden = residual + mlp_out).  out_f32 keeps the sum before the bias.
+__device__ __forceinline__ uint16_t decode_out(const DecodeArgs& a, int o, float y) {
+  if (a.out_f32 != nullptr) a.out_f32[o] = y;
+  if (a.down_bias != nullptr) y += h2f(a.down_bias[o]);
+  uint16_t h = f2h(y);
+  if (a.residual != nullptr) h = f2h(h2f(a.residual[o]) + h2f(h));
+  return h;
+}
 
 // Resolve selected position j to (storage view index, validity):
 // slot >= 0 -> HBM slot, slot < 0 -> host copy indexed by block id.  An id or

@@ -545,9 +545,7 @@ __global__ void __launch_bounds__(kThreads8, 2) k_down_rep(DecodeArgs a) {
 #pragma unroll
     for (int w = 0; w < kWaves; ++w) y += wsum[w * kWave + lane];
     if (GX == 1) {
-      if (a.out_f32 != nullptr) a.out_f32[o] = y;
-      if (a.down_bias != nullptr) y += h2f(a.down_bias[o]);
-      a.out[o] = f2h(y);
+      a.out[o] = decode_out(a, o, y);
     } else {
       a.outpart[(long long)gx * a.H + o] = y;
     }
@@ -569,9 +567,7 @@ __global__ void __launch_bounds__(256) k_fin_rep(DecodeArgs a) {
     for (int i = 0; i < 8; ++i) y += v[i];
   }
   for (; g < G; ++g) y += p[(long long)g * a.H];
-  if (a.out_f32 != nullptr) a.out_f32[o] = y;
-  if (a.down_bias != nullptr) y += h2f(a.down_bias[o]);
-  a.out[o] = f2h(y);
+  a.out[o] = decode_out(a, o, y);
 }
 
 // Dense NF4 rows (the LM head: all rows of a row-major [out][in] NF4

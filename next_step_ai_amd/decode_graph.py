@@ -69,7 +69,6 @@ class StackGraph:
             raise RuntimeError("every layer of a stack must have the same hidden size and device")
         self.x = torch.zeros(H, dtype=torch.float16, device=self.device)
         self.bufs = [torch.empty(H, dtype=torch.float16, device=self.device) for _ in range(2)]
-        self.out = torch.empty(H, dtype=torch.float16, device=self.device)
         self.sels = [torch.empty(m.top_k, dtype=torch.int32, device=self.device) for m in layers]
         self.graph = torch.cuda.CUDAGraph()
         side = torch.cuda.Stream(self.device)
@@ -86,9 +85,9 @@ class StackGraph:
     def _token(self):
         x = self.x
         for i, m in enumerate(self.layers):
-            m.forward(x, out=self.out, sel_out=self.sels[i], ws=self.ws)
             y = self.bufs[i % 2]
-            torch.add(x, self.out, out=y)  # the residual add of the decode loop
+            # y = x + mlp(x): the residual add of the decode loop, fused into the down kernel
+            m.forward(x, out=y, sel_out=self.sels[i], ws=self.ws, residual=x)
             x = y
         self._last = x
 

@@ -452,7 +452,10 @@ class SparseMlpLayer:
         return int(_lib.lib().nsmlp_layer_workspace_bytes(self.table.H, self.router.R, self.router.NB, self.top_k))
 
     def forward(self, x: torch.Tensor, out: torch.Tensor | None = None, sel_out: torch.Tensor | None = None,
-                ws: torch.Tensor | None = None):
+                ws: torch.Tensor | None = None, residual: torch.Tensor | None = None):
+        """One decode token: (out [H] fp16, sel [k] int32).  With ``residual``
+        [H] fp16, out = residual + mlp(x) with the decode loop's fp16 add
+        fused into the down kernel (``out`` may be ``residual`` itself)."""
         x16 = x.reshape(-1)
         if x16.dtype != torch.float16 or x16.device != self.device or x16.data_ptr() % 16:
             x16 = x16.to(device=self.device, dtype=torch.float16).contiguous().clone()
@@ -462,8 +465,16 @@ class SparseMlpLayer:
             sel_out = torch.empty(self.top_k, dtype=torch.int32, device=self.device)
         if ws is None:
             ws = workspace(self.workspace_bytes(), self.device)
-        _lib.call("nsmlp_decode_layer_f16", ctypes.byref(self._r), ctypes.byref(self._t), ptr(x16), self.top_k,
-                  ptr(sel_out), ptr(out), ptr(ws), ws.numel(), stream_handle(self.device))
+        if residual is None:
+            _lib.call("nsmlp_decode_layer_f16", ctypes.byref(self._r), ctypes.byref(self._t), ptr(x16), self.top_k,
+                      ptr(sel_out), ptr(out), ptr(ws), ws.numel(), stream_handle(self.device))
+        else:
+            r16 = residual.reshape(-1)
+            if r16.dtype != torch.float16 or r16.device != self.device or not r16.is_contiguous() \
+                    or int(r16.numel()) != self.table.H:
+                raise RuntimeError(f"residual must be a contiguous fp16 [{self.table.H}] tensor on {self.device}")
+            _lib.call("nsmlp_decode_layer_add_f16", ctypes.byref(self._r), ctypes.byref(self._t), ptr(x16), ptr(r16),
+                      self.top_k, ptr(sel_out), ptr(out), ptr(ws), ws.numel(), stream_handle(self.device))
         if self.cache is not None:  # the blocks that missed take slots for the next tokens
             self.cache.promote(sel_out)
         return out, sel_out

@@ -96,3 +96,29 @@ def test_layer_graph_with_hot_cache_promotion(gpu):
             assert torch.equal(a, b), f"token {t}: cache state differs"
         assert eager.cache.state_cpu()[2] == captured.cache.state_cpu()[2]
         assert torch.equal(eager.table.lookup, captured.table.lookup)
+
+
+@pytest.mark.parametrize("H,I,R,k", [
+    (16384, 8192, 16, 64),   # streaming path, the down workgroups write the output
+    (4096, 14336, 64, 64),   # streaming path with the final-sum kernel
+    (256, 2048, 8, 16),      # generic path
+    (2304, 4096, 16, 32),    # generic path (hidden not a multiple of 2048)
+])
+def test_fused_residual_add_equals_separate_add(gpu, H, I, R, k):
+    """out = residual + mlp(x) in the down kernel's epilogue is the fp16 add
+    torch does after the launch, bit for bit, also when out is the residual."""
+    from next_step_ai_amd.synth import make_synthetic_layer, synth_normal_f16
+
+    print(f"fused residual H={H} I={I} k={k}", flush=True)
+    L = make_synthetic_layer(H=H, I=I, R=R, seed=95, device=gpu)
+    layer = L.layer(k)
+    res = synth_normal_f16(96, (H,), 4.0, gpu)
+    mlp, sel = layer.forward(L.x)
+    ref = res + mlp
+    out, sel2 = layer.forward(L.x, residual=res)
+    torch.cuda.synchronize()
+    assert torch.equal(sel2, sel) and torch.equal(out, ref)
+    inplace = res.clone()
+    layer.forward(L.x, out=inplace, residual=inplace)
+    torch.cuda.synchronize()
+    assert torch.equal(inplace, ref)
