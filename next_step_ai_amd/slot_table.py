@@ -447,6 +447,31 @@ class SparseMlpLayer:
         self._r = router.as_struct()
         self._t = table.as_struct()
         self.device = table.device
+        self._lookahead_done: torch.cuda.Event | None = None
+
+    def lookahead(self, hidden: torch.Tensor, stream: torch.cuda.Stream | None = None) -> torch.Tensor:
+        """Prefetch for this layer before its decode (the decode loop's
+        lookahead, RT:7780-7795): route ``hidden`` [H] with this layer's
+        router and promote the selected blocks that are not resident into
+        slots, on ``stream`` (a copy stream; default: the current stream).
+        The next ``forward`` on any stream waits for it.  Returns the
+        lookahead selection [k] int32.  Needs the layer's hot-block cache."""
+        if self.cache is None:
+            raise RuntimeError("lookahead promotes into the hot-block cache: build the layer with cache=")
+        cur = torch.cuda.current_stream(self.device)
+        s = cur if stream is None else stream
+        if s != cur:
+            s.wait_stream(cur)  # hidden is produced on the current stream
+        with torch.cuda.stream(s):
+            sel = self.router.route(hidden.reshape(1, -1), self.top_k).reshape(-1)
+            self.cache.promote(sel)
+            ev = torch.cuda.Event()
+            ev.record(s)
+        if s != cur:
+            hidden.record_stream(s)
+            sel.record_stream(cur)
+        self._lookahead_done = ev
+        return sel
 
     def workspace_bytes(self) -> int:
         return int(_lib.lib().nsmlp_layer_workspace_bytes(self.table.H, self.router.R, self.router.NB, self.top_k))
@@ -465,6 +490,9 @@ class SparseMlpLayer:
             sel_out = torch.empty(self.top_k, dtype=torch.int32, device=self.device)
         if ws is None:
             ws = workspace(self.workspace_bytes(), self.device)
+        if self._lookahead_done is not None:  # the promotion of a lookahead reads and writes the table
+            torch.cuda.current_stream(self.device).wait_event(self._lookahead_done)
+            self._lookahead_done = None
         if residual is None:
             _lib.call("nsmlp_decode_layer_f16", ctypes.byref(self._r), ctypes.byref(self._t), ptr(x16), self.top_k,
                       ptr(sel_out), ptr(out), ptr(ws), ws.numel(), stream_handle(self.device))

@@ -122,3 +122,41 @@ def test_fused_residual_add_equals_separate_add(gpu, H, I, R, k):
     layer.forward(L.x, out=inplace, residual=inplace)
     torch.cuda.synchronize()
     assert torch.equal(inplace, ref)
+
+
+def test_lookahead_promotes_on_a_copy_stream(gpu):
+    """Lookahead route + promotion on a side stream before the decode: the
+    decode gives the output of the fully resident layer, the first token
+    (room for every miss) finds every selected block resident, and the cache
+    state equals the same promotions run on the main stream (the lookahead's,
+    then the decode's own: a plan may evict a hit of the same selection, the
+    reference's rule, which the decode then promotes again)."""
+    from next_step_ai_amd.slot_table import HotBlockCache, SparseMlpLayer
+    from next_step_ai_amd.synth import make_synthetic_layer
+
+    H, I, R, k = 2048, 8192, 16, 48
+    print("lookahead on a copy stream", flush=True)
+    L = make_synthetic_layer(H=H, I=I, R=R, seed=97, device=gpu)
+    full = L.layer(k)
+    rng = np.random.default_rng(97)
+    resident = torch.from_numpy(rng.choice(L.NB, size=40, replace=False))
+    t_a = L.slot_table(resident_blocks=resident, host_copy=True, capacity=40 + k)
+    t_b = L.slot_table(resident_blocks=resident, host_copy=True, capacity=40 + k)
+    ahead = SparseMlpLayer(L.router(), t_a, k, cache=HotBlockCache(t_a))
+    plain = SparseMlpLayer(L.router(), t_b, k, cache=HotBlockCache(t_b))
+    side = torch.cuda.Stream(gpu)
+    for t, x in enumerate(_inputs(gpu, H, 4, 97)):
+        ref_out, ref_sel = full.forward(x)
+        sel_ahead = ahead.lookahead(x, side)
+        out, sel = ahead.forward(x)
+        plain.cache.promote(plain.router.route(x.reshape(1, -1), k).reshape(-1))
+        out_p, _ = plain.forward(x)
+        torch.cuda.synchronize()
+        assert torch.equal(out_p, ref_out)
+        assert torch.equal(sel_ahead, ref_sel) and torch.equal(sel, ref_sel)
+        assert torch.equal(out, ref_out), f"token {t}: output differs"
+        if t == 0:
+            assert bool((t_a.lookup[sel.long()] >= 0).all()), "a selected block is not resident"
+        for a, b in zip(ahead.cache.state_cpu()[:2], plain.cache.state_cpu()[:2]):
+            assert torch.equal(a, b)
+        assert torch.equal(t_a.lookup, t_b.lookup)
