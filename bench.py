@@ -31,7 +31,8 @@ the selected blocks' misses (62 of 208) read from pinned host copies over
 the host link; --config 5 decodes 64 tokens through a stack of 126 resident
 layers (x <- x + mlp(x)) and reports the end-to-end decode_tok_s; --config 6
 times the NF4 LM head (vocabulary 128256 x hidden 16384) for one token;
---graph replays each config-5 token as one captured HIP graph.
+--graph replays each config-5 token as one captured HIP graph; --config 7 times the
+dense-guard prefill MLP (256 tokens through every block) on MFMA.
 Each prints the same JSON line shape with its own config.
 
 --copy-calibration BYTES runs only a plain device copy of BYTES (the
@@ -55,7 +56,8 @@ PEAK_GBS = 8000.0
 MODEL_LAYERS = 126
 # config id -> (hidden, intermediate, basis rank, top-k)
 CONFIGS = {1: (4096, 14336, 64, 64), 2: (16384, 53248, 64, 208), 3: (16384, 53248, 64, 208),
-           4: (16384, 53248, 64, 208), 5: (16384, 53248, 64, 208), 6: (16384, 53248, 64, 208)}
+           4: (16384, 53248, 64, 208), 5: (16384, 53248, 64, 208), 6: (16384, 53248, 64, 208),
+           7: (16384, 53248, 64, 1664)}
 LM_VOCAB = 128256
 PREFILL_TOKENS = 256
 PEAK_F16_TFLOPS = 2500.0  # dense fp16 MFMA
@@ -70,6 +72,8 @@ WORKLOADS = {
        "64 decode tokens at batch 1, x <- x + mlp(x) per layer",
     6: "405B NF4 LM head decode: logits over vocabulary 128256 from hidden 16384 (dense NF4 GEMV, "
        "every input block active), one token",
+    7: "405B-shaped dense-guard prefill MLP: 256 tokens through every block (hidden 16384, intermediate 53248), "
+       "fp16 MFMA GEMMs over NF4 weights decoded as staged",
 }
 STACK_LAYERS = 126
 STACK_TOKENS = 64
@@ -371,6 +375,55 @@ def run_prefill(args) -> int:
     return 0
 
 
+def run_dense_guard(args) -> int:
+    """Config 7: the dense-guard prefill MLP (every block for every token)."""
+    import torch
+
+    from next_step_ai_amd.synth import make_synthetic_layer, sub_seed, synth_normal_f16
+
+    device = torch.device("cuda", 0)
+    torch.cuda.set_device(device)
+    H, I, R, _ = CONFIGS[7]
+    qbs, M = 64, PREFILL_TOKENS
+    n_layers = min(args.layers, 2)
+    layers = []
+    for l in range(n_layers):
+        L = make_synthetic_layer(H=H, I=I, R=R, seed=7000 + l, device=device, double_quant=args.absmax == "dq8",
+                                 keep_f32_absmax=args.absmax == "f32")
+        L.table = L.slot_table(drop_reference_down=True)
+        L.xs = synth_normal_f16(sub_seed(7000 + l, "x"), (M, H), 1.0, device)
+        layers.append(L)
+    outs = [torch.empty((M, H), dtype=torch.float16, device=device) for _ in layers]
+    n = len(layers)
+    steps = max(1, args.steps // 20)
+    for i in range(max(1, args.warmup // 10)):
+        layers[i % n].table.dense_mlp(layers[i % n].xs, out=outs[i % n])
+    torch.cuda.synchronize()
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
+    t0 = time.perf_counter()
+    for i in range(steps):
+        L = layers[i % n]
+        ev[i][0].record()
+        L.table.dense_mlp(L.xs, out=outs[i % n])
+        ev[i][1].record()
+    torch.cuda.synchronize()
+    step_us = (time.perf_counter() - t0) / steps * 1e6
+    us = statistics.mean(a.elapsed_time(b) for a, b in ev) * 1e3
+    flop = 2.0 * 3 * M * I * H
+    res = base_result(args, M / (step_us * 1e-6), step_us, H, I, R, I // 32, qbs)
+    res["metric"] = "dense-guard prefill MLP tok/s per layer + MFMA TFLOP/s vs peak, 405B shape, 256 tokens"
+    res["steps"] = steps
+    res["config"].update({"tokens": M, "rotating_layers": n})
+    res.update({
+        "dense_mlp_us": round(us, 3),
+        "roofline": {"bound": "mfma", "achieved": round(flop / (us * 1e-6) / 1e12, 2), "peak": PEAK_F16_TFLOPS,
+                     "unit": "TFLOP/s", "frac": round(flop / (us * 1e-6) / 1e12 / PEAK_F16_TFLOPS, 4),
+                     "traffic": None, "flop": flop, "kernels": "k_dg_gu + k_dg_down + k_dg_fin"},
+    })
+    print(json.dumps(res), flush=True)
+    return 0
+
+
 def run_stack(args) -> int:
     """Config 5: 126 resident layers, 64 decode tokens through all of them."""
     import torch
@@ -555,6 +608,8 @@ def main() -> int:
         return run_stack(args)
     if args.config == 6:
         return run_lm_head(args)
+    if args.config == 7:
+        return run_dense_guard(args)
 
     import torch
 

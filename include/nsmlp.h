@@ -203,6 +203,18 @@ size_t nsmlp_prefill_workspace_bytes(int H, int NB, int M, int k);
 int nsmlp_prefill_slots_f16(const nsmlp_slot_table* table, const void* x, int M, const int32_t* sel, int k, void* out,
                             void* ws, size_t ws_bytes, void* stream);
 
+/* Dense-guard prefill MLP (version >= 102): replaces RT:5775-5831
+ * (_dense_guard_mlp_forward_exact_chunked_4bit), every intermediate block for
+ * every token, with the reference's rounding points: weights fp16(code *
+ * absmax), g = fp16(x Wg^T), act = fp16(fp16(silu(g)) * fp16(x Wu^T)),
+ * out = fp16(act Wd^T + down_bias) (+ residual: fp16(residual + out)).
+ * x [M][H] fp16 (16-byte aligned), residual [M][H] fp16 or NULL, out [M][H]
+ * fp16.  H % 256 == 0, I % 128 == 0; blocks read from their HBM slots or
+ * host copies.  Deterministic. */
+size_t nsmlp_dense_mlp_workspace_bytes(int H, int I, int M);
+int nsmlp_dense_mlp_slots_f16(const nsmlp_slot_table* table, const void* x, int M, const void* residual, void* out,
+                              void* ws, size_t ws_bytes, void* stream);
+
 /* ------------------------------------------------ hot-block cache (device)
  * Promotion of missed blocks into the table's fixed-capacity slots, as
  * stream-ordered kernels with no host round trip.  Replaces the host-side

@@ -93,6 +93,8 @@ SIGNATURES: dict[str, tuple] = {
                                          P]),
     "nsmlp_prefill_workspace_bytes": (SZ, [I32, I32, I32, I32]),
     "nsmlp_prefill_slots_f16": (I32, [ctypes.POINTER(SlotTable), P, I32, P, I32, P, P, SZ, P]),
+    "nsmlp_dense_mlp_workspace_bytes": (SZ, [I32, I32, I32]),
+    "nsmlp_dense_mlp_slots_f16": (I32, [ctypes.POINTER(SlotTable), P, I32, P, P, P, SZ, P]),
     "nsmlp_single_kernel_workspace_bytes": (SZ, [I32, I32]),
     "nsmlp_single_kernel_decode_f16": (I32, [P, P, P, P, P, P, P, P, P, P, P, P, I32, I32, I32, I32, P, SZ, P]),
     "nsmlp_fused_decode_workspace_bytes": (SZ, [I32, I32]),

@@ -17,7 +17,7 @@ CSRC = os.path.join(HERE, "csrc")
 BUILD = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libnsmlp.so")
 SOURCES = ["nsmlp_capi.hip", "nsmlp_router.hip", "nsmlp_decode.hip", "nsmlp_stream.hip", "nsmlp_ops.hip",
-           "nsmlp_prefill.hip", "nsmlp_cache.hip"]
+           "nsmlp_prefill.hip", "nsmlp_cache.hip", "nsmlp_dense_guard.hip"]
 
 ARCH = "gfx950"
 HIPCC_FLAGS = [

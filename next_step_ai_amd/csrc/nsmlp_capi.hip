@@ -548,6 +548,56 @@ int nsmlp_prefill_slots_f16(const nsmlp_slot_table* table, const void* x, int M,
   return check_launch("prefill");
 }
 
+static int dense_guard_splits(int H, int NB, int M) {
+  // block ranges of the down GEMM: enough workgroups for the CUs
+  const int tiles = H / 256 * ((M + 255) / 256);
+  int S = 1;
+  while (S < 8 && tiles * S < 256 && S * 2 <= NB / 2) S *= 2;
+  return S;
+}
+
+size_t nsmlp_dense_mlp_workspace_bytes(int H, int I, int M) {
+  if (H <= 0 || I <= 0 || M <= 0) return 0;
+  const size_t S = (size_t)dense_guard_splits(H, I / 32, M);
+  return align_up(kCounterBytes) + align_up((size_t)M * I * 2) + align_up(S * M * H * 4);
+}
+
+int nsmlp_dense_mlp_slots_f16(const nsmlp_slot_table* table, const void* x, int M, const void* residual, void* out,
+                              void* ws, size_t ws_bytes, void* stream) {
+  DenseGuardArgs g;
+  memset(&g, 0, sizeof(g));
+  int rc = table_to_args(table, g.d);
+  if (rc) return rc;
+  const int H = g.d.H, I = g.d.NB * 32;
+  if (H % 256 != 0 || I % 128 != 0)
+    return set_error(NSMLP_EINVAL, "dense MLP needs hidden %% 256 == 0 and intermediate %% 128 == 0 (got %d, %d)", H, I);
+  if (g.d.qbs < 32 || (g.d.qbs & (g.d.qbs - 1)) != 0 || H % g.d.qbs != 0)
+    return set_error(NSMLP_EINVAL, "quant block size %d must be a power of two >= 32 dividing %d", g.d.qbs, H);
+  if (M <= 0) return set_error(NSMLP_EINVAL, "M=%d must be positive", M);
+  if ((long long)M * I * 2 >= (1LL << 31) || (long long)M * H * 2 >= (1LL << 31))
+    return set_error(NSMLP_EINVAL, "M=%d too large for one dense MLP call at H=%d, I=%d (split the tokens)", M, H, I);
+  if (!x || !out) return set_error(NSMLP_EINVAL, "x and out must be non-NULL");
+  if (!aligned16(x)) return set_error(NSMLP_EINVAL, "x must be 16-byte aligned");
+  const size_t need = nsmlp_dense_mlp_workspace_bytes(H, I, M);
+  if (ws == nullptr || ws_bytes < need)
+    return set_error(NSMLP_ENOSPC, "dense MLP workspace needs %zu bytes, got %zu", need, ws_bytes);
+  if (((uintptr_t)ws & (kAlign - 1)) != 0) return set_error(NSMLP_EINVAL, "workspace must be 256-byte aligned");
+  char* base = (char*)ws;
+  g.d.status = (int*)(base + kStatusOff);
+  g.d.qbs_shift = __builtin_ctz((unsigned)g.d.qbs);
+  g.x = (const uint16_t*)x;
+  g.M = M;
+  g.S = dense_guard_splits(H, g.d.NB, M);
+  size_t off = align_up(kCounterBytes);
+  g.act = (uint16_t*)(base + off);
+  off += align_up((size_t)M * I * 2);
+  g.part = (float*)(base + off);
+  g.out = (uint16_t*)out;
+  g.residual = (const uint16_t*)residual;
+  launch_dense_guard(g, (hipStream_t)stream);
+  return check_launch("dense MLP");
+}
+
 size_t nsmlp_single_kernel_workspace_bytes(int H, int top_k) { return decode_ws_layout(H, top_k).total; }
 
 int nsmlp_single_kernel_decode_f16(const void* x, const uint8_t* gate_packed, const float* gate_absmax,

@@ -329,6 +329,29 @@ __device__ __forceinline__ void st_coherent_i32(int* p, int v) {
 
 __device__ __forceinline__ float silu_mul(float g, float u) { return g / (1.0f + __expf(-g)) * u; }
 
+// ------------------------------------------------------------------ MFMA --
+// v_mfma_f32_16x16x32_f16 lane layout (measured): A[i][k] and B[k][j] in lane
+// l hold i (or j) = l % 16, k = 8 (l / 16) + 0..7; C[i][j] in lane l holds
+// j = l % 16, i = 4 (l / 16) + r, r = 0..3.
+typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
+typedef float float4_t __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ half8_t as_h8(uint4 v) { return __builtin_bit_cast(half8_t, v); }
+
+__device__ __forceinline__ float4_t mfma16(half8_t a, half8_t b, float4_t c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+
+// Wait states between MFMAs and VALU reads of their results, beyond what the
+// compiler inserts: reads of a 16x16x32 result that follow its MFMA closely
+// have returned values that changed from run to run in the last elements
+// (written last), so MFMA results are read only after this drain.
+__device__ __forceinline__ void mfma_drain() {
+  __builtin_amdgcn_sched_barrier(0);
+  asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory");
+  __builtin_amdgcn_sched_barrier(0);
+}
+
 // ---------------------------------------------------------- buffer loads --
 // Weight streams use raw buffer loads through per-block descriptors: a
 // descriptor whose extent is zero (or an offset past the extent) makes the
@@ -630,6 +653,20 @@ struct PrefillArgs {
   uint16_t* act;          // [M k][32] fp16 silu(gate) * up per (block, token) entry
 };
 void launch_prefill(const PrefillArgs& p, hipStream_t s);
+
+// Dense-guard prefill MLP: every block for every token (M tokens) over a slot
+// table, as staged GEMMs on MFMA.  H % 256 == 0, NB % 4 == 0.
+struct DenseGuardArgs {
+  DecodeArgs d;              // slot table views, H, NB, qbs, code books, dq state, status, down_bias
+  const uint16_t* x;         // [M][H] fp16
+  int M;
+  uint16_t* act;             // [M][NB*32] fp16 (workspace)
+  float* part;               // [S][M][H] fp32 partial sums over S block ranges (workspace)
+  int S;
+  uint16_t* out;             // [M][H] fp16
+  const uint16_t* residual;  // [M][H] fp16 added to the rounded output, or nullptr
+};
+void launch_dense_guard(const DenseGuardArgs& g, hipStream_t s);
 
 // Dense NF4 rows (the LM head): y[t][o] = sum_i W[o][i] x[t][i] over a
 // row-major [out][in] NF4 matrix, in % 32 == 0, in <= 16384.

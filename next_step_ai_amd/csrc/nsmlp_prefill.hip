@@ -31,9 +31,6 @@ namespace nsmlp {
 
 namespace {
 
-typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
-typedef float float4_t __attribute__((ext_vector_type(4)));
-
 constexpr int kPfThreads = 512;
 constexpr int kPfWaves = kPfThreads / kWave;
 constexpr int kChunk = 128;      // gate/up columns per wave step
@@ -76,7 +73,6 @@ __device__ __forceinline__ half8_t codes8(uint32_t word, const uint32_t* cpair) 
   return __builtin_bit_cast(half8_t, v);
 }
 
-__device__ __forceinline__ half8_t as_h8(uint4 v) { return __builtin_bit_cast(half8_t, v); }
 
 // v * 2^31 truncated toward zero (|v| < 2^23), in fp32/int32 steps: hi =
 // trunc(v * 2^8) carries the bits above 2^-8, the remainder v - hi * 2^-8 is
@@ -88,19 +84,6 @@ __device__ __forceinline__ long long to_fix31(float v) {
   return ((long long)hi << 23) + (long long)lo;
 }
 
-__device__ __forceinline__ float4_t mfma16(half8_t a, half8_t b, float4_t c) {
-  return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
-}
-
-// Wait states between MFMAs and VALU reads of their results, beyond what the
-// compiler inserts: reads of a 16x16x32 result that follow its MFMA closely
-// have returned values that changed from run to run in the last elements
-// (written last), so MFMA results are read only after this drain.
-__device__ __forceinline__ void mfma_drain() {
-  __builtin_amdgcn_sched_barrier(0);
-  asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory");
-  __builtin_amdgcn_sched_barrier(0);
-}
 
 }  // namespace
 

@@ -292,6 +292,28 @@ class SparseMlpSlotTable:
         return out
 
 
+    def dense_mlp(self, x: torch.Tensor, out: torch.Tensor | None = None,
+                  residual: torch.Tensor | None = None) -> torch.Tensor:
+        """The dense-guard prefill MLP (RT:5775-5831): every block for every
+        token of ``x`` [M, H], as full-width MFMA GEMMs with the reference's
+        rounding points (fp16 weights, g, silu(g), u, act); ``out`` [M, H]
+        fp16, plus ``residual`` [M, H] when given (fused fp16 add)."""
+        x16 = x.reshape(-1, self.H).to(device=self.device, dtype=torch.float16).contiguous()
+        M = int(x16.shape[0])
+        if out is None:
+            out = torch.empty((M, self.H), dtype=torch.float16, device=self.device)
+        r16 = None
+        if residual is not None:
+            r16 = residual.reshape(M, self.H)
+            if r16.dtype != torch.float16 or r16.device != self.device or not r16.is_contiguous():
+                raise RuntimeError("residual must be a contiguous fp16 [M, H] tensor on the table's device")
+        nbytes = int(_lib.lib().nsmlp_dense_mlp_workspace_bytes(self.H, self.I, M))
+        ws = workspace(nbytes, self.device)
+        st = self._struct if self._struct is not None else self.as_struct()
+        _lib.call("nsmlp_dense_mlp_slots_f16", ctypes.byref(st), ptr(x16), M, ptr(r16), ptr(out), ptr(ws), ws.numel(),
+                  stream_handle(self.device))
+        return out
+
     def prefill(self, x: torch.Tensor, sel: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
         """M tokens ``x`` [M, H] with their own selected block ids ``sel``
         [M, k] (the multi-token branch, RT:4857-4908 + RT:5453): grouped MFMA
