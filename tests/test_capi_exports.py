@@ -76,3 +76,45 @@ def test_no_cpu_fallback_without_gpu():
             torch.zeros(1, 64, dtype=torch.float16), torch.zeros(1, 1, dtype=torch.int32),
             packed_weight=torch.zeros(64 * 16, dtype=torch.uint8), absmax=torch.ones(64),
             code=torch.zeros(16), out_features=32, in_features=64, quant_block_size=32, bias=None, block_size=32)
+
+
+def test_host_validation_of_lm_head_dense_and_residual_entry_points(lib):
+    """Argument checks of the LM-head, dense-guard and residual entry points
+    run on the host before any device work (no GPU needed)."""
+    import ctypes
+
+    from next_step_ai_amd import _lib
+
+    L = _lib.lib()
+    assert L.nsmlp_version() >= 102
+    assert L.nsmlp_dense_linear_nf4_f16(None, None, 1, None, None, None) == -22
+    assert b"NULL matrix" in L.nsmlp_last_error()
+    m = _lib.Nf4Matrix(out_features=10, in_features=20000, qbs=64)
+    assert L.nsmlp_dense_linear_nf4_f16(ctypes.byref(m), None, 1, None, None, None) == -22
+    assert b"in_features" in L.nsmlp_last_error()
+    m = _lib.Nf4Matrix(out_features=10, in_features=4096, qbs=48)
+    assert L.nsmlp_dense_linear_nf4_f16(ctypes.byref(m), None, 1, None, None, None) == -22
+    assert b"quant block size" in L.nsmlp_last_error()
+    m = _lib.Nf4Matrix(out_features=10, in_features=4096, qbs=64, dq_block=100)
+    assert L.nsmlp_dense_linear_nf4_f16(ctypes.byref(m), None, 1, None, None, None) == -22
+    assert b"dq_block" in L.nsmlp_last_error()
+    m = _lib.Nf4Matrix(out_features=300000, in_features=16384, qbs=64)
+    assert L.nsmlp_dense_linear_nf4_f16(ctypes.byref(m), None, 1, None, None, None) == -22
+    assert b"2 GiB" in L.nsmlp_last_error()
+    m = _lib.Nf4Matrix(out_features=10, in_features=4096, qbs=64)
+    assert L.nsmlp_dense_linear_nf4_f16(ctypes.byref(m), None, 0, None, None, None) == 0  # no rows: nothing to do
+    assert L.nsmlp_dense_linear_nf4_f16(ctypes.byref(m), None, 1, None, None, None) == -22
+    assert b"NULL tensor" in L.nsmlp_last_error()
+    # dense-guard MLP: shape rules and workspace sizing
+    t = _lib.SlotTable(H=1000, I=4096, qbs=64, n_slots=128)
+    assert L.nsmlp_dense_mlp_slots_f16(ctypes.byref(t), None, 4, None, None, None, 0, None) == -22
+    t = _lib.SlotTable(H=2048, I=4096, qbs=64, n_slots=128)
+    assert L.nsmlp_dense_mlp_workspace_bytes(2048, 4096, 256) > 256 * 4096 * 2 + 256 * 2048 * 4
+    # the residual layer call needs a residual
+    r = _lib.Router(R=16, basis_top_k=16, NB=128)
+    assert L.nsmlp_decode_layer_add_f16(ctypes.byref(r), ctypes.byref(t), None, None, 16, None, None, None, 0,
+                                        None) == -22
+    assert b"residual" in L.nsmlp_last_error()
+    # the input linear takes block sizes that are multiples of 32
+    assert L.nsmlp_input_linear_nf4_f16(None, 1, 4096, None, 1, None, None, None, 64, 10, None, 48, None, None) == -22
+    assert b"block_size" in L.nsmlp_last_error()

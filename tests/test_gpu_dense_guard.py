@@ -120,3 +120,21 @@ def test_dense_mlp_formats_residency_and_residual(gpu):
     assert torch.equal(y_dq, y_f32), "double-quantised absmax differs from the resolved fp32 path"
     assert torch.equal(y_host, y_f32), "host-resident blocks differ from HBM slots"
     assert torch.equal(y_res, res + y_f32) and torch.equal(inplace, res + y_f32)
+
+
+def test_dense_mlp_smallest_shape(gpu, orc):
+    """One gate/up workgroup (4 blocks), one down row tile split in two block
+    ranges, three tokens."""
+    from next_step_ai_amd.synth import make_synthetic_layer, synth_normal_f16
+
+    H, I, R, M = 256, 128, 8, 3
+    print(f"dense guard smallest H={H} I={I} M={M}", flush=True)
+    L = make_synthetic_layer(H=H, I=I, R=R, seed=139, device=gpu)
+    x = synth_normal_f16(140, (M, H), 1.0, gpu)
+    y = L.slot_table().dense_mlp(x)
+    code = torch.tensor(orc.nf4_code(), device=gpu)
+    ref = _torch_dense_guard(L, x, code)
+    torch.cuda.synchronize()
+    e = float(torch.linalg.norm(y.double() - ref) / torch.linalg.norm(ref))
+    print(f"  relL2={e:.3e}", flush=True)
+    assert e <= 1e-3

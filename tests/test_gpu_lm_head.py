@@ -156,3 +156,18 @@ def test_lm_head_405b_vocab_sampled_rows(gpu, orc):
     sub_f32 = f32.index_select(1, rows).contiguous()
     _check_random(orc, xs, pk_rows, am_rows, 256, H, qbs, sub_out.contiguous(), sub_f32)
     del packed, absmax
+
+
+@pytest.mark.parametrize("V,H,qbs,rows", [(1, 32, 32, 1), (3, 64, 32, 5), (6, 2080, 32, 2)])
+def test_dense_linear_tiny_and_ragged_shapes(gpu, orc, V, H, qbs, rows):
+    """Fewer rows than one 4-row item, one active lane, a split with a single
+    32-column lane group past 2048 columns, five token rows (2 + 2 + 1)."""
+    print(f"lm head tiny V={V} H={H} rows={rows}", flush=True)
+    rng = np.random.default_rng(V * 7 + H)
+    packed, absmax, x, ref = _known_case(rng, V, H, qbs, rows)
+    x = np.clip(x, -2, 2).astype(np.float16)
+    ref = orc.dense_linear_nf4(x.view(np.uint16), packed, absmax, V, H, qbs)
+    code = torch.tensor(orc.nf4_code(), device=gpu)
+    out, f32 = _run(gpu, x, torch.from_numpy(packed).to(gpu), torch.from_numpy(absmax).to(gpu), code, V, H, qbs)
+    assert np.array_equal(_np(f32).astype(np.float64), ref)
+    assert np.array_equal(_np(out).view(np.uint16), orc.f32_to_f16_bits(ref.astype(np.float32)))
