@@ -156,6 +156,19 @@ __device__ __forceinline__ void dg_pipeline(int c_lo, int c_hi, LoadX load_x, Lo
   }
 }
 
+// Weight staging of the gate/up kernel in pairs of chunks: a row's 128
+// columns of a pair are 64 contiguous bytes of packed NF4, read by 4
+// consecutive lanes (a load that reads 32 bytes of each row per chunk runs at
+// a lower rate).  Load j of lane l takes staged row 16 w + 128 j + l / 4 and
+// 16-byte segment (l % 4) ^ 2 j of that row's 64 bytes, i.e. chunk
+// ((l % 4) / 2) ^ j of the pair, columns 32 (l % 2) .. + 31: every lane
+// decodes one piece per chunk.
+struct DgPair {
+  uint4 w[2];
+  float am[2];     // fp32 absmax, or the absmax2 (double-quantised)
+  uint32_t qa[2];  // u8 absmax codes (double-quantised)
+};
+
 template <bool DQ>
 __global__ void __launch_bounds__(kDgThreads, 2) k_dg_gu(DenseGuardArgs g) {
   extern __shared__ __attribute__((aligned(16))) uint8_t dg_lds[];
@@ -171,54 +184,66 @@ __global__ void __launch_bounds__(kDgThreads, 2) k_dg_gu(DenseGuardArgs g) {
   dg_pairs(cp, d.code, tid, 2);
   dg_pairs(cp + 512, d.code_up, tid, 2);
   if constexpr (DQ) c2s[tid] = (tid < 256 ? d.gate.code2 : d.up.code2)[tid & 255];
-  // wave w stages the 32 rows of block 4 nt + w % 4 of the gate (w < 4) or
-  // up projection (staged rows r = 32 w + lane % 32; gate 0-127, up 128-255),
-  // columns 32 (lane / 32) .. + 31 of each chunk, so the block and its buffer
-  // descriptors are uniform over the wave and 16 consecutive lanes write 16
-  // consecutive staged rows (no bank conflicts)
-  const uint32_t wrow = (uint32_t)(lane & 31);
-  const int half = lane >> 5, r = 32 * wave + (int)wrow;
-  const bool wup = wave >= 4;
-  const int blk = 4 * nt + (wave & 3);
+  // load j of this wave: staged rows 16 wave + 128 j .. + 15, all in block
+  // 4 nt + wave / 2 of the gate (j = 0) or up (j = 1) projection, so each
+  // load's block and buffer descriptors are uniform over the wave
+  const uint32_t rs = (uint32_t)d.gate.row_stride, A = (uint32_t)d.gate.abs_row_stride;
+  const uint32_t wrow = (uint32_t)((16 * wave + (lane >> 2)) & 31);  // row inside the block
+  const int u = (lane & 3) >> 1, half = lane & 1;
+  const int blk = 4 * nt + (wave >> 1);
   const BlockRef br = resolve_id(d, blk);
   if (!br.ok && lane == 0) atomicOr(d.status, 1);
-  const ProjView& pv = wup ? d.up : d.gate;
-  const ProjView& hv = wup ? d.host_up : d.host_gate;
-  const uint32_t rs = (uint32_t)d.gate.row_stride, A = (uint32_t)d.gate.abs_row_stride;
-  const rsrc_t rw = make_rsrc((br.dev ? pv.packed : hv.packed) + br.q * pv.blk_stride, br.ok ? (int)(32 * rs) : 0);
-  rsrc_t ra = rw, r2 = rw;
-  if constexpr (DQ) {
-    ra = make_rsrc((br.dev ? pv.qabsmax : hv.qabsmax) + br.q * pv.abs_blk_stride, br.ok ? (int)(32 * A) : 0);
-    r2 = make_rsrc(pv.absmax2, br.ok ? (int)((((long long)I * A + (1 << d.dq_shift) - 1) >> d.dq_shift) * 4) : 0);
-  } else {
-    ra = make_rsrc((br.dev ? pv.absmax : hv.absmax) + br.q * pv.abs_blk_stride, br.ok ? (int)(32 * A * 4) : 0);
+  rsrc_t rw[2], ra[2], r2[2];
+#pragma unroll
+  for (int jj = 0; jj < 2; ++jj) {
+    const ProjView& pv = jj ? d.up : d.gate;
+    const ProjView& hv = jj ? d.host_up : d.host_gate;
+    rw[jj] = make_rsrc((br.dev ? pv.packed : hv.packed) + br.q * pv.blk_stride, br.ok ? (int)(32 * rs) : 0);
+    if constexpr (DQ) {
+      ra[jj] = make_rsrc((br.dev ? pv.qabsmax : hv.qabsmax) + br.q * pv.abs_blk_stride, br.ok ? (int)(32 * A) : 0);
+      r2[jj] = make_rsrc(pv.absmax2,
+                         br.ok ? (int)((((long long)I * A + (1 << d.dq_shift) - 1) >> d.dq_shift) * 4) : 0);
+    } else {
+      ra[jj] = make_rsrc((br.dev ? pv.absmax : hv.absmax) + br.q * pv.abs_blk_stride, br.ok ? (int)(32 * A * 4) : 0);
+      r2[jj] = ra[jj];
+    }
   }
   const rsrc_t rx = make_rsrc(g.x, (int)((long long)M * H * 2));
-  const int nch = H / kDgK;
+  const int nch = H / kDgK, np = (nch + 1) / 2;
   auto load_x = [&](uint4 (&X)[4], int c) {
     const bool live = c < nch;
     dg_load_rows(X, rx, tid, t0, M, (uint32_t)H, (uint32_t)(live ? c : 0) * kDgK, live);
   };
-  auto load_w = [&](DgW& W, int c) {
-    const bool live = c < nch;
-    const uint32_t col = (uint32_t)(live ? c : 0) * kDgK + 32u * (uint32_t)half;
-    const uint32_t ce = col >> d.qbs_shift;
-    W.w = buf_ld16(rw, live ? wrow * rs + (col >> 1) : kOffNone, 0);
-    if constexpr (DQ) {
-      W.qa = buf_ldu8(ra, live ? ((wrow >> 1) * A + ce) * 2u + (wrow & 1u) : kOffNone, 0);
-      const uint32_t f = (32u * (uint32_t)blk + wrow) * A + ce;
-      W.am = buf_ldfc(r2, live ? (f >> d.dq_shift) * 4u : kOffNone, 0);
-    } else {
-      W.qa = 0;
-      W.am = buf_ldf(ra, live ? (wrow * A + ce) * 4u : kOffNone, 0);
+  auto load_p = [&](DgPair& P, int pr) {
+    const bool live = pr < np;
+#pragma unroll
+    for (int jj = 0; jj < 2; ++jj) {
+      const uint32_t seg = (uint32_t)((lane & 3) ^ (2 * jj));  // chunk seg / 2, half seg % 2
+      const uint32_t col = (uint32_t)pr * 128u + seg * 32u;
+      const bool ok = live && (int)col < H;
+      const uint32_t ce = col >> d.qbs_shift;
+      P.w[jj] = buf_ld16(rw[jj], ok ? wrow * rs + (col >> 1) : kOffNone, 0);
+      if constexpr (DQ) {
+        P.qa[jj] = buf_ldu8(ra[jj], ok ? ((wrow >> 1) * A + ce) * 2u + (wrow & 1u) : kOffNone, 0);
+        const uint32_t f = (32u * (uint32_t)blk + wrow) * A + ce;
+        P.am[jj] = buf_ldfc(r2[jj], ok ? (f >> d.dq_shift) * 4u : kOffNone, 0);
+      } else {
+        P.qa[jj] = 0;
+        P.am[jj] = buf_ldf(ra[jj], ok ? (wrow * A + ce) * 4u : kOffNone, 0);
+      }
     }
   };
-  auto store_x = [&](int bi, const uint4 (&X)[4]) { dg_store_rows(As + bi * kDgStage, X, tid); };
-  auto store_w = [&](int bi, const DgW& W) {
-    float am = W.am;
-    if constexpr (DQ) am = dq_absmax(c2s[(wup ? 256 : 0) + W.qa], W.am, wup ? d.up.offset : d.gate.offset);
-    dg_decode32<2>(Bs + bi * kDgStage + r * kDgRow + 32 * half, W.w, am, cp + (wup ? 512 : 0) + (lane & 1));
+  // chunk k of a pair into buffer bi: this lane's piece jj = k ^ u (gate for
+  // jj = 0, up for jj = 1)
+  auto decode = [&](int bi, const DgPair& P, int k) {
+    const bool up = (k ^ u) != 0;
+    const uint4 w = up ? P.w[1] : P.w[0];
+    float am = up ? P.am[1] : P.am[0];
+    if constexpr (DQ) am = dq_absmax(c2s[(up ? 256 : 0) + (up ? P.qa[1] : P.qa[0])], am, up ? d.up.offset : d.gate.offset);
+    const int row = 16 * wave + (up ? 128 : 0) + (lane >> 2);
+    dg_decode32<2>(Bs + bi * kDgStage + row * kDgRow + 32 * half, w, am, cp + (up ? 512 : 0) + (lane & 1));
   };
+  auto store_x = [&](int bi, const uint4 (&X)[4]) { dg_store_rows(As + bi * kDgStage, X, tid); };
   const int mq = wave & 3, nh = wave >> 2;
   auto brow = [nh](int ni) { return (ni < 4 ? 0 : 128) + 64 * nh + 16 * (ni & 3); };
   float4_t acc[4][8];
@@ -226,8 +251,35 @@ __global__ void __launch_bounds__(kDgThreads, 2) k_dg_gu(DenseGuardArgs g) {
   for (int mi = 0; mi < 4; ++mi)
 #pragma unroll
     for (int ni = 0; ni < 8; ++ni) acc[mi][ni] = float4_t{0.0f, 0.0f, 0.0f, 0.0f};
-  auto mma = [&](int bi) { dg_mma(acc, As + bi * kDgStage, Bs + bi * kDgStage, mq, lane, brow); };
-  dg_pipeline(0, nch, load_x, load_w, store_x, store_w, mma);
+  uint4 X[2][4];
+  DgPair P[2];
+  load_p(P[0], 0);
+  load_p(P[1], 1);
+  load_x(X[0], 0);
+  load_x(X[1], 1);
+  __syncthreads();  // code tables
+  store_x(0, X[0]);
+  decode(0, P[0], 0);
+  load_x(X[0], 2);
+  __syncthreads();
+  // chunk c computes from buffer c & 1 while chunk c + 1 is staged into the
+  // other buffer (token rows from registers, weights decoded from the pair
+  // registers) and chunk c + 3's token rows are loaded; a pair's registers
+  // are reloaded with the pair after next once its second chunk is decoded.
+  // Unrolled by 4 chunks so every register index is static.
+  for (int c = 0; c < nch; c += 4) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int cc = c + i;
+      if (cc < nch) dg_mma(acc, As + (i & 1) * kDgStage, Bs + (i & 1) * kDgStage, mq, lane, brow);  // uniform
+      const int nb = (i + 1) & 1;
+      store_x(nb, X[nb]);
+      decode(nb, P[((i + 1) >> 1) & 1], (i + 1) & 1);
+      load_x(X[nb], cc + 3);
+      if (((i + 1) & 1) == 1) load_p(P[((i + 1) >> 1) & 1], ((cc + 1) >> 1) + 2);
+      __syncthreads();
+    }
+  }
   mfma_drain();
   // act = fp16(fp16(silu(fp16(g))) * fp16(u)) for (token, row)
   const int j = lane & 15, gq = lane >> 4;
