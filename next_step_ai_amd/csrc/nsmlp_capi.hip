@@ -493,6 +493,22 @@ int nsmlp_decode_layer_add_f16(const nsmlp_router* router, const nsmlp_slot_tabl
   return decode_layer(router, table, x, residual, k, sel_out, out, ws, ws_bytes, stream);
 }
 
+static int dense_guard_splits(int H, int NB, int M) {
+  // block ranges of the down GEMM: enough workgroups for the CUs
+  const int tiles = H / 256 * ((M + 255) / 256);
+  int S = 1;
+  while (S < 8 && tiles * S < 256 && S * 2 <= NB / 2) S *= 2;
+  return S;
+}
+
+// The prefill's down runs as the dense GEMM over a scattered act matrix when
+// the tokens' blocks cover most of the layer (M k >= 2 NB) and the shapes fit
+// it; otherwise as the grouped per-block down.
+static bool prefill_dense_down(int H, int NB, int M, int k) {
+  return H % 256 == 0 && NB % 4 == 0 && (long long)M * k >= 2LL * NB && (long long)M * NB * 64 < (1LL << 31) &&
+         (long long)M * H * 2 < (1LL << 31);
+}
+
 size_t nsmlp_prefill_workspace_bytes(int H, int NB, int M, int k) {
   if (H <= 0 || NB <= 0 || M <= 0 || k <= 0) return 0;
   const size_t words = (size_t)(M + 31) / 32, TG = (size_t)(M + 127) / 128, nk = (size_t)M * (size_t)k;
@@ -501,7 +517,12 @@ size_t nsmlp_prefill_workspace_bytes(int H, int NB, int M, int k) {
   off += align_up(((size_t)NB + 1) * 4);          // offsets
   off += align_up((size_t)NB * (TG + 1) * 4);     // group starts
   off += align_up(nk * 4);                         // tokens
-  off += align_up(nk * 32 * 2);                    // act
+  if (prefill_dense_down(H, NB, M, k)) {
+    off += align_up((size_t)M * NB * 64);          // dense act [M][NB 32] fp16
+    off += align_up((size_t)dense_guard_splits(H, NB, M) * M * H * 4);  // partial sums
+  } else {
+    off += align_up(nk * 32 * 2);                  // act per (block, token) entry
+  }
   return off;
 }
 
@@ -543,17 +564,16 @@ int nsmlp_prefill_slots_f16(const nsmlp_slot_table* table, const void* x, int M,
   off += align_up((size_t)p.d.NB * (p.TG + 1) * 4);
   p.tokens = (int32_t*)(base + off);
   off += align_up(nk * 4);
-  p.act = (uint16_t*)(base + off);
+  if (prefill_dense_down(p.d.H, p.d.NB, M, k)) {
+    p.act_dense = (uint16_t*)(base + off);
+    off += align_up((size_t)M * p.d.NB * 64);
+    p.part = (float*)(base + off);
+    p.S = dense_guard_splits(p.d.H, p.d.NB, M);
+  } else {
+    p.act = (uint16_t*)(base + off);
+  }
   launch_prefill(p, (hipStream_t)stream);
   return check_launch("prefill");
-}
-
-static int dense_guard_splits(int H, int NB, int M) {
-  // block ranges of the down GEMM: enough workgroups for the CUs
-  const int tiles = H / 256 * ((M + 255) / 256);
-  int S = 1;
-  while (S < 8 && tiles * S < 256 && S * 2 <= NB / 2) S *= 2;
-  return S;
 }
 
 size_t nsmlp_dense_mlp_workspace_bytes(int H, int I, int M) {

@@ -410,27 +410,37 @@ __global__ void __launch_bounds__(256) k_dg_fin(DenseGuardArgs g) {
   g.out[i] = h;
 }
 
-}  // namespace
+using DgFn = void (*)(DenseGuardArgs);
+const DgFn kDgGu[2] = {k_dg_gu<false>, k_dg_gu<true>};
+const DgFn kDgDown[2] = {k_dg_down<false>, k_dg_down<true>};
 
-void launch_dense_guard(const DenseGuardArgs& g, hipStream_t st) {
-  using Fn = void (*)(DenseGuardArgs);
-  static const Fn gu[2] = {k_dg_gu<false>, k_dg_gu<true>};
-  static const Fn dn[2] = {k_dg_down<false>, k_dg_down<true>};
+void dg_set_lds() {
   static std::once_flag once;
   std::call_once(once, [] {
     for (int q = 0; q < 2; ++q) {
-      (void)hipFuncSetAttribute(reinterpret_cast<const void*>(gu[q]), hipFuncAttributeMaxDynamicSharedMemorySize,
+      (void)hipFuncSetAttribute(reinterpret_cast<const void*>(kDgGu[q]), hipFuncAttributeMaxDynamicSharedMemorySize,
                                 (int)kDgLds);
-      (void)hipFuncSetAttribute(reinterpret_cast<const void*>(dn[q]), hipFuncAttributeMaxDynamicSharedMemorySize,
-                                (int)kDgLds);
+      (void)hipFuncSetAttribute(reinterpret_cast<const void*>(kDgDown[q]),
+                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)kDgLds);
     }
   });
-  const int dq = g.d.dq ? 1 : 0;
+}
+
+}  // namespace
+
+void launch_dense_down(const DenseGuardArgs& g, hipStream_t st) {
+  dg_set_lds();
   const unsigned mt = (unsigned)((g.M + kDgTok - 1) / kDgTok);
-  gu[dq]<<<dim3((unsigned)(g.d.NB / 4), mt), dim3(kDgThreads), kDgLds, st>>>(g);
-  dn[dq]<<<dim3((unsigned)(g.d.H / 256 * g.S), mt), dim3(kDgThreads), kDgLds, st>>>(g);
+  kDgDown[g.d.dq ? 1 : 0]<<<dim3((unsigned)(g.d.H / 256 * g.S), mt), dim3(kDgThreads), kDgLds, st>>>(g);
   const long long n = (long long)g.M * g.d.H;
   k_dg_fin<<<dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st>>>(g);
+}
+
+void launch_dense_guard(const DenseGuardArgs& g, hipStream_t st) {
+  dg_set_lds();
+  const unsigned mt = (unsigned)((g.M + kDgTok - 1) / kDgTok);
+  kDgGu[g.d.dq ? 1 : 0]<<<dim3((unsigned)(g.d.NB / 4), mt), dim3(kDgThreads), kDgLds, st>>>(g);
+  launch_dense_down(g, st);
 }
 
 }  // namespace nsmlp

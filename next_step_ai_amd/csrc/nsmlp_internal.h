@@ -650,7 +650,12 @@ struct PrefillArgs {
   int32_t* grp;           // [NB][TG + 1] CSR index of the first token of each 128-token group
   int TG;                 // token groups
   int32_t* tokens;        // [M k] token ids per block, ascending
-  uint16_t* act;          // [M k][32] fp16 silu(gate) * up per (block, token) entry
+  uint16_t* act;          // [M k][32] fp16 silu(gate) * up per (block, token) entry (grouped down)
+  // dense down (when the union covers most blocks): act scattered into a
+  // zeroed [M][NB 32] matrix, then the dense-guard down GEMM over it
+  uint16_t* act_dense;    // or nullptr
+  float* part;            // [S][M][H] fp32 partial sums
+  int S;
 };
 void launch_prefill(const PrefillArgs& p, hipStream_t s);
 
@@ -667,6 +672,8 @@ struct DenseGuardArgs {
   const uint16_t* residual;  // [M][H] fp16 added to the rounded output, or nullptr
 };
 void launch_dense_guard(const DenseGuardArgs& g, hipStream_t s);
+// The down GEMM and the final sum alone, over g.act (the prefill's dense path).
+void launch_dense_down(const DenseGuardArgs& g, hipStream_t s);
 
 // Dense NF4 rows (the LM head): y[t][o] = sum_i W[o][i] x[t][i] over a
 // row-major [out][in] NF4 matrix, in % 32 == 0, in <= 16384.

@@ -25,6 +25,8 @@
 // chunk is permuted (lane group g takes columns 32 g .. 32 g + 31 over the
 // chunk's four MFMA steps) so that each lane reads contiguous bytes; A and B
 // use the same permutation, which leaves the dot products unchanged.
+#include <cstring>
+
 #include "nsmlp_internal.h"
 
 namespace nsmlp {
@@ -330,7 +332,11 @@ __global__ void __launch_bounds__(kPfThreads, 4) k_pf_gu(PrefillArgs p) {  // 4 
     for (int o = tid; o < T * 32; o += kPfThreads) {
       const int ti = o >> 5, row = o & 31;
       const float gs = cs[ti * 64 + row], us = cs[ti * 64 + 32 + row];
-      p.act[(long long)(beg + t0 + ti) * 32 + row] = br.ok ? f2h(silu_mul(gs, us)) : (uint16_t)0;
+      const uint16_t a = br.ok ? f2h(silu_mul(gs, us)) : (uint16_t)0;
+      if (p.act_dense != nullptr)  // token row, column 32 b + row of the zeroed dense act
+        p.act_dense[(long long)p.tokens[beg + t0 + ti] * (d.NB * 32) + 32 * b + row] = a;
+      else
+        p.act[(long long)(beg + t0 + ti) * 32 + row] = a;
     }
     __syncthreads();
   }
@@ -536,10 +542,26 @@ void launch_prefill(const PrefillArgs& p, hipStream_t s) {
   const long long n = (long long)p.M * p.k;
   k_pf_mark<<<dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s>>>(p);
   k_pf_csr<<<dim3(1), dim3(1024), 0, s>>>(p);
+  if (p.act_dense != nullptr) launch_zero_u32(reinterpret_cast<uint32_t*>(p.act_dense), (long long)p.M * p.d.NB * 16, s);
   if (p.d.dq)
     k_pf_gu<true><<<dim3(p.d.NB), dim3(kPfThreads), 0, s>>>(p);
   else
     k_pf_gu<false><<<dim3(p.d.NB), dim3(kPfThreads), 0, s>>>(p);
+  if (p.act_dense != nullptr) {
+    // every token's act is zero outside its own blocks, so the dense down GEMM
+    // over the scattered act is the per-token sum over the selected blocks
+    DenseGuardArgs g;
+    memset(&g, 0, sizeof(g));
+    g.d = p.d;
+    g.x = p.x;
+    g.M = p.M;
+    g.act = p.act_dense;
+    g.part = p.part;
+    g.S = p.S;
+    g.out = p.out;
+    launch_dense_down(g, s);
+    return;
+  }
   const dim3 gd((unsigned)((p.d.H / 64) * p.TG));
   if (p.d.dq)
     k_pf_down<true><<<gd, dim3(kPfThreads), 0, s>>>(p);

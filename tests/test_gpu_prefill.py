@@ -4,7 +4,8 @@ Bar (per token row, the same as the decode tests): relL2(gpu, exact) <=
 max(1e-3, e_ref) and relL2(gpu, fallback) <= 2 e_ref + 1e-3, where e_ref is
 the reference fallback restatement's own error (fp16 weights, gate, up, act).
 Double-quantised absmax must give bit-identical results to fp32 slots of the
-resolved absmax; repeated calls must be bit-identical (fixed-point down sums)."""
+resolved absmax; repeated calls must be bit-identical (fixed-point sums in the
+grouped down, fixed-order fp32 sums in the dense down)."""
 import numpy as np
 import pytest
 import torch
@@ -47,7 +48,8 @@ def _check_rows(orc, y, ye, yf, rows, what):
 
 
 @pytest.mark.parametrize("H,I,M,k,seed", [
-    (1024, 4096, 40, 16, 1),       # one token group, few tokens per block
+    (2048, 8192, 4, 16, 3),        # M k < 2 NB: the grouped per-block down
+    (1024, 4096, 40, 16, 1),       # one token group, few tokens per block (dense down over the scattered act)
     (4096, 14336, 256, 64, 2),     # 8B-shaped layer, M = 256 (two token groups)
 ])
 def test_prefill_matches_oracle(gpu, orc, H, I, M, k, seed):
