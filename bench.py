@@ -366,7 +366,7 @@ def run_prefill(args) -> int:
         "union_bytes": ubytes,
         "roofline": {"bound": "hbm", "achieved": round(ubytes / (mlp_us * 1e-6) / 1e9, 2), "peak": PEAK_GBS,
                      "unit": "GB/s", "frac": round(ubytes / (mlp_us * 1e-6) / 1e9 / PEAK_GBS, 4), "traffic": None,
-                     "kernels": "k_pf_mark + k_pf_csr + k_pf_gu + k_pf_down"},
+                     "kernels": "k_pf_mark + k_pf_scan + k_pf_list + k_pf_gu + k_dg_down + k_dg_fin (k_pf_down for small unions)"},
         "mfma": {"useful_tflops": round(useful_flop / (mlp_us * 1e-6) / 1e12, 2), "peak_tflops": PEAK_F16_TFLOPS,
                  "frac": round(useful_flop / (mlp_us * 1e-6) / 1e12 / PEAK_F16_TFLOPS, 4),
                  "useful_flop": useful_flop},

@@ -4,8 +4,8 @@
 // token only if the token selected it).  Grouped per block on MFMA
 // (v_mfma_f32_16x16x32_f16, fp32 accumulation):
 //
-//   k_pf_mark / k_pf_csr  token lists per block (CSR, ascending token ids),
-//                         from a [NB][M/32] membership bitmap;
+//   k_pf_mark / k_pf_scan / k_pf_list  token lists per block (CSR, ascending
+//               token ids), from a [NB][M/32] membership bitmap and counts;
 //   k_pf_gu     one workgroup per block: gate and up of the block's tokens
 //               as a staged GEMM, the token rows gathered as the MFMA A
 //               operand and the NF4 rows decoded to fp16(code * absmax) as the
@@ -92,6 +92,8 @@ __device__ __forceinline__ long long to_fix31(float v) {
 
 namespace {
 
+// Membership bitmap and per-block token counts (offsets[b + 1]; a repeated
+// (token, block) pair is counted once).
 __global__ void k_pf_mark(PrefillArgs p) {
   const long long i = (long long)blockIdx.x * 256 + threadIdx.x;
   if (i >= (long long)p.M * p.k) return;
@@ -101,24 +103,17 @@ __global__ void k_pf_mark(PrefillArgs p) {
     atomicOr(p.d.status, 1);
     return;
   }
-  atomicOr(&p.bitmap[(long long)b * p.words + (t >> 5)], 1u << (t & 31));
+  const uint32_t bit = 1u << (t & 31);
+  if ((atomicOr(&p.bitmap[(long long)b * p.words + (t >> 5)], bit) & bit) == 0) atomicAdd(&p.offsets[b + 1], 1);
 }
 
-// One workgroup: counts, exclusive scan, token lists and group starts.
-__global__ void __launch_bounds__(1024) k_pf_csr(PrefillArgs p) {
+// Exclusive scan of the block counts, in place (one workgroup).
+__global__ void __launch_bounds__(1024) k_pf_scan(PrefillArgs p) {
   __shared__ int wsum[16];
   __shared__ int carry_s;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int NB = p.d.NB;
-  for (int b = tid; b < NB; b += 1024) {
-    int c = 0;
-    for (int w = 0; w < p.words; ++w) c += __popc(p.bitmap[(long long)b * p.words + w]);
-    p.offsets[b + 1] = c;
-  }
-  if (tid == 0) {
-    p.offsets[0] = 0;
-    carry_s = 0;
-  }
+  if (tid == 0) carry_s = 0;
   __syncthreads();
   for (int base = 0; base < NB; base += 1024) {
     const int b = base + tid;
@@ -138,19 +133,33 @@ __global__ void __launch_bounds__(1024) k_pf_csr(PrefillArgs p) {
     if (tid == 1023) carry_s = before + incl;
     __syncthreads();
   }
-  for (int b = tid; b < NB; b += 1024) {
-    int pos = p.offsets[b];
-    int32_t* g = p.grp + (long long)b * (p.TG + 1);
-    for (int w = 0; w < p.words; ++w) {
+}
+
+// Token list of block b (ascending token ids) and its token-group starts, one
+// thread per block; the bitmap words go out 8 at a time.
+__global__ void __launch_bounds__(256) k_pf_list(PrefillArgs p) {
+  const int b = (int)blockIdx.x * 256 + (int)threadIdx.x;
+  if (b >= p.d.NB) return;
+  int pos = p.offsets[b];
+  int32_t* g = p.grp + (long long)b * (p.TG + 1);
+  const uint32_t* bm = p.bitmap + (long long)b * p.words;
+  for (int w0 = 0; w0 < p.words; w0 += 8) {
+    uint32_t v[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) v[u] = w0 + u < p.words ? bm[w0 + u] : 0u;
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int w = w0 + u;
+      if (w >= p.words) break;
       if ((w & 3) == 0) g[w >> 2] = pos;
-      uint32_t bits = p.bitmap[(long long)b * p.words + w];
+      uint32_t bits = v[u];
       while (bits) {
         p.tokens[pos++] = w * 32 + __builtin_ctz(bits);
         bits &= bits - 1;
       }
     }
-    for (int tg = (p.words + 3) >> 2; tg <= p.TG; ++tg) g[tg] = pos;
   }
+  for (int tg = (p.words + 3) >> 2; tg <= p.TG; ++tg) g[tg] = pos;
 }
 
 // Gate/up of one block for all its tokens, as a staged GEMM.  A pass takes
@@ -538,10 +547,12 @@ __global__ void __launch_bounds__(kPfThreads, 2) k_pf_down(PrefillArgs p) {
 }  // namespace
 
 void launch_prefill(const PrefillArgs& p, hipStream_t s) {
-  launch_zero_u32(p.bitmap, (long long)p.d.NB * p.words, s);
+  // the bitmap and the block counts (offsets, right after it) start at zero
+  launch_zero_u32(p.bitmap, (long long)(reinterpret_cast<const uint32_t*>(p.offsets + p.d.NB + 1) - p.bitmap), s);
   const long long n = (long long)p.M * p.k;
   k_pf_mark<<<dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s>>>(p);
-  k_pf_csr<<<dim3(1), dim3(1024), 0, s>>>(p);
+  k_pf_scan<<<dim3(1), dim3(1024), 0, s>>>(p);
+  k_pf_list<<<dim3((unsigned)((p.d.NB + 255) / 256)), dim3(256), 0, s>>>(p);
   if (p.act_dense != nullptr) launch_zero_u32(reinterpret_cast<uint32_t*>(p.act_dense), (long long)p.M * p.d.NB * 16, s);
   if (p.d.dq)
     k_pf_gu<true><<<dim3(p.d.NB), dim3(kPfThreads), 0, s>>>(p);
