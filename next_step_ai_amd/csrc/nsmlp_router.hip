@@ -2,7 +2,9 @@
 // _compute_sparse_basis_latent + _route_sparse_mlp, RT:4209-4238 and
 // RT:4311-4352), as three gfx950 kernels:
 //   1. latent          : one workgroup per latent row: exact fp16 dot product
-//                        of x with the enc_w row (Exact3), one fp16 rounding.
+//                        of x with the enc_w row (Exact3), one fp16 rounding;
+//                        from 8 tokens on, one workgroup per 8 x 8 tile of
+//                        latent rows and tokens (k_latent_tiled).
 //   2. scores          : fp16 latent (+ the basis_top_k mask) -> exact score
 //                        dots (8 lanes per block) -> fp16, clamp, optional
 //                        down_block_norm scaling.
@@ -71,6 +73,63 @@ __global__ void __launch_bounds__(kLatThreads) k_latent(RouteArgs a) {
       exact_merge(t, Exact3{__shfl_xor(t.a0, m, kWave), __shfl_xor(t.a1, m, kWave), __shfl_xor(t.a2, m, kWave)});
     if (lane == 0) a.lat16[(long long)row * a.R + r] = exact_to_f16(t);
   }
+}
+
+// Many tokens: one workgroup per tile of 8 latent rows x 8 tokens; its 16
+// waves each sum a sixteenth of the hidden size.  Lane l takes latent row
+// l / 8 and token l % 8 of the tile and reads 8 columns of both per step
+// (16-byte loads; the 8 lanes of one row or token read the same bytes), so
+// each x and enc_w byte is read once per tile instead of once per output.
+// Exact3 sums do not depend on how the terms are split, so the fp16 latent
+// equals k_latent's.
+constexpr int kLtRows = 8, kLtTok = 8, kLtThreads = 1024;
+
+__global__ void __launch_bounds__(kLtThreads) k_latent_tiled(RouteArgs a) {
+  const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
+  const int r = (int)blockIdx.x * kLtRows + (lane >> 3);
+  const int t = (int)blockIdx.y * kLtTok + (lane & 7);
+  const int rc = r < a.R ? r : a.R - 1, tc = t < a.rows ? t : a.rows - 1;  // clamped: every load is in range
+  const uint16_t* __restrict__ x = a.x + (long long)tc * a.H;
+  const uint16_t* __restrict__ w = a.enc_w + (long long)rc * a.H;
+  const int span = (a.H + 8 * kLtThreads / kWave - 1) / (8 * kLtThreads / kWave) * 8;  // columns per wave
+  const int c_lo = wave * span, c_hi = min(a.H, c_lo + span);
+  Exact3 acc = exact_zero();
+#pragma unroll 4
+  for (int c = c_lo; c < c_hi; c += 8) {
+    const uint4 xv = *reinterpret_cast<const uint4*>(x + c);
+    const uint4 wv = *reinterpret_cast<const uint4*>(w + c);
+    const uint32_t xs[4] = {xv.x, xv.y, xv.z, xv.w};
+    const uint32_t ws[4] = {wv.x, wv.y, wv.z, wv.w};
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      exact_add(acc, (double)(h2f((uint16_t)(xs[q] & 0xFFFFu)) * h2f((uint16_t)(ws[q] & 0xFFFFu))));
+      exact_add(acc, (double)(h2f((uint16_t)(xs[q] >> 16)) * h2f((uint16_t)(ws[q] >> 16))));
+    }
+  }
+  __shared__ double red[kLtThreads / kWave][kWave][3];
+  red[wave][lane][0] = acc.a0;
+  red[wave][lane][1] = acc.a1;
+  red[wave][lane][2] = acc.a2;
+  __syncthreads();
+  if (wave != 0) return;
+  Exact3 sum = exact_zero();
+#pragma unroll
+  for (int v = 0; v < kLtThreads / kWave; ++v) exact_merge(sum, Exact3{red[v][lane][0], red[v][lane][1], red[v][lane][2]});
+  if (a.enc_b != nullptr) exact_add(sum, (double)h2f(a.enc_b[rc]));
+  if (r < a.R && t < a.rows) a.lat16[(long long)t * a.R + r] = exact_to_f16(sum);
+}
+
+void launch_latent(const RouteArgs& a, hipStream_t s) {
+  if (a.vec && a.rows >= kLtTok) {
+    const dim3 g((a.R + kLtRows - 1) / kLtRows, (a.rows + kLtTok - 1) / kLtTok);
+    hipLaunchKernelGGL(k_latent_tiled, g, dim3(kLtThreads), 0, s, a);
+    return;
+  }
+  const dim3 g1(a.R, a.rows);
+  if (a.vec)
+    hipLaunchKernelGGL(k_latent<true>, g1, dim3(kLatThreads), 0, s, a);
+  else
+    hipLaunchKernelGGL(k_latent<false>, g1, dim3(kLatThreads), 0, s, a);
 }
 
 // Scores: 8 lanes per block (kScoreLanes), each summing every 8th basis
@@ -195,21 +254,13 @@ __global__ void __launch_bounds__(kSelThreads) k_select(RouteArgs a) {
 }  // namespace
 
 void launch_route_scores(const RouteArgs& a, hipStream_t s) {
-  dim3 g1(a.R, a.rows);
-  if (a.vec)
-    hipLaunchKernelGGL(k_latent<true>, g1, dim3(kLatThreads), 0, s, a);
-  else
-    hipLaunchKernelGGL(k_latent<false>, g1, dim3(kLatThreads), 0, s, a);
+  launch_latent(a, s);
   dim3 g2((a.NB + kScoresPerWg - 1) / kScoresPerWg, a.rows);
   hipLaunchKernelGGL(k_scores, g2, dim3(kScoreThreads), (size_t)a.R * sizeof(uint16_t), s, a);
 }
 
 void launch_route(const RouteArgs& a, hipStream_t s) {
-  dim3 g1(a.R, a.rows);
-  if (a.vec)
-    hipLaunchKernelGGL(k_latent<true>, g1, dim3(kLatThreads), 0, s, a);
-  else
-    hipLaunchKernelGGL(k_latent<false>, g1, dim3(kLatThreads), 0, s, a);
+  launch_latent(a, s);
   dim3 g2((a.NB + kScoresPerWg - 1) / kScoresPerWg, a.rows);
   hipLaunchKernelGGL(k_scores, g2, dim3(kScoreThreads), (size_t)a.R * sizeof(uint16_t), s, a);
   const size_t lds = a.sorted ? (size_t)a.k * sizeof(uint32_t) : 0;

@@ -127,3 +127,25 @@ def test_route_sparse_mlp_dropin(gpu, orc):
         _, _, sel_o = orc.route(x[0, t], enc_w, enc_b, sw, sb, k)
         assert np.array_equal(out[t].cpu().numpy(), sel_o)
     assert route_sparse_mlp(_dev(x, gpu), None) is None
+
+
+@pytest.mark.parametrize("H,R,N,sx,sw", [
+    (4096, 20, 37, 1.0, 0.02),   # ragged tiles: 20 latent rows, 37 tokens
+    (16384, 64, 64, 3.0, 1.0),   # 405B hidden size, large products
+])
+def test_route_many_rows_tiled_latent(gpu, orc, H, R, N, sx, sw):
+    """From 8 tokens on the latent is computed in 8 x 8 tiles of latent rows
+    and tokens (a split of the same exact sums): latent, scores and selection
+    of every row bit-exact against the oracle."""
+    NB, k = 96, 10
+    rng = np.random.default_rng(H + N)
+    x = _rand16(rng, (N, H), sx)
+    enc_w, enc_b = _rand16(rng, (R, H), sw), _rand16(rng, R, 0.02)
+    swt, sb = _rand16(rng, (NB, R), 0.02), _rand16(rng, NB, 0.02)
+    print(f"route many rows H={H} R={R} N={N}", flush=True)
+    sel, lat, sc = _route_gpu(gpu, x, enc_w, enc_b, swt, sb, k)
+    for t in range(N):
+        lat_o, sc_o, sel_o = orc.route(x[t], enc_w, enc_b, swt, sb, k)
+        assert np.array_equal(lat[t], lat_o), f"latent of row {t}"
+        assert np.array_equal(sc[t], sc_o), f"scores of row {t}"
+        assert np.array_equal(sel[t], sel_o), f"selection of row {t}"
