@@ -35,16 +35,8 @@ namespace {
 
 constexpr int kPfThreads = 512;
 constexpr int kPfWaves = kPfThreads / kWave;
-constexpr int kChunk = 128;      // gate/up columns per wave step
 constexpr int kTokGroup = 128;   // tokens per down workgroup
 constexpr double kFixInv = 1.0 / 2147483648.0;  // down accumulator: int64 units of 2^-31
-
-__device__ __forceinline__ half8_t mfma_zero_h8() {
-  half8_t h;
-#pragma unroll
-  for (int e = 0; e < 8; ++e) h[e] = (_Float16)0.0f;
-  return h;
-}
 
 // Code-pair table: entry e (a packed NF4 byte) holds fp16 code[e >> 4] in
 // the low half (the even element) and fp16 code[e & 15] in the high half.

@@ -839,7 +839,7 @@ void launch_rows(const RowsArgs& a, int nt, hipStream_t s) {
   static const Fn fns[2][2] = {{k_rows_rep<false, 1>, k_rows_rep<false, 2>}, {k_rows_rep<true, 1>, k_rows_rep<true, 2>}};
   const size_t lds = (size_t)kRepLutBytes + 2 * kWaves * 4 * 2 * sizeof(float) + 256 * sizeof(float);
   static std::once_flag once;
-  std::call_once(once, [lds] {
+  std::call_once(once, [] {
     for (int d = 0; d < 2; ++d)
       for (int t = 0; t < 2; ++t) set_lds_limit(fns[d][t], lds);
   });
