@@ -138,10 +138,21 @@ void launch_latent(const RouteArgs& a, hipStream_t s) {
 constexpr int kScoreLanes = 8;
 constexpr int kScoresPerWg = kScoreThreads / kScoreLanes;
 
+// From 8 tokens on (and R <= 128), a workgroup scores 8 tokens with the same
+// prefetched score_w terms (score_w is then read once per 8 tokens); the
+// basis_top_k mask keeps at most 4 entries per thread (8 R <= 4 * 256).
+constexpr int kScTok = 8;
+
+__host__ __device__ inline int scores_tokens_per_wg(int rows, int R) {
+  return rows >= kScTok && R * kScTok <= 4 * kScoreThreads ? kScTok : 1;
+}
+
 __global__ void __launch_bounds__(kScoreThreads) k_scores(RouteArgs a) {
-  const int row = blockIdx.y;
+  const int tpw = scores_tokens_per_wg(a.rows, a.R);  // tokens of this workgroup
+  const int row0 = (int)blockIdx.y * tpw;
+  const int nrow = min(tpw, a.rows - row0);
   const int tid = threadIdx.x;
-  extern __shared__ uint16_t lat16[];  // [R]
+  extern __shared__ uint16_t lat16[];  // [tpw][R]
   // score_w terms of this lane (loaded before waiting for the latent)
   const int j = blockIdx.x * kScoresPerWg + tid / kScoreLanes;
   const int part = tid % kScoreLanes;
@@ -159,50 +170,64 @@ __global__ void __launch_bounds__(kScoreThreads) k_scores(RouteArgs a) {
     const int r = part + i * kScoreLanes;
     wv[i] = r < a.R ? w[r] : (uint16_t)0;
   }
-  for (int r = tid; r < a.R; r += kScoreThreads) lat16[r] = a.lat16[(long long)row * a.R + r];
+  for (int i = tid; i < nrow * a.R; i += kScoreThreads) lat16[i] = a.lat16[(long long)row0 * a.R + i];
   __syncthreads();
-  // basis_top_k mask over |latent| (RT:4233-4238); ties keep the lower index.
+  // basis_top_k mask over |latent| per token (RT:4233-4238); ties keep the
+  // lower index
   int btk = a.basis_top_k < 1 ? 1 : (a.basis_top_k > a.R ? a.R : a.basis_top_k);
   if (btk < a.R) {
-    uint16_t keep_val[4];
+    uint16_t keep_val[4];  // nrow * R <= 4 * kScoreThreads entries
     int nmine = 0;
-    for (int r = tid; r < a.R; r += kScoreThreads) {
-      uint32_t kr = f16_order_key((uint16_t)(lat16[r] & 0x7FFFu));
+    for (int i = tid; i < nrow * a.R; i += kScoreThreads) {
+      const uint16_t* lt = lat16 + (i / a.R) * a.R;
+      const int r = i % a.R;
+      uint32_t kr = f16_order_key((uint16_t)(lt[r] & 0x7FFFu));
       int rank = 0;
       for (int q = 0; q < a.R; ++q) {
-        uint32_t kq = f16_order_key((uint16_t)(lat16[q] & 0x7FFFu));
+        uint32_t kq = f16_order_key((uint16_t)(lt[q] & 0x7FFFu));
         rank += (kq > kr) || (kq == kr && q < r);
       }
-      keep_val[nmine++] = rank < btk ? lat16[r] : (uint16_t)(lat16[r] & 0x8000u);
+      keep_val[nmine++] = rank < btk ? lt[r] : (uint16_t)(lt[r] & 0x8000u);
     }
     __syncthreads();
     nmine = 0;
-    for (int r = tid; r < a.R; r += kScoreThreads) lat16[r] = keep_val[nmine++];
+    for (int i = tid; i < nrow * a.R; i += kScoreThreads) lat16[i] = keep_val[nmine++];
     __syncthreads();
   }
   if (blockIdx.x == 0 && a.latent_out != nullptr)
-    for (int r = tid; r < a.R; r += kScoreThreads) a.latent_out[(long long)row * a.R + r] = lat16[r];
-  Exact3 acc = exact_zero();
+    for (int i = tid; i < nrow * a.R; i += kScoreThreads) a.latent_out[(long long)row0 * a.R + i] = lat16[i];
   const uint16_t amask = a.legacy_abs ? 0x7FFFu : 0xFFFFu;
+  for (int tt = 0; tt < nrow; ++tt) {
+    const uint16_t* lt = lat16 + tt * a.R;
+    Exact3 acc = exact_zero();
 #pragma unroll
-  for (int i = 0; i < kPre; ++i) {
-    const int r = part + i * kScoreLanes;
-    if (r < a.R) exact_add(acc, (double)(h2f((uint16_t)(lat16[r] & amask)) * h2f(wv[i])));
-  }
-  for (int r = part + kPre * kScoreLanes; r < a.R; r += kScoreLanes) {
-    const float p = h2f((uint16_t)(lat16[r] & amask)) * h2f(w[r]);
-    exact_add(acc, (double)p);
-  }
+    for (int i = 0; i < kPre; ++i) {
+      const int r = part + i * kScoreLanes;
+      if (r < a.R) exact_add(acc, (double)(h2f((uint16_t)(lt[r] & amask)) * h2f(wv[i])));
+    }
+    for (int r = part + kPre * kScoreLanes; r < a.R; r += kScoreLanes) {
+      const float p = h2f((uint16_t)(lt[r] & amask)) * h2f(w[r]);
+      exact_add(acc, (double)p);
+    }
 #pragma unroll
-  for (int m = 1; m < kScoreLanes; m <<= 1)
-    exact_merge(acc, Exact3{__shfl_xor(acc.a0, m, kWave), __shfl_xor(acc.a1, m, kWave), __shfl_xor(acc.a2, m, kWave)});
-  if (part != 0 || j >= a.NB) return;
-  if (has_b) exact_add(acc, (double)h2f(sb));
-  uint16_t sc = exact_to_f16(acc);
-  if (!a.legacy_abs && (sc & 0x8000u)) sc = 0;  // clamp_min(0) (RT:4331)
-  if (has_n) sc = f2h(h2f(sc) * h2f(sn));  // fp16 x fp16 is exact in fp32
-  a.scores[(long long)row * a.NB + j] = sc;
-  if (a.scores_out != nullptr) a.scores_out[(long long)row * a.NB + j] = sc;
+    for (int m = 1; m < kScoreLanes; m <<= 1)
+      exact_merge(acc, Exact3{__shfl_xor(acc.a0, m, kWave), __shfl_xor(acc.a1, m, kWave), __shfl_xor(acc.a2, m, kWave)});
+    if (part == 0 && j < a.NB) {
+      if (has_b) exact_add(acc, (double)h2f(sb));
+      uint16_t sc = exact_to_f16(acc);
+      if (!a.legacy_abs && (sc & 0x8000u)) sc = 0;  // clamp_min(0) (RT:4331)
+      if (has_n) sc = f2h(h2f(sc) * h2f(sn));  // fp16 x fp16 is exact in fp32
+      const long long o = (long long)(row0 + tt) * a.NB + j;
+      a.scores[o] = sc;
+      if (a.scores_out != nullptr) a.scores_out[o] = sc;
+    }
+  }
+}
+
+void launch_scores(const RouteArgs& a, hipStream_t s) {
+  const int tpw = scores_tokens_per_wg(a.rows, a.R);
+  const dim3 g((a.NB + kScoresPerWg - 1) / kScoresPerWg, (a.rows + tpw - 1) / tpw);
+  hipLaunchKernelGGL(k_scores, g, dim3(kScoreThreads), (size_t)a.R * tpw * sizeof(uint16_t), s, a);
 }
 
 // Top-k of one token's scores (keys: fp16 order key, ties to the lower block
@@ -255,14 +280,12 @@ __global__ void __launch_bounds__(kSelThreads) k_select(RouteArgs a) {
 
 void launch_route_scores(const RouteArgs& a, hipStream_t s) {
   launch_latent(a, s);
-  dim3 g2((a.NB + kScoresPerWg - 1) / kScoresPerWg, a.rows);
-  hipLaunchKernelGGL(k_scores, g2, dim3(kScoreThreads), (size_t)a.R * sizeof(uint16_t), s, a);
+  launch_scores(a, s);
 }
 
 void launch_route(const RouteArgs& a, hipStream_t s) {
   launch_latent(a, s);
-  dim3 g2((a.NB + kScoresPerWg - 1) / kScoresPerWg, a.rows);
-  hipLaunchKernelGGL(k_scores, g2, dim3(kScoreThreads), (size_t)a.R * sizeof(uint16_t), s, a);
+  launch_scores(a, s);
   const size_t lds = a.sorted ? (size_t)a.k * sizeof(uint32_t) : 0;
   const int kpt = (a.NB + kSelThreads - 1) / kSelThreads;  // NB <= 65535: kpt <= 64
   const dim3 g3(a.rows), b3(kSelThreads);

@@ -129,23 +129,33 @@ def test_route_sparse_mlp_dropin(gpu, orc):
     assert route_sparse_mlp(_dev(x, gpu), None) is None
 
 
-@pytest.mark.parametrize("H,R,N,sx,sw", [
-    (4096, 20, 37, 1.0, 0.02),   # ragged tiles: 20 latent rows, 37 tokens
-    (16384, 64, 64, 3.0, 1.0),   # 405B hidden size, large products
+@pytest.mark.parametrize("H,R,N,sx,sw,btk,legacy", [
+    (4096, 20, 37, 1.0, 0.02, None, False),   # ragged tiles: 20 latent rows, 37 tokens
+    (16384, 64, 64, 3.0, 1.0, None, False),   # 405B hidden size, large products
+    (2048, 64, 29, 1.0, 0.02, 17, False),     # basis_top_k mask on 8 tokens per scores workgroup
+    (1024, 200, 19, 1.0, 0.02, 50, False),    # R > 128: one token per scores workgroup
+    (2048, 32, 21, 1.0, 0.02, None, True),    # legacy |latent| scores with down_block_norm
 ])
-def test_route_many_rows_tiled_latent(gpu, orc, H, R, N, sx, sw):
+def test_route_many_rows_tiled_latent(gpu, orc, H, R, N, sx, sw, btk, legacy):
     """From 8 tokens on the latent is computed in 8 x 8 tiles of latent rows
-    and tokens (a split of the same exact sums): latent, scores and selection
-    of every row bit-exact against the oracle."""
-    NB, k = 96, 10
+    and tokens (a split of the same exact sums) and the scores of 8 tokens
+    share one workgroup: latent, scores and selection of every row bit-exact
+    against the oracle."""
+    NB, k = 97, 10
     rng = np.random.default_rng(H + N)
     x = _rand16(rng, (N, H), sx)
     enc_w, enc_b = _rand16(rng, (R, H), sw), _rand16(rng, R, 0.02)
     swt, sb = _rand16(rng, (NB, R), 0.02), _rand16(rng, NB, 0.02)
-    print(f"route many rows H={H} R={R} N={N}", flush=True)
-    sel, lat, sc = _route_gpu(gpu, x, enc_w, enc_b, swt, sb, k)
+    dbn = None
+    if legacy:
+        swt = (swt & 0x7FFF).astype(np.uint16)
+        sb = None
+        dbn = (rng.random(NB) * 2).astype(np.float32)
+    print(f"route many rows H={H} R={R} N={N} btk={btk} legacy={legacy}", flush=True)
+    sel, lat, sc = _route_gpu(gpu, x, enc_w, enc_b, swt, sb, k, btk=btk, legacy=legacy, dbn=dbn)
     for t in range(N):
-        lat_o, sc_o, sel_o = orc.route(x[t], enc_w, enc_b, swt, sb, k)
+        lat_o, sc_o, sel_o = orc.route(x[t], enc_w, enc_b, swt, sb, k, basis_top_k=btk, legacy_abs=legacy,
+                                       down_block_norm=dbn)
         assert np.array_equal(lat[t], lat_o), f"latent of row {t}"
         assert np.array_equal(sc[t], sc_o), f"scores of row {t}"
         assert np.array_equal(sel[t], sel_o), f"selection of row {t}"
