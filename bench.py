@@ -384,7 +384,7 @@ def run_dense_guard(args) -> int:
     device = torch.device("cuda", 0)
     torch.cuda.set_device(device)
     H, I, R, _ = CONFIGS[7]
-    qbs, M = 64, PREFILL_TOKENS
+    qbs, M = 64, args.tokens
     n_layers = min(args.layers, 2)
     layers = []
     for l in range(n_layers):
@@ -411,7 +411,7 @@ def run_dense_guard(args) -> int:
     us = statistics.mean(a.elapsed_time(b) for a, b in ev) * 1e3
     flop = 2.0 * 3 * M * I * H
     res = base_result(args, M / (step_us * 1e-6), step_us, H, I, R, I // 32, qbs)
-    res["metric"] = "dense-guard prefill MLP tok/s per layer + MFMA TFLOP/s vs peak, 405B shape, 256 tokens"
+    res["metric"] = f"dense-guard prefill MLP tok/s per layer + MFMA TFLOP/s vs peak, 405B shape, {M} tokens"
     res["steps"] = steps
     res["config"].update({"tokens": M, "rotating_layers": n})
     res.update({
@@ -591,6 +591,8 @@ def main() -> int:
                     help="config 5: the residual add as its own launch instead of in the down kernel")
     ap.add_argument("--graph", action="store_true",
                     help="config 5: replay each token as one captured graph instead of eager launches")
+    ap.add_argument("--tokens", type=int, default=PREFILL_TOKENS,
+                    help="prompt tokens of --config 7 (the dense guard; 256 by default)")
     ap.add_argument("--absmax", choices=("dq8", "f32"), default="dq8",
                     help="absmax storage: double-quantised u8 (default) or resolved fp32")
     args = ap.parse_args()

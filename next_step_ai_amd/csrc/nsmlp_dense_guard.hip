@@ -21,6 +21,10 @@
 //              partial sums per range;
 //   k_dg_fin   y = fp16(sum of the S partials in range order + bias).
 //
+// Prompts of at most 64 tokens use 64-token tiles (wave w then computes 16
+// tokens x 64 rows; the per-element K order is the same, so every token's
+// result equals the 256-token tiles' bit for bit).
+//
 // Every sum is taken in a fixed order, so the result does not change from run
 // to run.
 #include <mutex>
@@ -32,7 +36,7 @@ namespace nsmlp {
 namespace {
 
 constexpr int kDgThreads = 512;
-constexpr int kDgTok = 256;                 // tokens per tile
+constexpr int kDgTok = 256;                 // tokens per tile (64 for prompts of at most 64 tokens)
 constexpr int kDgK = 64;                    // columns per chunk
 constexpr int kDgRow = 72;                  // halfs per staged row (64 + 8: conflict-free fragment reads)
 constexpr int kDgStage = 256 * kDgRow;      // halfs per staged operand (256 rows)
@@ -78,43 +82,46 @@ struct DgW {
   uint32_t qa;  // u8 absmax code (double-quantised)
 };
 
-// The wave's 64 x 128 tile for one staged chunk: A rows (tokens) 64 mq + 16 mi
-// + lane % 16, B rows brow(ni) + lane % 16, K halves 32 ks + 8 (lane / 16).
-template <typename BRow>
-__device__ __forceinline__ void dg_mma(float4_t (&acc)[4][8], const _Float16* As, const _Float16* Bs, int mq,
+// The wave's 16 MT x 128 tile for one staged chunk (MT = 4: 256-token tiles,
+// MT = 1: 64-token tiles): A rows (tokens) 16 MT mq + 16 mi + lane % 16, B
+// rows brow(ni) + lane % 16, K halves 32 ks + 8 (lane / 16).
+template <int MT, typename BRow>
+__device__ __forceinline__ void dg_mma(float4_t (&acc)[MT][8], const _Float16* As, const _Float16* Bs, int mq,
                                        int lane, BRow brow) {
   const int j = lane & 15, g = lane >> 4;
 #pragma unroll
   for (int ks = 0; ks < 2; ++ks) {
-    half8_t a[4];
+    half8_t a[MT];
 #pragma unroll
-    for (int mi = 0; mi < 4; ++mi)
-      a[mi] = as_h8(*reinterpret_cast<const uint4*>(As + (64 * mq + 16 * mi + j) * kDgRow + 32 * ks + 8 * g));
+    for (int mi = 0; mi < MT; ++mi)
+      a[mi] = as_h8(*reinterpret_cast<const uint4*>(As + (16 * MT * mq + 16 * mi + j) * kDgRow + 32 * ks + 8 * g));
 #pragma unroll
     for (int ni = 0; ni < 8; ++ni) {
       const half8_t b = as_h8(*reinterpret_cast<const uint4*>(Bs + (brow(ni) + j) * kDgRow + 32 * ks + 8 * g));
 #pragma unroll
-      for (int mi = 0; mi < 4; ++mi) acc[mi][ni] = mfma16(a[mi], b, acc[mi][ni]);
+      for (int mi = 0; mi < MT; ++mi) acc[mi][ni] = mfma16(a[mi], b, acc[mi][ni]);
     }
     // keep the next step's fragment reads after this step's MFMAs (register pressure)
     __builtin_amdgcn_sched_barrier(0);
   }
 }
 
-// Token rows of one chunk: piece p = tid + 512 h (h < 4) is token p / 8,
-// columns 8 (p % 8) .. + 7 of the chunk.
-__device__ __forceinline__ void dg_load_rows(uint4 (&x)[4], rsrc_t r, int tid, int t0, int M, uint32_t row_len,
+// Token rows of one chunk (64 MT tokens): piece p = tid + 512 h (h < MT) is
+// token p / 8, columns 8 (p % 8) .. + 7 of the chunk.
+template <int MT>
+__device__ __forceinline__ void dg_load_rows(uint4 (&x)[MT], rsrc_t r, int tid, int t0, int M, uint32_t row_len,
                                              uint32_t k0, bool live) {
 #pragma unroll
-  for (int h = 0; h < 4; ++h) {
+  for (int h = 0; h < MT; ++h) {
     const int p = tid + h * kDgThreads, t = t0 + (p >> 3);
     x[h] = buf_ld16c(r, (live && t < M) ? ((uint32_t)t * row_len + k0 + (uint32_t)(p & 7) * 8u) * 2u : kOffNone, 0);
   }
 }
 
-__device__ __forceinline__ void dg_store_rows(_Float16* As, const uint4 (&x)[4], int tid) {
+template <int MT>
+__device__ __forceinline__ void dg_store_rows(_Float16* As, const uint4 (&x)[MT], int tid) {
 #pragma unroll
-  for (int h = 0; h < 4; ++h) {
+  for (int h = 0; h < MT; ++h) {
     const int p = tid + h * kDgThreads;
     *reinterpret_cast<uint4*>(As + (p >> 3) * kDgRow + (p & 7) * 8) = x[h];
   }
@@ -125,10 +132,10 @@ __device__ __forceinline__ void dg_store_rows(_Float16* As, const uint4 (&x)[4],
 // from registers and chunk c + 2 is loaded into registers, so each global
 // load has a whole chunk of MFMAs to arrive; unrolled by two so the register
 // stages are named.
-template <typename LoadX, typename LoadW, typename StoreX, typename StoreW, typename Mma>
+template <int MT, typename LoadX, typename LoadW, typename StoreX, typename StoreW, typename Mma>
 __device__ __forceinline__ void dg_pipeline(int c_lo, int c_hi, LoadX load_x, LoadW load_w, StoreX store_x,
                                             StoreW store_w, Mma mma) {
-  uint4 X0[4], X1[4];
+  uint4 X0[MT], X1[MT];
   DgW W0, W1;
   load_x(X0, c_lo);
   load_w(W0, c_lo);
@@ -169,7 +176,7 @@ struct DgPair {
   uint32_t qa[2];  // u8 absmax codes (double-quantised)
 };
 
-template <bool DQ>
+template <bool DQ, int MT>
 __global__ void __launch_bounds__(kDgThreads, 2) k_dg_gu(DenseGuardArgs g) {
   extern __shared__ __attribute__((aligned(16))) uint8_t dg_lds[];
   _Float16* As = reinterpret_cast<_Float16*>(dg_lds);  // [2][256][72] token rows
@@ -179,7 +186,7 @@ __global__ void __launch_bounds__(kDgThreads, 2) k_dg_gu(DenseGuardArgs g) {
   const DecodeArgs& d = g.d;
   const int tid = threadIdx.x, lane = tid & (kWave - 1);
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int nt = blockIdx.x, t0 = blockIdx.y * kDgTok;
+  const int nt = blockIdx.x, t0 = blockIdx.y * 64 * MT;
   const int H = d.H, I = d.NB * 32, M = g.M;
   dg_pairs(cp, d.code, tid, 2);
   dg_pairs(cp + 512, d.code_up, tid, 2);
@@ -210,7 +217,7 @@ __global__ void __launch_bounds__(kDgThreads, 2) k_dg_gu(DenseGuardArgs g) {
   }
   const rsrc_t rx = make_rsrc(g.x, (int)((long long)M * H * 2));
   const int nch = H / kDgK, np = (nch + 1) / 2;
-  auto load_x = [&](uint4 (&X)[4], int c) {
+  auto load_x = [&](uint4 (&X)[MT], int c) {
     const bool live = c < nch;
     dg_load_rows(X, rx, tid, t0, M, (uint32_t)H, (uint32_t)(live ? c : 0) * kDgK, live);
   };
@@ -243,15 +250,15 @@ __global__ void __launch_bounds__(kDgThreads, 2) k_dg_gu(DenseGuardArgs g) {
     const int row = 16 * wave + (up ? 128 : 0) + (lane >> 2);
     dg_decode32<2>(Bs + bi * kDgStage + row * kDgRow + 32 * half, w, am, cp + (up ? 512 : 0) + (lane & 1));
   };
-  auto store_x = [&](int bi, const uint4 (&X)[4]) { dg_store_rows(As + bi * kDgStage, X, tid); };
+  auto store_x = [&](int bi, const uint4 (&X)[MT]) { dg_store_rows<MT>(As + bi * kDgStage, X, tid); };
   const int mq = wave & 3, nh = wave >> 2;
   auto brow = [nh](int ni) { return (ni < 4 ? 0 : 128) + 64 * nh + 16 * (ni & 3); };
-  float4_t acc[4][8];
+  float4_t acc[MT][8];
 #pragma unroll
-  for (int mi = 0; mi < 4; ++mi)
+  for (int mi = 0; mi < MT; ++mi)
 #pragma unroll
     for (int ni = 0; ni < 8; ++ni) acc[mi][ni] = float4_t{0.0f, 0.0f, 0.0f, 0.0f};
-  uint4 X[2][4];
+  uint4 X[2][MT];
   DgPair P[2];
   load_p(P[0], 0);
   load_p(P[1], 1);
@@ -284,10 +291,10 @@ __global__ void __launch_bounds__(kDgThreads, 2) k_dg_gu(DenseGuardArgs g) {
   // act = fp16(fp16(silu(fp16(g))) * fp16(u)) for (token, row)
   const int j = lane & 15, gq = lane >> 4;
 #pragma unroll
-  for (int mi = 0; mi < 4; ++mi) {
+  for (int mi = 0; mi < MT; ++mi) {
 #pragma unroll
     for (int rr = 0; rr < 4; ++rr) {
-      const int t = t0 + 64 * mq + 16 * mi + 4 * gq + rr;
+      const int t = t0 + 16 * MT * mq + 16 * mi + 4 * gq + rr;
       if (t < M) {
 #pragma unroll
         for (int ni = 0; ni < 4; ++ni) {
@@ -301,7 +308,7 @@ __global__ void __launch_bounds__(kDgThreads, 2) k_dg_gu(DenseGuardArgs g) {
   }
 }
 
-template <bool DQ>
+template <bool DQ, int MT>
 __global__ void __launch_bounds__(kDgThreads, 2) k_dg_down(DenseGuardArgs g) {
   extern __shared__ __attribute__((aligned(16))) uint8_t dg_lds[];
   _Float16* As = reinterpret_cast<_Float16*>(dg_lds);  // [2][256][72] act rows
@@ -324,7 +331,7 @@ __global__ void __launch_bounds__(kDgThreads, 2) k_dg_down(DenseGuardArgs g) {
     nt = blockIdx.x % ntiles;
     s = blockIdx.x / ntiles;
   }
-  const int t0 = blockIdx.y * kDgTok, o0 = nt * 256;
+  const int t0 = blockIdx.y * 64 * MT, o0 = nt * 256;
   const int C = NB / 2;  // chunks of two blocks
   const int c_lo = (int)((long long)s * C / S), c_hi = (int)((long long)(s + 1) * C / S);
   dg_pairs(cp, d.code_down, tid, 4);
@@ -340,7 +347,7 @@ __global__ void __launch_bounds__(kDgThreads, 2) k_dg_down(DenseGuardArgs g) {
   const rsrc_t rx = make_rsrc(g.act, (int)((long long)M * I * 2));
   const rsrc_t r2 = DQ ? make_rsrc(d.down.absmax2, (int)((((long long)H * Ad + (1 << d.dq_shift) - 1) >> d.dq_shift) * 4))
                        : rx;
-  auto load_x = [&](uint4 (&X)[4], int c) {
+  auto load_x = [&](uint4 (&X)[MT], int c) {
     const bool live = c < c_hi;
     dg_load_rows(X, rx, tid, t0, M, (uint32_t)I, (uint32_t)(live ? c : c_lo) * kDgK, live);
   };
@@ -365,7 +372,7 @@ __global__ void __launch_bounds__(kDgThreads, 2) k_dg_down(DenseGuardArgs g) {
       W.am = buf_ldf(ra, o * 4u, 0);
     }
   };
-  auto store_x = [&](int bi, const uint4 (&X)[4]) { dg_store_rows(As + bi * kDgStage, X, tid); };
+  auto store_x = [&](int bi, const uint4 (&X)[MT]) { dg_store_rows<MT>(As + bi * kDgStage, X, tid); };
   auto store_w = [&](int bi, const DgW& W) {
     float am = W.am;
     if constexpr (DQ) am = dq_absmax(c2s[W.qa], W.am, d.down.offset);
@@ -373,21 +380,21 @@ __global__ void __launch_bounds__(kDgThreads, 2) k_dg_down(DenseGuardArgs g) {
   };
   const int mq = wave & 3, nh = wave >> 2;
   auto brow = [nh](int ni) { return 128 * nh + 16 * ni; };
-  float4_t acc[4][8];
+  float4_t acc[MT][8];
 #pragma unroll
-  for (int mi = 0; mi < 4; ++mi)
+  for (int mi = 0; mi < MT; ++mi)
 #pragma unroll
     for (int ni = 0; ni < 8; ++ni) acc[mi][ni] = float4_t{0.0f, 0.0f, 0.0f, 0.0f};
   auto mma = [&](int bi) { dg_mma(acc, As + bi * kDgStage, Bs + bi * kDgStage, mq, lane, brow); };
-  dg_pipeline(c_lo, c_hi, load_x, load_w, store_x, store_w, mma);
+  dg_pipeline<MT>(c_lo, c_hi, load_x, load_w, store_x, store_w, mma);
   mfma_drain();
   const int j = lane & 15, gq = lane >> 4;
   float* part = g.part + (long long)s * M * H;
 #pragma unroll
-  for (int mi = 0; mi < 4; ++mi) {
+  for (int mi = 0; mi < MT; ++mi) {
 #pragma unroll
     for (int rr = 0; rr < 4; ++rr) {
-      const int t = t0 + 64 * mq + 16 * mi + 4 * gq + rr;
+      const int t = t0 + 16 * MT * mq + 16 * mi + 4 * gq + rr;
       if (t < M) {
 #pragma unroll
         for (int ni = 0; ni < 8; ++ni) part[(long long)t * H + o0 + 128 * nh + 16 * ni + j] = acc[mi][ni][rr];
@@ -411,18 +418,24 @@ __global__ void __launch_bounds__(256) k_dg_fin(DenseGuardArgs g) {
 }
 
 using DgFn = void (*)(DenseGuardArgs);
-const DgFn kDgGu[2] = {k_dg_gu<false>, k_dg_gu<true>};
-const DgFn kDgDown[2] = {k_dg_down<false>, k_dg_down<true>};
+// [dq][0: 256-token tiles, 1: 64-token tiles]
+const DgFn kDgGu[2][2] = {{k_dg_gu<false, 4>, k_dg_gu<false, 1>}, {k_dg_gu<true, 4>, k_dg_gu<true, 1>}};
+const DgFn kDgDown[2][2] = {{k_dg_down<false, 4>, k_dg_down<false, 1>}, {k_dg_down<true, 4>, k_dg_down<true, 1>}};
+
+// Token tile: 64 tokens for prompts of at most 64 (a 256-token tile would
+// spend its MFMAs and token-row staging on padding), else 256.
+int dg_tile_tokens(int M) { return M <= 64 ? 64 : kDgTok; }
 
 void dg_set_lds() {
   static std::once_flag once;
   std::call_once(once, [] {
-    for (int q = 0; q < 2; ++q) {
-      (void)hipFuncSetAttribute(reinterpret_cast<const void*>(kDgGu[q]), hipFuncAttributeMaxDynamicSharedMemorySize,
-                                (int)kDgLds);
-      (void)hipFuncSetAttribute(reinterpret_cast<const void*>(kDgDown[q]),
-                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)kDgLds);
-    }
+    for (int q = 0; q < 2; ++q)
+      for (int m = 0; m < 2; ++m) {
+        (void)hipFuncSetAttribute(reinterpret_cast<const void*>(kDgGu[q][m]),
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, (int)kDgLds);
+        (void)hipFuncSetAttribute(reinterpret_cast<const void*>(kDgDown[q][m]),
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, (int)kDgLds);
+      }
   });
 }
 
@@ -430,16 +443,18 @@ void dg_set_lds() {
 
 void launch_dense_down(const DenseGuardArgs& g, hipStream_t st) {
   dg_set_lds();
-  const unsigned mt = (unsigned)((g.M + kDgTok - 1) / kDgTok);
-  kDgDown[g.d.dq ? 1 : 0]<<<dim3((unsigned)(g.d.H / 256 * g.S), mt), dim3(kDgThreads), kDgLds, st>>>(g);
+  const int tt = dg_tile_tokens(g.M);
+  const unsigned mt = (unsigned)((g.M + tt - 1) / tt);
+  kDgDown[g.d.dq ? 1 : 0][tt == kDgTok ? 0 : 1]<<<dim3((unsigned)(g.d.H / 256 * g.S), mt), dim3(kDgThreads), kDgLds, st>>>(g);
   const long long n = (long long)g.M * g.d.H;
   k_dg_fin<<<dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st>>>(g);
 }
 
 void launch_dense_guard(const DenseGuardArgs& g, hipStream_t st) {
   dg_set_lds();
-  const unsigned mt = (unsigned)((g.M + kDgTok - 1) / kDgTok);
-  kDgGu[g.d.dq ? 1 : 0]<<<dim3((unsigned)(g.d.NB / 4), mt), dim3(kDgThreads), kDgLds, st>>>(g);
+  const int tt = dg_tile_tokens(g.M);
+  const unsigned mt = (unsigned)((g.M + tt - 1) / tt);
+  kDgGu[g.d.dq ? 1 : 0][tt == kDgTok ? 0 : 1]<<<dim3((unsigned)(g.d.NB / 4), mt), dim3(kDgThreads), kDgLds, st>>>(g);
   launch_dense_down(g, st);
 }
 
