@@ -21,9 +21,9 @@
 //              partial sums per range;
 //   k_dg_fin   y = fp16(sum of the S partials in range order + bias).
 //
-// Prompts of at most 64 tokens use 64-token tiles (wave w then computes 16
-// tokens x 64 rows; the per-element K order is the same, so every token's
-// result equals the 256-token tiles' bit for bit).
+// Prompts of at most 64 or 128 tokens use 64- or 128-token tiles (wave w then
+// computes 16 or 32 tokens x 64 rows; the per-element K order is the same, so
+// every token's result equals the 256-token tiles' bit for bit).
 //
 // Every sum is taken in a fixed order, so the result does not change from run
 // to run.
@@ -36,7 +36,7 @@ namespace nsmlp {
 namespace {
 
 constexpr int kDgThreads = 512;
-constexpr int kDgTok = 256;                 // tokens per tile (64 for prompts of at most 64 tokens)
+constexpr int kDgTok = 256;                 // tokens per tile (64 or 128 for prompts of at most 64 or 128 tokens)
 constexpr int kDgK = 64;                    // columns per chunk
 constexpr int kDgRow = 72;                  // halfs per staged row (64 + 8: conflict-free fragment reads)
 constexpr int kDgStage = 256 * kDgRow;      // halfs per staged operand (256 rows)
@@ -418,19 +418,23 @@ __global__ void __launch_bounds__(256) k_dg_fin(DenseGuardArgs g) {
 }
 
 using DgFn = void (*)(DenseGuardArgs);
-// [dq][0: 256-token tiles, 1: 64-token tiles]
-const DgFn kDgGu[2][2] = {{k_dg_gu<false, 4>, k_dg_gu<false, 1>}, {k_dg_gu<true, 4>, k_dg_gu<true, 1>}};
-const DgFn kDgDown[2][2] = {{k_dg_down<false, 4>, k_dg_down<false, 1>}, {k_dg_down<true, 4>, k_dg_down<true, 1>}};
+// [dq][MT - 1 of the 64 MT-token tile: 1, 2 or 4]
+const DgFn kDgGu[2][4] = {{k_dg_gu<false, 1>, k_dg_gu<false, 2>, nullptr, k_dg_gu<false, 4>},
+                          {k_dg_gu<true, 1>, k_dg_gu<true, 2>, nullptr, k_dg_gu<true, 4>}};
+const DgFn kDgDown[2][4] = {{k_dg_down<false, 1>, k_dg_down<false, 2>, nullptr, k_dg_down<false, 4>},
+                            {k_dg_down<true, 1>, k_dg_down<true, 2>, nullptr, k_dg_down<true, 4>}};
 
-// Token tile: 64 tokens for prompts of at most 64 (a 256-token tile would
-// spend its MFMAs and token-row staging on padding), else 256.
-int dg_tile_tokens(int M) { return M <= 64 ? 64 : kDgTok; }
+// Token tile: the smallest of 64, 128 and 256 tokens that holds a prompt of
+// at most 128 tokens (a larger tile would spend its MFMAs and token-row
+// staging on padding), else 256.
+int dg_tile_tokens(int M) { return M <= 64 ? 64 : (M <= 128 ? 128 : kDgTok); }
 
 void dg_set_lds() {
   static std::once_flag once;
   std::call_once(once, [] {
     for (int q = 0; q < 2; ++q)
-      for (int m = 0; m < 2; ++m) {
+      for (int m = 0; m < 4; ++m) {
+        if (kDgGu[q][m] == nullptr) continue;
         (void)hipFuncSetAttribute(reinterpret_cast<const void*>(kDgGu[q][m]),
                                   hipFuncAttributeMaxDynamicSharedMemorySize, (int)kDgLds);
         (void)hipFuncSetAttribute(reinterpret_cast<const void*>(kDgDown[q][m]),
@@ -445,7 +449,7 @@ void launch_dense_down(const DenseGuardArgs& g, hipStream_t st) {
   dg_set_lds();
   const int tt = dg_tile_tokens(g.M);
   const unsigned mt = (unsigned)((g.M + tt - 1) / tt);
-  kDgDown[g.d.dq ? 1 : 0][tt == kDgTok ? 0 : 1]<<<dim3((unsigned)(g.d.H / 256 * g.S), mt), dim3(kDgThreads), kDgLds, st>>>(g);
+  kDgDown[g.d.dq ? 1 : 0][tt / 64 - 1]<<<dim3((unsigned)(g.d.H / 256 * g.S), mt), dim3(kDgThreads), kDgLds, st>>>(g);
   const long long n = (long long)g.M * g.d.H;
   k_dg_fin<<<dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st>>>(g);
 }
@@ -454,7 +458,7 @@ void launch_dense_guard(const DenseGuardArgs& g, hipStream_t st) {
   dg_set_lds();
   const int tt = dg_tile_tokens(g.M);
   const unsigned mt = (unsigned)((g.M + tt - 1) / tt);
-  kDgGu[g.d.dq ? 1 : 0][tt == kDgTok ? 0 : 1]<<<dim3((unsigned)(g.d.NB / 4), mt), dim3(kDgThreads), kDgLds, st>>>(g);
+  kDgGu[g.d.dq ? 1 : 0][tt / 64 - 1]<<<dim3((unsigned)(g.d.NB / 4), mt), dim3(kDgThreads), kDgLds, st>>>(g);
   launch_dense_down(g, st);
 }
 
