@@ -21,9 +21,10 @@
 //              partial sums per range;
 //   k_dg_fin   y = fp16(sum of the S partials in range order + bias).
 //
-// Prompts of at most 64 or 128 tokens use 64- or 128-token tiles (wave w then
-// computes 16 or 32 tokens x 64 rows; the per-element K order is the same, so
-// every token's result equals the 256-token tiles' bit for bit).
+// Prompts of fewer than 256 tokens use the smallest tile of 64, 128 or 192
+// tokens that holds them (wave w then computes 16, 32 or 48 tokens x 64 rows;
+// the per-element K order is the same, so every token's result equals the
+// 256-token tiles' bit for bit).
 //
 // Every sum is taken in a fixed order, so the result does not change from run
 // to run.
@@ -36,7 +37,7 @@ namespace nsmlp {
 namespace {
 
 constexpr int kDgThreads = 512;
-constexpr int kDgTok = 256;                 // tokens per tile (64 or 128 for prompts of at most 64 or 128 tokens)
+constexpr int kDgTok = 256;                 // tokens per tile (64, 128 or 192 for shorter prompts)
 constexpr int kDgK = 64;                    // columns per chunk
 constexpr int kDgRow = 72;                  // halfs per staged row (64 + 8: conflict-free fragment reads)
 constexpr int kDgStage = 256 * kDgRow;      // halfs per staged operand (256 rows)
@@ -418,23 +419,22 @@ __global__ void __launch_bounds__(256) k_dg_fin(DenseGuardArgs g) {
 }
 
 using DgFn = void (*)(DenseGuardArgs);
-// [dq][MT - 1 of the 64 MT-token tile: 1, 2 or 4]
-const DgFn kDgGu[2][4] = {{k_dg_gu<false, 1>, k_dg_gu<false, 2>, nullptr, k_dg_gu<false, 4>},
-                          {k_dg_gu<true, 1>, k_dg_gu<true, 2>, nullptr, k_dg_gu<true, 4>}};
-const DgFn kDgDown[2][4] = {{k_dg_down<false, 1>, k_dg_down<false, 2>, nullptr, k_dg_down<false, 4>},
-                            {k_dg_down<true, 1>, k_dg_down<true, 2>, nullptr, k_dg_down<true, 4>}};
+// [dq][MT - 1 of the 64 MT-token tile]
+const DgFn kDgGu[2][4] = {{k_dg_gu<false, 1>, k_dg_gu<false, 2>, k_dg_gu<false, 3>, k_dg_gu<false, 4>},
+                          {k_dg_gu<true, 1>, k_dg_gu<true, 2>, k_dg_gu<true, 3>, k_dg_gu<true, 4>}};
+const DgFn kDgDown[2][4] = {{k_dg_down<false, 1>, k_dg_down<false, 2>, k_dg_down<false, 3>, k_dg_down<false, 4>},
+                            {k_dg_down<true, 1>, k_dg_down<true, 2>, k_dg_down<true, 3>, k_dg_down<true, 4>}};
 
-// Token tile: the smallest of 64, 128 and 256 tokens that holds a prompt of
-// at most 128 tokens (a larger tile would spend its MFMAs and token-row
-// staging on padding), else 256.
-int dg_tile_tokens(int M) { return M <= 64 ? 64 : (M <= 128 ? 128 : kDgTok); }
+// Token tile: the smallest multiple of 64 tokens that holds a prompt of at
+// most 256 tokens (a larger tile would spend its MFMAs and token-row staging
+// on padding), else 256.
+int dg_tile_tokens(int M) { return M >= kDgTok ? kDgTok : (M + 63) / 64 * 64; }
 
 void dg_set_lds() {
   static std::once_flag once;
   std::call_once(once, [] {
     for (int q = 0; q < 2; ++q)
       for (int m = 0; m < 4; ++m) {
-        if (kDgGu[q][m] == nullptr) continue;
         (void)hipFuncSetAttribute(reinterpret_cast<const void*>(kDgGu[q][m]),
                                   hipFuncAttributeMaxDynamicSharedMemorySize, (int)kDgLds);
         (void)hipFuncSetAttribute(reinterpret_cast<const void*>(kDgDown[q][m]),

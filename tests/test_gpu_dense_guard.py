@@ -140,17 +140,17 @@ def test_dense_mlp_smallest_shape(gpu, orc):
     assert e <= 1e-3
 
 
-@pytest.mark.parametrize("M", [37, 64, 100, 128])
+@pytest.mark.parametrize("M", [37, 64, 100, 128, 150])
 def test_dense_mlp_short_prompt_tile_bit_identical(gpu, M):
-    """Up to 64 (128) tokens run in 64- (128-) token tiles; each token's output
-    equals the 256-token tiles' (a 129-token call) bit for bit."""
+    """Fewer than 256 tokens run in 64-, 128- or 192-token tiles; each token's
+    output equals the 256-token tiles' (a 257-token call) bit for bit."""
     from next_step_ai_amd.synth import make_synthetic_layer, synth_normal_f16
 
     H, I, R = 4096, 14336, 64
     print(f"dense guard short prompt H={H} I={I} M={M}", flush=True)
     L = make_synthetic_layer(H=H, I=I, R=R, seed=141, device=gpu, double_quant=True)
     t = L.slot_table()
-    x = synth_normal_f16(142, (129, H), 1.0, gpu)
+    x = synth_normal_f16(142, (257, H), 1.0, gpu)
     y_long = t.dense_mlp(x)
     y_short = t.dense_mlp(x[:M].contiguous())
     res = synth_normal_f16(143, (M, H), 1.0, gpu)
