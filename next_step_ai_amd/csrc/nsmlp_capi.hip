@@ -494,8 +494,10 @@ int nsmlp_decode_layer_add_f16(const nsmlp_router* router, const nsmlp_slot_tabl
 }
 
 static int dense_guard_splits(int H, int NB, int M) {
-  // block ranges of the down GEMM: enough workgroups for the CUs
-  const int tiles = H / 256 * ((M + 255) / 256);
+  // block ranges of the down GEMM: enough workgroups for the CUs in the launch
+  // of the whole 256-token tiles (the rest of the tokens get a launch of one
+  // smaller tile)
+  const int tiles = H / 256 * (M / 256 > 1 ? M / 256 : 1);
   int S = 1;
   while (S < 8 && tiles * S < 256 && S * 2 <= NB / 2) S *= 2;
   return S;

@@ -21,9 +21,10 @@
 //              partial sums per range;
 //   k_dg_fin   y = fp16(sum of the S partials in range order + bias).
 //
-// Prompts of fewer than 256 tokens use the smallest tile of 64, 128 or 192
-// tokens that holds them (wave w then computes 16, 32 or 48 tokens x 64 rows;
-// the per-element K order is the same, so every token's result equals the
+// The tokens past the last whole 256-token tile (all of a prompt of fewer than
+// 256) go in a second launch with the smallest tile of 64, 128 or 192 tokens
+// that holds them (wave w then computes 16, 32 or 48 tokens x 64 rows; the
+// per-element K order is the same, so every token's result equals the
 // 256-token tiles' bit for bit).
 //
 // Every sum is taken in a fixed order, so the result does not change from run
@@ -187,7 +188,7 @@ __global__ void __launch_bounds__(kDgThreads, 2) k_dg_gu(DenseGuardArgs g) {
   const DecodeArgs& d = g.d;
   const int tid = threadIdx.x, lane = tid & (kWave - 1);
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int nt = blockIdx.x, t0 = blockIdx.y * 64 * MT;
+  const int nt = blockIdx.x, t0 = g.t_base + (int)blockIdx.y * 64 * MT;
   const int H = d.H, I = d.NB * 32, M = g.M;
   dg_pairs(cp, d.code, tid, 2);
   dg_pairs(cp + 512, d.code_up, tid, 2);
@@ -332,7 +333,7 @@ __global__ void __launch_bounds__(kDgThreads, 2) k_dg_down(DenseGuardArgs g) {
     nt = blockIdx.x % ntiles;
     s = blockIdx.x / ntiles;
   }
-  const int t0 = blockIdx.y * 64 * MT, o0 = nt * 256;
+  const int t0 = g.t_base + (int)blockIdx.y * 64 * MT, o0 = nt * 256;
   const int C = NB / 2;  // chunks of two blocks
   const int c_lo = (int)((long long)s * C / S), c_hi = (int)((long long)(s + 1) * C / S);
   dg_pairs(cp, d.code_down, tid, 4);
@@ -425,10 +426,22 @@ const DgFn kDgGu[2][4] = {{k_dg_gu<false, 1>, k_dg_gu<false, 2>, k_dg_gu<false, 
 const DgFn kDgDown[2][4] = {{k_dg_down<false, 1>, k_dg_down<false, 2>, k_dg_down<false, 3>, k_dg_down<false, 4>},
                             {k_dg_down<true, 1>, k_dg_down<true, 2>, k_dg_down<true, 3>, k_dg_down<true, 4>}};
 
-// Token tile: the smallest multiple of 64 tokens that holds a prompt of at
-// most 256 tokens (a larger tile would spend its MFMAs and token-row staging
-// on padding), else 256.
-int dg_tile_tokens(int M) { return M >= kDgTok ? kDgTok : (M + 63) / 64 * 64; }
+// Token tiles: whole 256-token tiles, then the rest of the prompt in the
+// smallest tile of 64, 128 or 192 tokens that holds it (a 256-token tile would
+// spend its MFMAs and token-row staging on padding): one launch per tile size.
+template <typename Launch>
+void dg_token_tiles(const DenseGuardArgs& g, Launch launch) {
+  const int full = g.M / kDgTok, rest = g.M - full * kDgTok;
+  DenseGuardArgs a = g;
+  if (full > 0) {
+    a.t_base = 0;
+    launch(a, 3, full);
+  }
+  if (rest > 0) {
+    a.t_base = full * kDgTok;
+    launch(a, (rest + 63) / 64 - 1, 1);
+  }
+}
 
 void dg_set_lds() {
   static std::once_flag once;
@@ -447,18 +460,19 @@ void dg_set_lds() {
 
 void launch_dense_down(const DenseGuardArgs& g, hipStream_t st) {
   dg_set_lds();
-  const int tt = dg_tile_tokens(g.M);
-  const unsigned mt = (unsigned)((g.M + tt - 1) / tt);
-  kDgDown[g.d.dq ? 1 : 0][tt / 64 - 1]<<<dim3((unsigned)(g.d.H / 256 * g.S), mt), dim3(kDgThreads), kDgLds, st>>>(g);
+  dg_token_tiles(g, [&](const DenseGuardArgs& a, int mt_idx, int tiles) {
+    kDgDown[a.d.dq ? 1 : 0][mt_idx]<<<dim3((unsigned)(a.d.H / 256 * a.S), (unsigned)tiles), dim3(kDgThreads), kDgLds,
+                                      st>>>(a);
+  });
   const long long n = (long long)g.M * g.d.H;
   k_dg_fin<<<dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st>>>(g);
 }
 
 void launch_dense_guard(const DenseGuardArgs& g, hipStream_t st) {
   dg_set_lds();
-  const int tt = dg_tile_tokens(g.M);
-  const unsigned mt = (unsigned)((g.M + tt - 1) / tt);
-  kDgGu[g.d.dq ? 1 : 0][tt / 64 - 1]<<<dim3((unsigned)(g.d.NB / 4), mt), dim3(kDgThreads), kDgLds, st>>>(g);
+  dg_token_tiles(g, [&](const DenseGuardArgs& a, int mt_idx, int tiles) {
+    kDgGu[a.d.dq ? 1 : 0][mt_idx]<<<dim3((unsigned)(a.d.NB / 4), (unsigned)tiles), dim3(kDgThreads), kDgLds, st>>>(a);
+  });
   launch_dense_down(g, st);
 }
 

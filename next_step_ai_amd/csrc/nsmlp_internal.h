@@ -670,6 +670,7 @@ struct DenseGuardArgs {
   int S;
   uint16_t* out;             // [M][H] fp16
   const uint16_t* residual;  // [M][H] fp16 added to the rounded output, or nullptr
+  int t_base;                // first token of the launch's tiles (set by the launchers)
 };
 void launch_dense_guard(const DenseGuardArgs& g, hipStream_t s);
 // The down GEMM and the final sum alone, over g.act (the prefill's dense path).

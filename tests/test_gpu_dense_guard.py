@@ -140,21 +140,26 @@ def test_dense_mlp_smallest_shape(gpu, orc):
     assert e <= 1e-3
 
 
-@pytest.mark.parametrize("M", [37, 64, 100, 128, 150])
-def test_dense_mlp_short_prompt_tile_bit_identical(gpu, M):
-    """Fewer than 256 tokens run in 64-, 128- or 192-token tiles; each token's
-    output equals the 256-token tiles' (a 257-token call) bit for bit."""
+@pytest.mark.parametrize("M", [37, 64, 100, 128, 150, 300])
+def test_dense_mlp_token_tiles_bit_identical(gpu, M):
+    """Tokens past the last whole 256-token tile (all of a shorter prompt) run
+    in a 64-, 128- or 192-token tile; every token's output equals the one a
+    full 256-token tile gives it, bit for bit."""
     from next_step_ai_amd.synth import make_synthetic_layer, synth_normal_f16
 
     H, I, R = 4096, 14336, 64
-    print(f"dense guard short prompt H={H} I={I} M={M}", flush=True)
+    print(f"dense guard token tiles H={H} I={I} M={M}", flush=True)
     L = make_synthetic_layer(H=H, I=I, R=R, seed=141, device=gpu, double_quant=True)
     t = L.slot_table()
-    x = synth_normal_f16(142, (257, H), 1.0, gpu)
-    y_long = t.dense_mlp(x)
-    y_short = t.dense_mlp(x[:M].contiguous())
+    x = synth_normal_f16(142, (300, H), 1.0, gpu)
+    y_full = t.dense_mlp(x[:256].contiguous())        # one 256-token tile
+    y = t.dense_mlp(x[:M].contiguous())
     res = synth_normal_f16(143, (M, H), 1.0, gpu)
     y_res = t.dense_mlp(x[:M].contiguous(), residual=res)
+    if M > 256:
+        y_tail = t.dense_mlp(x[M - 256:M].contiguous())  # the last M - 256 tokens inside a full tile
     torch.cuda.synchronize()
-    assert torch.equal(y_short, y_long[:M])
-    assert torch.equal(y_res, res + y_short)
+    assert torch.equal(y[:min(M, 256)], y_full[:min(M, 256)])
+    if M > 256:
+        assert torch.equal(y[256:], y_tail[512 - M:])
+    assert torch.equal(y_res, res + y)
