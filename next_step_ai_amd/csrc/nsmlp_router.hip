@@ -81,7 +81,9 @@ __global__ void __launch_bounds__(kLatThreads) k_latent(RouteArgs a) {
 // (16-byte loads; the 8 lanes of one row or token read the same bytes), so
 // each x and enc_w byte is read once per tile instead of once per output.
 // Exact3 sums do not depend on how the terms are split, so the fp16 latent
-// equals k_latent's.
+// equals k_latent's.  A tile whose terms' magnitudes add up to less than 2^39
+// per output (the common case) keeps two-part sums (Exact2: 5 instead of 9
+// fp64 operations per term); otherwise it sums again in three parts.
 constexpr int kLtRows = 8, kLtTok = 8, kLtThreads = 1024;
 
 __global__ void __launch_bounds__(kLtThreads) k_latent_tiled(RouteArgs a) {
@@ -93,7 +95,13 @@ __global__ void __launch_bounds__(kLtThreads) k_latent_tiled(RouteArgs a) {
   const uint16_t* __restrict__ w = a.enc_w + (long long)rc * a.H;
   const int span = (a.H + 8 * kLtThreads / kWave - 1) / (8 * kLtThreads / kWave) * 8;  // columns per wave
   const int c_lo = wave * span, c_hi = min(a.H, c_lo + span);
-  Exact3 acc = exact_zero();
+  __shared__ double red[kLtThreads / kWave][kWave][3];
+  __shared__ float bred[kLtThreads / kWave][kWave];
+  __shared__ int use3;
+  // First pass: the two-part sums and the sum of |term| (fp32: relative error
+  // below 2^-13 over this lane's terms, against a 4x margin below).
+  Exact2 acc2{0.0, 0.0};
+  float bound = 0.0f;
 #pragma unroll 4
   for (int c = c_lo; c < c_hi; c += 8) {
     const uint4 xv = *reinterpret_cast<const uint4*>(x + c);
@@ -102,19 +110,59 @@ __global__ void __launch_bounds__(kLtThreads) k_latent_tiled(RouteArgs a) {
     const uint32_t ws[4] = {wv.x, wv.y, wv.z, wv.w};
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
-      exact_add(acc, (double)(h2f((uint16_t)(xs[q] & 0xFFFFu)) * h2f((uint16_t)(ws[q] & 0xFFFFu))));
-      exact_add(acc, (double)(h2f((uint16_t)(xs[q] >> 16)) * h2f((uint16_t)(ws[q] >> 16))));
+      const float p0 = h2f((uint16_t)(xs[q] & 0xFFFFu)) * h2f((uint16_t)(ws[q] & 0xFFFFu));
+      const float p1 = h2f((uint16_t)(xs[q] >> 16)) * h2f((uint16_t)(ws[q] >> 16));
+      bound += fabsf(p0) + fabsf(p1);
+      exact2_add(acc2, (double)p0);
+      exact2_add(acc2, (double)p1);
     }
   }
-  __shared__ double red[kLtThreads / kWave][kWave][3];
-  red[wave][lane][0] = acc.a0;
-  red[wave][lane][1] = acc.a1;
-  red[wave][lane][2] = acc.a2;
+  red[wave][lane][0] = acc2.a0;
+  red[wave][lane][1] = acc2.a1;
+  bred[wave][lane] = bound;
   __syncthreads();
-  if (wave != 0) return;
   Exact3 sum = exact_zero();
+  if (wave == 0) {
+    Exact2 s2{0.0, 0.0};
+    float b = 0.0f;
 #pragma unroll
-  for (int v = 0; v < kLtThreads / kWave; ++v) exact_merge(sum, Exact3{red[v][lane][0], red[v][lane][1], red[v][lane][2]});
+    for (int v = 0; v < kLtThreads / kWave; ++v) {
+      s2.a0 += red[v][lane][0];
+      s2.a1 += red[v][lane][1];
+      b += bred[v][lane];
+    }
+    sum = exact2_to_3(s2);
+    // exact while the magnitudes stay below 2^40 (|a1| < 2^42 needed)
+    const bool big = !(b < 549755813888.0f);  // 2^39; also catches inf and nan
+    if (lane == 0) use3 = __ballot(big) != 0ull;
+  }
+  __syncthreads();
+  if (use3) {
+    // Large terms: the three-part sums (exact for any fp16 inputs)
+    Exact3 acc = exact_zero();
+#pragma unroll 4
+    for (int c = c_lo; c < c_hi; c += 8) {
+      const uint4 xv = *reinterpret_cast<const uint4*>(x + c);
+      const uint4 wv = *reinterpret_cast<const uint4*>(w + c);
+      const uint32_t xs[4] = {xv.x, xv.y, xv.z, xv.w};
+      const uint32_t ws[4] = {wv.x, wv.y, wv.z, wv.w};
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        exact_add(acc, (double)(h2f((uint16_t)(xs[q] & 0xFFFFu)) * h2f((uint16_t)(ws[q] & 0xFFFFu))));
+        exact_add(acc, (double)(h2f((uint16_t)(xs[q] >> 16)) * h2f((uint16_t)(ws[q] >> 16))));
+      }
+    }
+    __syncthreads();  // the first pass's partials have been read
+    red[wave][lane][0] = acc.a0;
+    red[wave][lane][1] = acc.a1;
+    red[wave][lane][2] = acc.a2;
+    __syncthreads();
+    if (wave != 0) return;
+    sum = exact_zero();
+#pragma unroll
+    for (int v = 0; v < kLtThreads / kWave; ++v) exact_merge(sum, Exact3{red[v][lane][0], red[v][lane][1], red[v][lane][2]});
+  }
+  if (wave != 0) return;
   if (a.enc_b != nullptr) exact_add(sum, (double)h2f(a.enc_b[rc]));
   if (r < a.R && t < a.rows) a.lat16[(long long)t * a.R + r] = exact_to_f16(sum);
 }

@@ -159,3 +159,30 @@ def test_route_many_rows_tiled_latent(gpu, orc, H, R, N, sx, sw, btk, legacy):
         assert np.array_equal(lat[t], lat_o), f"latent of row {t}"
         assert np.array_equal(sc[t], sc_o), f"scores of row {t}"
         assert np.array_equal(sel[t], sel_o), f"selection of row {t}"
+
+
+def test_route_tiled_latent_large_terms_exact(gpu, orc):
+    """Terms of 65504^2 that reach 2^42 before they cancel: the tiled latent
+    must fall back to three-part sums (a two-part sum would round the small
+    term 1 x (0.5 + 2^-11) added while the running sum is above 2^42)."""
+    H, R, N, NB, k = 4096, 8, 8, 40, 5
+    big = np.float16(65504.0)
+    x = np.zeros((N, H), dtype=np.float16)
+    w = np.zeros((R, H), dtype=np.float16)
+    x[:, :1280] = big
+    w[:, :1280] = big                      # waves 0-4 of the tile: +65504^2 each
+    x[:, 1536:2816] = big
+    w[:, 1536:2816] = -big                 # waves 6-10: the same terms with the other sign
+    for t in range(N):
+        x[t, 1280] = np.float16(1.0 + t / 8.0)
+    for r in range(R):
+        w[r, 1280] = np.float16(0.5 + 2.0 ** -11 + r * 2.0 ** -10)
+    rng = np.random.default_rng(23)
+    x16, w16 = x.view(np.uint16), w.view(np.uint16)
+    enc_b = _rand16(rng, R, 0.02)
+    swt, sb = _rand16(rng, (NB, R), 0.02), _rand16(rng, NB, 0.02)
+    sel, lat, sc = _route_gpu(gpu, x16, w16, enc_b, swt, sb, k)
+    for t in range(N):
+        lat_o, sc_o, sel_o = orc.route(x16[t], w16, enc_b, swt, sb, k)
+        assert np.array_equal(lat[t], lat_o), f"latent of row {t}"
+        assert np.array_equal(sc[t], sc_o) and np.array_equal(sel[t], sel_o)
