@@ -51,6 +51,7 @@ def _check_rows(orc, y, ye, yf, rows, what):
     (2048, 8192, 4, 16, 3),        # M k < 2 NB: the grouped per-block down
     (1024, 4096, 40, 16, 1),       # one token group, few tokens per block (dense down over the scattered act)
     (4096, 14336, 256, 64, 2),     # 8B-shaped layer, M = 256 (two token groups)
+    (2048, 8192, 300, 16, 5),      # dense down over a 256-token tile plus a 64-token tile
 ])
 def test_prefill_matches_oracle(gpu, orc, H, I, M, k, seed):
     from next_step_ai_amd.synth import make_synthetic_layer, synth_normal_f16
