@@ -101,11 +101,17 @@ def router_bytes(H: int, R: int, NB: int) -> int:
 
 
 def host_threads() -> int:
+    """Threads for the CPU baseline: the host's CPU share when the
+    environment sets one (OMP_NUM_THREADS; the GPU boxes allot 16 cores per
+    GPU), else every core this process may run on."""
     try:
         n = len(os.sched_getaffinity(0))
     except AttributeError:
         n = os.cpu_count() or 1
-    return max(1, min(16, n))
+    share = os.environ.get("OMP_NUM_THREADS", "").strip()
+    if share.isdigit() and int(share) > 0:
+        n = min(n, int(share))
+    return max(1, n)
 
 
 def cpu_model() -> str:
@@ -117,6 +123,33 @@ def cpu_model() -> str:
     except OSError:
         pass
     return "unknown"
+
+
+def host_description() -> dict:
+    """The host the CPU baseline ran on: lscpu's model, sockets and cores,
+    os.cpu_count(), the affinity mask and torch's thread count."""
+    import subprocess
+
+    import torch
+
+    info = {"model": cpu_model(), "os_cpu_count": os.cpu_count()}
+    try:
+        info["affinity_cpus"] = len(os.sched_getaffinity(0))
+    except AttributeError:
+        pass
+    info["torch_num_threads"] = torch.get_num_threads()
+    info["omp_num_threads_env"] = os.environ.get("OMP_NUM_THREADS")
+    try:
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+        fields = dict(line.split(":", 1) for line in out.splitlines() if ":" in line)
+        for key, name in (("Model name", "lscpu_model"), ("Socket(s)", "sockets"),
+                          ("Core(s) per socket", "cores_per_socket"), ("Thread(s) per core", "threads_per_core")):
+            if key in fields:
+                v = fields[key].strip()
+                info[name] = int(v) if v.isdigit() else v
+    except (OSError, subprocess.SubprocessError, ValueError):
+        pass
+    return info
 
 
 def measured_traffic(config: int, absmax: str):
@@ -168,9 +201,10 @@ def cpu_baseline(layer, sel, runs: int, H: int, I: int, k: int, qbs: int, absmax
         orc.route(x16, ew, eb, sw, sb, k)
         orc.sparse_mlp(x16.reshape(1, H), al, gp, ga, upk, ua, dp, da, qbs=qbs, want_exact=False, want_fallback=True)
 
-    one()  # warm-up
+    for _ in range(3):  # warm-ups
+        one()
     times = []
-    for _ in range(max(1, runs)):
+    for _ in range(max(10, runs)):
         t0 = time.perf_counter()
         one()
         times.append(time.perf_counter() - t0)
@@ -183,8 +217,10 @@ def cpu_baseline(layer, sel, runs: int, H: int, I: int, k: int, qbs: int, absmax
         "cores": threads,
         "kind": "port",
         "cpu": cpu_model(),
+        "host": host_description(),
         "sample": f"1 layer (router + dequant-fallback MLP over {k} pre-gathered blocks, fp16 rounding points, "
-                  f"fp64 accumulation), median of {len(times)} runs after 1 warm-up, {threads} OpenMP threads",
+                  f"fp64 accumulation), median of {len(times)} runs after 3 warm-ups, {threads} OpenMP threads "
+                  f"(the host's CPU share)",
     }
 
 
@@ -561,17 +597,19 @@ def run_lm_head(args) -> int:
         am = (absmax.resolve() if isinstance(absmax, NestedAbsmax) else absmax).view(V, H // qbs)[:sample].cpu().numpy()
         xh = xs[0].cpu().view(torch.int16).numpy().view(np.uint16)
         orc.set_num_threads(host_threads())
+        for _ in range(3):  # warm-ups
+            orc.dense_linear_nf4(xh, pk, am, sample, H, qbs)
         times = []
-        for _ in range(max(1, args.cpu_runs)):
+        for _ in range(max(10, args.cpu_runs)):
             c0 = time.perf_counter()
             orc.dense_linear_nf4(xh, pk, am, sample, H, qbs)
             times.append(time.perf_counter() - c0)
         full_s = statistics.median(times) * V / sample
         res["cpu_baseline"] = {"value": round(1.0 / full_s, 4), "unit": "tok/s", "cores": host_threads(),
-                               "kind": "port",
+                               "kind": "port", "host": host_description(),
                                "sample": f"oracle NF4 dequant + fp64 GEMV over the first {sample} of {V} vocabulary "
-                                         f"rows, median of {max(1, args.cpu_runs)}, scaled by {V}/{sample}; "
-                                         f"{cpu_model()}",
+                                         f"rows, median of {len(times)} runs after 3 warm-ups, scaled by "
+                                         f"{V}/{sample}; {cpu_model()}",
                                "us_per_token": round(full_s * 1e6, 1)}
     print(json.dumps(res), flush=True)
     return 0
@@ -584,7 +622,7 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--config", type=int, default=2, choices=sorted(CONFIGS))
     ap.add_argument("--layers", type=int, default=8, help="distinct layers rotated over the steps")
-    ap.add_argument("--cpu-runs", type=int, default=5)
+    ap.add_argument("--cpu-runs", type=int, default=10, help="timed CPU-baseline runs (at least 10)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="BYTES")
     ap.add_argument("--unfused-residual", action="store_true",

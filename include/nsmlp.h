@@ -66,10 +66,24 @@ int nsmlp_version(void);
 int nsmlp_device_supported(int device);
 
 /* Zero the counter region of a workspace; call once after allocating it.
- * The first int32 of a workspace is a status word: the kernels set bit 0 when
- * a selected block id is out of range, or not resident with no host copy
- * (such a block contributes zero).  It stays set until the caller clears it. */
+ * The first int32 of a workspace is a status word, set by the kernels and
+ * kept until the caller clears it:
+ *   NSMLP_STATUS_BLOCK_UNAVAILABLE: a selected block id was out of range, or
+ *     not resident with no host copy (such a block contributed zero; the
+ *     reference's gather raises there, RT:4530-4578);
+ *   NSMLP_STATUS_FIXED_RANGE: a grouped prefill down partial was outside the
+ *     fixed-point range (|v| >= 2^23, inf or nan); those outputs are wrong. */
+#define NSMLP_STATUS_BLOCK_UNAVAILABLE 1
+#define NSMLP_STATUS_FIXED_RANGE 2
 int nsmlp_workspace_init(void* ws, size_t ws_bytes, void* stream);
+
+/* Status hand-over (version >= 103): ORs the status word of `ws` into *dst
+ * (device memory, or pinned host memory through its device pointer, see
+ * nsmlp_host_device_pointer; the caller zeroes it once) and clears the word,
+ * in stream order, in one kernel (no memset: it may be captured in a graph).
+ * The caller reads *dst once the stream has passed that point (an event), so
+ * the launches in between are not stalled. */
+int nsmlp_workspace_take_status(void* ws, int32_t* dst, void* stream);
 
 /* ------------------------------------------------------------------ router
  * Replaces RT:4311-4352 (_route_sparse_mlp) together with RT:4209-4238

@@ -28,6 +28,8 @@ NSMLP_ROUTE_LEGACY_ABS = 2
 NSMLP_DOWN_BLOCK_MAJOR = 0
 NSMLP_DOWN_GATHERED = 1
 NSMLP_CACHE_GROW_ONLY = 1
+NSMLP_STATUS_BLOCK_UNAVAILABLE = 1
+NSMLP_STATUS_FIXED_RANGE = 2
 
 
 class SlotTable(ctypes.Structure):
@@ -83,6 +85,7 @@ SIGNATURES: dict[str, tuple] = {
     "nsmlp_version": (I32, []),
     "nsmlp_device_supported": (I32, [I32]),
     "nsmlp_workspace_init": (I32, [P, SZ, P]),
+    "nsmlp_workspace_take_status": (I32, [P, P, P]),
     "nsmlp_route_workspace_bytes": (SZ, [I32, I32, I32, I32, I32]),
     "nsmlp_route_f16": (I32, [P, I32, I32, P, P, I32, I32, P, P, P, I32, I32, I32, P, P, P, P, SZ, P]),
     "nsmlp_decode_workspace_bytes": (SZ, [I32, I32]),

@@ -2,6 +2,7 @@
 current HIP stream, per-(device, stream) workspaces and the NF4 code book."""
 from __future__ import annotations
 
+import ctypes
 import threading
 
 import torch
@@ -59,6 +60,65 @@ def workspace(nbytes: int, device: torch.device) -> torch.Tensor:
             _lib.call("nsmlp_workspace_init", ptr(ws), ws.numel(), key[1])
             _workspaces[key] = ws
         return ws
+
+
+_STATUS_TEXT = {
+    _lib.NSMLP_STATUS_BLOCK_UNAVAILABLE:
+        "a selected block id was out of range, or its block is neither in an HBM slot nor host-copied "
+        "(it contributed zero to the output)",
+    _lib.NSMLP_STATUS_FIXED_RANGE:
+        "a grouped prefill down partial was outside the fixed-point range (|v| >= 2^23, inf or nan); "
+        "those outputs are wrong",
+}
+
+
+def status_message(value: int, what: str) -> str:
+    parts = [text for bit, text in _STATUS_TEXT.items() if value & bit]
+    return f"{what}: " + "; ".join(parts or ["unknown status"]) + f" (status word {value:#x})"
+
+
+class StatusWord:
+    """The kernels' status word, read without stalling the launch stream.
+
+    ``take(ws)`` enqueues ``nsmlp_workspace_take_status``: the workspace's
+    status word is ORed into a pinned host word and cleared, and an event
+    marks that point of the stream.  ``poll()`` raises ``RuntimeError`` if a
+    finished take reported a problem and returns without waiting otherwise;
+    ``check()`` waits for the last take first.  The reference raises from
+    its gather for such blocks (RT:4530-4578)."""
+
+    def __init__(self, device: torch.device, what: str):
+        self.device = device
+        self.what = what
+        self.host = torch.zeros(1, dtype=torch.int32, pin_memory=True)
+        out = ctypes.c_void_p()
+        _lib.call("nsmlp_host_device_pointer", ctypes.c_void_p(self.host.data_ptr()), ctypes.byref(out))
+        self._dptr = int(out.value)
+        self._event: torch.cuda.Event | None = None
+
+    def take(self, ws: torch.Tensor) -> None:
+        if torch.cuda.is_current_stream_capturing():
+            raise RuntimeError(f"{self.what}: the status check cannot run inside a graph capture")
+        _lib.call("nsmlp_workspace_take_status", ptr(ws), self._dptr, stream_handle(self.device))
+        ev = torch.cuda.Event()
+        ev.record(torch.cuda.current_stream(self.device))
+        self._event = ev
+
+    def _read(self) -> None:
+        self._event = None
+        v = int(self.host[0])
+        if v:
+            self.host[0] = 0
+            raise RuntimeError(status_message(v, self.what))
+
+    def poll(self) -> None:
+        if self._event is not None and self._event.query():
+            self._read()
+
+    def check(self) -> None:
+        if self._event is not None:
+            self._event.synchronize()
+            self._read()
 
 
 def nf4_code(device: torch.device) -> torch.Tensor:

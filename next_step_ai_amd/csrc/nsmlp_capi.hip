@@ -366,7 +366,7 @@ extern "C" {
 
 const char* nsmlp_last_error(void) { return g_err; }
 
-int nsmlp_version(void) { return 102; }
+int nsmlp_version(void) { return 103; }
 
 int nsmlp_device_supported(int device) {
   hipDeviceProp_t prop;
@@ -379,6 +379,13 @@ int nsmlp_workspace_init(void* ws, size_t ws_bytes, void* stream) {
     return set_error(NSMLP_ENOSPC, "workspace needs at least %zu bytes", kCounterBytes);
   launch_zero_u32((uint32_t*)ws, (long long)(kCounterBytes / 4), (hipStream_t)stream);
   return check_launch("workspace init");
+}
+
+int nsmlp_workspace_take_status(void* ws, int32_t* dst, void* stream) {
+  if (ws == nullptr || dst == nullptr) return set_error(NSMLP_EINVAL, "ws and dst must be non-NULL");
+  if (((uintptr_t)ws & (kAlign - 1)) != 0) return set_error(NSMLP_EINVAL, "workspace must be 256-byte aligned");
+  launch_take_status((int*)((char*)ws + kStatusOff), (int*)dst, (hipStream_t)stream);
+  return check_launch("take status");
 }
 
 size_t nsmlp_route_workspace_bytes(int rows, int H, int R, int NB, int k) {
@@ -494,10 +501,12 @@ int nsmlp_decode_layer_add_f16(const nsmlp_router* router, const nsmlp_slot_tabl
 }
 
 static int dense_guard_splits(int H, int NB, int M) {
-  // block ranges of the down GEMM: enough workgroups for the CUs in the launch
-  // of the whole 256-token tiles (the rest of the tokens get a launch of one
-  // smaller tile)
-  const int tiles = H / 256 * (M / 256 > 1 ? M / 256 : 1);
+  // block ranges of the down GEMM: enough workgroups for the CUs with one
+  // 256-token tile.  S depends on the layer shape only, not on M: the fp32
+  // partials are added per range, so a token's output bits then do not
+  // depend on how many tokens share the call.
+  (void)M;
+  const int tiles = H / 256;
   int S = 1;
   while (S < 8 && tiles * S < 256 && S * 2 <= NB / 2) S *= 2;
   return S;

@@ -358,7 +358,8 @@ __global__ void __launch_bounds__(kDgThreads, 2) k_dg_down(DenseGuardArgs g) {
     const int b = 2 * (live ? c : c_lo) + hb;
     const int slot = d.lookup ? d.lookup[b] : b;
     const bool dev = slot >= 0;
-    const bool ok = live && (dev ? slot < d.n_slots : have_host);
+    const bool used = g.offsets == nullptr || g.offsets[b + 1] > g.offsets[b];
+    const bool ok = live && used && (dev ? slot < d.n_slots : have_host);
     const long long q = ok ? (dev ? slot : b) : 0;
     const rsrc_t rw = make_rsrc((dev ? d.down.packed : d.host_down.packed) + q * d.down.blk_stride, ok ? H * 16 : 0);
     W.w = buf_ld16(rw, o * 16u, 0);

@@ -695,6 +695,10 @@ struct DenseGuardArgs {
   uint16_t* out;             // [M][H] fp16
   const uint16_t* residual;  // [M][H] fp16 added to the rounded output, or nullptr
   int t_base;                // first token of the launch's tiles (set by the launchers)
+  // the prefill's dense down: CSR offsets [NB + 1] of the blocks' token lists;
+  // a block with no tokens has an all-zero act column and its down weights
+  // are not read (nullptr: every block is read)
+  const int32_t* offsets;
 };
 void launch_dense_guard(const DenseGuardArgs& g, hipStream_t s);
 // The down GEMM and the final sum alone, over g.act (the prefill's dense path).
@@ -807,6 +811,7 @@ struct LinearArgs {
 void launch_output_linear(const LinearArgs& a, hipStream_t s);
 void launch_input_linear(const LinearArgs& a, hipStream_t s);
 void launch_zero_u32(uint32_t* p, long long n, hipStream_t s);
+void launch_take_status(int* status, int* dst, hipStream_t s);
 void launch_silu_mul(const uint16_t* g, const uint16_t* u, uint16_t* out, long long n, hipStream_t s);
 template <typename AbsT>  // float or uint8_t (double-quantised codes)
 void launch_gather_rows(const uint8_t* src, const AbsT* src_abs, const int32_t* blocks, int src_blocks, int n,

@@ -135,6 +135,21 @@ __global__ void k_zero_u32(uint32_t* p, long long n) {
   if (i < n) p[i] = 0u;
 }
 
+// Status hand-over: the workspace's status word is ORed into dst and
+// cleared, in stream order (a kernel, not a memset, so it may sit in a
+// captured graph).  dst may be pinned host memory: its accesses are
+// system-scope, and it is read only when there is something to add.
+__global__ void k_take_status(int* status, int* dst) {
+  if (threadIdx.x == 0) {
+    const int v = *status;
+    *status = 0;
+    if (v != 0) {
+      const int old = __hip_atomic_load(dst, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+      __hip_atomic_store(dst, old | v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+    }
+  }
+}
+
 __global__ void k_silu_mul(const uint16_t* g, const uint16_t* u, uint16_t* out, long long n) {
   long long i = (long long)blockIdx.x * kThreads + threadIdx.x;
   if (i < n) out[i] = f2h(silu_mul(h2f(g[i]), h2f(u[i])));
@@ -321,6 +336,10 @@ void launch_input_linear(const LinearArgs& a, hipStream_t s) {
 
 void launch_zero_u32(uint32_t* p, long long n, hipStream_t s) {
   hipLaunchKernelGGL(k_zero_u32, dim3(grid_for(n)), dim3(kThreads), 0, s, p, n);
+}
+
+void launch_take_status(int* status, int* dst, hipStream_t s) {
+  hipLaunchKernelGGL(k_take_status, dim3(1), dim3(64), 0, s, status, dst);
 }
 
 void launch_silu_mul(const uint16_t* g, const uint16_t* u, uint16_t* out, long long n, hipStream_t s) {

@@ -407,6 +407,7 @@ __global__ void __launch_bounds__(kPfThreads, 2) k_pf_down(PrefillArgs p) {
   const int n2 = DQ ? (int)((((long long)d.H * Ad + (1 << d.dq_shift) - 1) >> d.dq_shift) * 4) : 0;
   const rsrc_t r_a2 = make_rsrc(d.down.absmax2, n2);
   const bool have_host = d.host_down.packed != nullptr;
+  bool out_of_range = false;  // a partial outside the fixed-point range (reported in the status word)
 
   for (int seg = 0; seg * 256 < nbw; ++seg) {
     const int nseg = min(256, nbw - seg * 256);
@@ -515,7 +516,9 @@ __global__ void __launch_bounds__(kPfThreads, 2) k_pf_down(PrefillArgs p) {
                 const int tl = tk[r] - t0;
 #pragma unroll
                 for (int nt = 0; nt < 4; ++nt) {
-                  atomicAdd(&acc_s[tl][nt * 16 + j], (unsigned long long)to_fix31(c[nt][r] * am[nt]));
+                  const float v = c[nt][r] * am[nt];
+                  out_of_range |= !(fabsf(v) < 8388608.0f);  // 2^23; also inf and nan
+                  atomicAdd(&acc_s[tl][nt * 16 + j], (unsigned long long)to_fix31(v));
                 }
               }
             }
@@ -525,6 +528,7 @@ __global__ void __launch_bounds__(kPfThreads, 2) k_pf_down(PrefillArgs p) {
       }
     }
   }
+  if (out_of_range) atomicOr(d.status, NSMLP_STATUS_FIXED_RANGE);
   __syncthreads();
   for (int i = tid; i < kTokGroup * 64; i += kPfThreads) {
     const int tl = i >> 6, row = i & 63;
@@ -562,6 +566,7 @@ void launch_prefill(const PrefillArgs& p, hipStream_t s) {
     g.part = p.part;
     g.S = p.S;
     g.out = p.out;
+    g.offsets = p.offsets;  // blocks no token selected are skipped (their act is zero)
     launch_dense_down(g, s);
     return;
   }

@@ -134,7 +134,9 @@ __global__ void __launch_bounds__(kLtThreads) k_latent_tiled(RouteArgs a) {
     sum = exact2_to_3(s2);
     // exact while the magnitudes stay below 2^40 (|a1| < 2^42 needed)
     const bool big = !(b < 549755813888.0f);  // 2^39; also catches inf and nan
-    if (lane == 0) use3 = __ballot(big) != 0ull;
+    // every lane of wave 0 votes (one lane per output of the tile)
+    const bool any_big = __ballot(big) != 0ull;
+    if (lane == 0) use3 = any_big;
   }
   __syncthreads();
   if (use3) {

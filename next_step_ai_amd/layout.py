@@ -18,6 +18,11 @@ import torch
 
 @dataclass(frozen=True)
 class MlpBlockBankLayout:
+    """One layer's intermediate dimension cut into ``num_blocks`` blocks of
+    ``block_size`` rows (gate/up) and columns (down).  The field names and
+    constructor are those the runtime builds from its routing artifact
+    (block_bank.py:7-36, RT:906-912); an inconsistent layout cannot be made."""
+
     layer_idx: int
     hidden_size: int
     intermediate_size: int
@@ -26,71 +31,60 @@ class MlpBlockBankLayout:
 
     def __post_init__(self) -> None:
         if int(self.layer_idx) < 0:
-            raise RuntimeError(f"layer_idx must be >= 0, got {int(self.layer_idx)}")
-        if int(self.hidden_size) <= 0:
-            raise RuntimeError(f"hidden_size must be > 0, got {int(self.hidden_size)}")
-        if int(self.intermediate_size) <= 0:
-            raise RuntimeError(f"intermediate_size must be > 0, got {int(self.intermediate_size)}")
-        if int(self.block_size) <= 0:
-            raise RuntimeError(f"block_size must be > 0, got {int(self.block_size)}")
-        if int(self.intermediate_size) % int(self.block_size) != 0:
-            raise RuntimeError(
-                f"intermediate_size={int(self.intermediate_size)} is not divisible by block_size={int(self.block_size)}"
-            )
-        expected = int(self.intermediate_size) // int(self.block_size)
-        if int(self.num_blocks) != expected:
-            raise RuntimeError(
-                f"num_blocks={int(self.num_blocks)} does not match intermediate_size/block_size={expected}"
-            )
+            raise RuntimeError(f"block bank: layer index {int(self.layer_idx)} is negative")
+        for field in ("hidden_size", "intermediate_size", "block_size"):
+            v = int(getattr(self, field))
+            if v < 1:
+                raise RuntimeError(f"block bank of layer {int(self.layer_idx)}: {field} = {v}, need at least 1")
+        whole, rest = divmod(int(self.intermediate_size), int(self.block_size))
+        if rest:
+            raise RuntimeError(f"block bank of layer {int(self.layer_idx)}: blocks of {int(self.block_size)} leave "
+                               f"{rest} of the {int(self.intermediate_size)} intermediate rows over")
+        if int(self.num_blocks) != whole:
+            raise RuntimeError(f"block bank of layer {int(self.layer_idx)}: {int(self.intermediate_size)} rows in "
+                               f"blocks of {int(self.block_size)} make {whole} blocks, not num_blocks="
+                               f"{int(self.num_blocks)}")
 
     def block_bounds(self, block_idx: int) -> tuple[int, int]:
-        i = int(block_idx)
-        if i < 0 or i >= int(self.num_blocks):
-            raise RuntimeError(f"block index out of range: {i} (num_blocks={int(self.num_blocks)})")
-        start = i * int(self.block_size)
-        return start, start + int(self.block_size)
+        """[first, last + 1) intermediate index of a block."""
+        b, bs = int(block_idx), int(self.block_size)
+        if not 0 <= b < int(self.num_blocks):
+            raise RuntimeError(f"block bank of layer {int(self.layer_idx)}: no block {b} "
+                               f"(it has {int(self.num_blocks)})")
+        return b * bs, (b + 1) * bs
 
     def as_dict(self) -> dict[str, int]:
-        return {
-            "layer_idx": int(self.layer_idx),
-            "hidden_size": int(self.hidden_size),
-            "intermediate_size": int(self.intermediate_size),
-            "block_size": int(self.block_size),
-            "num_blocks": int(self.num_blocks),
-        }
+        return {f: int(getattr(self, f)) for f in
+                ("layer_idx", "hidden_size", "intermediate_size", "block_size", "num_blocks")}
 
 
 def build_intermediate_mlp_block_bank_layout(*, layer_idx: int, hidden_size: int, intermediate_size: int,
                                              block_size: int, num_blocks: int | None = None) -> MlpBlockBankLayout:
-    inferred = int(intermediate_size) // max(int(block_size), 1)
-    return MlpBlockBankLayout(
-        layer_idx=int(layer_idx),
-        hidden_size=int(hidden_size),
-        intermediate_size=int(intermediate_size),
-        block_size=int(block_size),
-        num_blocks=int(inferred if num_blocks is None else num_blocks),
-    )
+    """The layout of a layer; ``num_blocks`` defaults to the number of whole
+    blocks (a given count is checked by the layout itself)."""
+    nb = int(intermediate_size) // max(1, int(block_size)) if num_blocks is None else int(num_blocks)
+    return MlpBlockBankLayout(layer_idx=int(layer_idx), hidden_size=int(hidden_size),
+                              intermediate_size=int(intermediate_size), block_size=int(block_size), num_blocks=nb)
 
 
 def validate_intermediate_mlp_block_bank_params(*, layout: MlpBlockBankLayout, gate_in_features: int,
                                                 gate_out_features: int, up_in_features: int, up_out_features: int,
                                                 down_in_features: int, down_out_features: int) -> None:
+    """The three projections must map hidden -> intermediate (gate, up) and
+    intermediate -> hidden (down) at the layout's sizes (block_bank.py:76-101;
+    the runtime checks this before a sparse forward, RT:5171-5172).  Every
+    mismatch is named in one RuntimeError."""
     H, I = int(layout.hidden_size), int(layout.intermediate_size)
-    if int(gate_in_features) != H or int(up_in_features) != H:
-        raise RuntimeError(
-            f"Layer {int(layout.layer_idx)} block-bank mismatch: gate/up in_features must equal hidden_size={H} "
-            f"(got gate={int(gate_in_features)}, up={int(up_in_features)})."
-        )
-    if int(gate_out_features) != I or int(up_out_features) != I:
-        raise RuntimeError(
-            f"Layer {int(layout.layer_idx)} block-bank mismatch: gate/up out_features must equal "
-            f"intermediate_size={I} (got gate={int(gate_out_features)}, up={int(up_out_features)})."
-        )
-    if int(down_out_features) != H or int(down_in_features) != I:
-        raise RuntimeError(
-            f"Layer {int(layout.layer_idx)} block-bank mismatch: down_proj expected out={H}, in={I}; "
-            f"got out={int(down_out_features)}, in={int(down_in_features)}."
-        )
+    expected = {"gate": (H, I), "up": (H, I), "down": (I, H)}
+    given = {"gate": (int(gate_in_features), int(gate_out_features)),
+             "up": (int(up_in_features), int(up_out_features)),
+             "down": (int(down_in_features), int(down_out_features))}
+    wrong = [f"{name} maps {given[name][0]} -> {given[name][1]} features, the bank needs "
+             f"{expected[name][0]} -> {expected[name][1]}" for name in ("gate", "up", "down")
+             if given[name] != expected[name]]
+    if wrong:
+        raise RuntimeError(f"layer {int(layout.layer_idx)}: projections do not fit the block bank: "
+                           + "; ".join(wrong))
 
 
 def build_sparse_active_layout(*, active_blocks: torch.Tensor, rows: int, block_size: int, max_valid_blocks: int,

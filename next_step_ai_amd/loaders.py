@@ -26,6 +26,8 @@ from dataclasses import dataclass
 
 import torch
 
+from .layout import (MlpBlockBankLayout, build_intermediate_mlp_block_bank_layout,
+                     validate_intermediate_mlp_block_bank_params)
 from .nested_absmax import NestedAbsmax
 from .slot_table import BLOCK, SparseMlpRouter, SparseMlpSlotTable
 
@@ -209,21 +211,26 @@ def _to_device(p: Nf4Param, device: torch.device):
 def slot_table_from_safetensors(source: str | os.PathLike | SafetensorShards, layer_idx: int, *,
                                 device: torch.device, prefix: str = "model.layers.{layer}.mlp.",
                                 resident_blocks: torch.Tensor | None = None, host_copy: bool = False,
-                                capacity: int | None = None) -> SparseMlpSlotTable:
+                                capacity: int | None = None,
+                                block_bank_layout: MlpBlockBankLayout | None = None) -> SparseMlpSlotTable:
     """The slot table of one layer's gate/up/down NF4 weights, read from a
     bitsandbytes safetensors checkpoint straight into block-major device
-    slots (double-quantised absmax stay u8 codes)."""
+    slots (double-quantised absmax stay u8 codes).  The checkpoint's shapes
+    are validated against ``block_bank_layout`` (the routing dict's
+    ``block_bank_layout``; default: the layout of the gate shape) as the
+    runtime does before a sparse forward (RT:5171-5172)."""
     shards = source if isinstance(source, SafetensorShards) else SafetensorShards(source)
     pre = prefix.format(layer=int(layer_idx))
     g = load_nf4_param(shards, f"{pre}gate_proj.weight")
     u = load_nf4_param(shards, f"{pre}up_proj.weight")
     d = load_nf4_param(shards, f"{pre}down_proj.weight")
     I, H = g.shape
-    if u.shape != (I, H) or d.shape != (H, I):
-        raise RuntimeError(f"layer {layer_idx}: gate {g.shape}, up {u.shape}, down {d.shape} are not "
-                           f"[I, H], [I, H], [H, I]")
-    if I % BLOCK != 0:
-        raise RuntimeError(f"intermediate_size={I} is not divisible by block_size={BLOCK}")
+    layout = block_bank_layout if block_bank_layout is not None else build_intermediate_mlp_block_bank_layout(
+        layer_idx=int(layer_idx), hidden_size=H, intermediate_size=I, block_size=BLOCK)
+    features = {"gate_in_features": g.shape[1], "gate_out_features": g.shape[0], "up_in_features": u.shape[1],
+                "up_out_features": u.shape[0], "down_in_features": d.shape[1], "down_out_features": d.shape[0]}
+    validate_intermediate_mlp_block_bank_params(layout=layout, **features)
+    H, I = int(layout.hidden_size), int(layout.intermediate_size)
     if len({g.blocksize, u.blocksize, d.blocksize}) != 1:
         raise RuntimeError(f"layer {layer_idx}: quant block sizes differ ({g.blocksize}, {u.blocksize}, "
                            f"{d.blocksize})")
@@ -234,7 +241,8 @@ def slot_table_from_safetensors(source: str | os.PathLike | SafetensorShards, la
     (gp, ga), (up, ua), (dp, da) = (_to_device(p, device) for p in (g, u, d))
     t = SparseMlpSlotTable.from_reference(gate_packed=gp, gate_absmax=ga, up_packed=up, up_absmax=ua,
                                           down_packed=dp, down_absmax=da, H=H, I=I, qbs=g.blocksize,
-                                          resident_blocks=resident_blocks, host_copy=host_copy, capacity=capacity)
+                                          resident_blocks=resident_blocks, host_copy=host_copy, capacity=capacity,
+                                          layer_idx=int(layer_idx), block_bank_layout=layout, features=features)
     t.code = g.code.to(device)
     t.as_struct()
     return t
@@ -342,6 +350,10 @@ def load_routing_artifact(path: str | os.PathLike, *, hidden_size: int, intermed
             "top_k": k, "basis_top_k": btk, "basis_rank": rank, "rank_effective": rank_eff,
             "artifact_target": target, "block_domain": domain, "block_size": block_size, "num_blocks": nb,
             "explained_variance_ratio": _stat(state, lstats, "explained_variance_ratio", 1.0),
+            # the layer's block bank, which the sparse forward validates the projections against (RT:906-912)
+            "block_bank_layout": build_intermediate_mlp_block_bank_layout(
+                layer_idx=lidx, hidden_size=int(hidden_size), intermediate_size=int(intermediate_size),
+                block_size=block_size, num_blocks=nb),
         }
     return out
 

@@ -24,24 +24,20 @@ from ._runtime import ptr, require_device, stream_handle
 
 def dynamic_map_signed() -> np.ndarray:
     """bitsandbytes' signed dynamic 8-bit map (``create_dynamic_map(signed=True,
-    max_exponent_bits=7, total_bits=8)``), restated from its published
-    construction: for exponent i = 0..6, the midpoints of 2^i + 1 evenly
-    spaced boundaries in [0.1, 1] scaled by 10^(i-6), with both signs; then 0
-    and 1; ascending (256 fp32 values)."""
-    vals: list[np.float32] = []
+    max_exponent_bits=7, total_bits=8)``), built the way its published
+    construction builds it, in torch fp32 on the CPU: for exponent i = 0..6,
+    the midpoints of ``linspace(0.1, 1, 2^i + 1)`` scaled by 10^(i-6), with
+    both signs; then 0 and 1; ascending (256 fp32 values)."""
+    parts = []
     for i in range(7):
-        items = (1 << i) + 1
-        scale = np.float32(10.0 ** (i - 6))
-        for j in range(items - 1):
-            b0 = np.float32(0.1 + (0.9 * j) / (items - 1))
-            b1 = np.float32(0.1 + (0.9 * (j + 1)) / (items - 1))
-            mean = np.float32((b0 + b1) * np.float32(0.5))
-            vals.append(np.float32(scale * mean))
-            vals.append(np.float32(-scale * mean))
-    vals += [np.float32(0.0), np.float32(1.0)]
-    out = np.array(vals, dtype=np.float32)
-    assert out.size == 256
-    return np.sort(out)
+        bounds = torch.linspace(0.1, 1.0, (1 << i) + 1, dtype=torch.float32)
+        mids = (bounds[:-1] + bounds[1:]) / 2.0
+        scale = 10.0 ** (i - 6)
+        parts += [scale * mids, -scale * mids]
+    parts.append(torch.tensor([0.0, 1.0], dtype=torch.float32))
+    out = torch.sort(torch.cat(parts)).values.numpy()
+    assert out.size == 256 and out.dtype == np.float32
+    return out
 
 
 _maps: dict[int | None, torch.Tensor] = {}

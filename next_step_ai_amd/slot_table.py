@@ -17,8 +17,10 @@ device and is read by the decode kernels directly:
 * absmax either fp32 or double-quantised (``NestedAbsmax``: u8 codes in the
   same positions, resolved by the kernels; RT:4621-4625).
 
-The fixed-capacity replacement policy keeps the reference's rule
-(``plan_fixed_capacity_bank_update``, RT:2576-2617).
+Misses are promoted into slots on the device (``HotBlockCache``) with the
+reference's fixed-capacity slot plan (RT:2576-2617): free slots first, then
+the lowest-score slot.  A block is hot iff its lookup entry is >= 0
+(RT:3588-3604); the kernels resolve that per block as they read it.
 """
 from __future__ import annotations
 
@@ -27,58 +29,12 @@ import ctypes
 import torch
 
 from . import _lib
-from ._runtime import nf4_code, ptr, require_device, stream_handle, workspace
+from ._runtime import StatusWord, nf4_code, ptr, require_device, stream_handle, workspace
+from .layout import (MlpBlockBankLayout, build_intermediate_mlp_block_bank_layout,
+                     validate_intermediate_mlp_block_bank_params)
 from .nested_absmax import NestedAbsmax
 
 BLOCK = 32
-
-
-def plan_fixed_capacity_bank_update(*, existing_block_ids_cpu: torch.Tensor, existing_scores_cpu: torch.Tensor,
-                                    active_count: int, capacity: int, novel_blocks_cpu: torch.Tensor):
-    """Slot plan for promoting ``novel_blocks_cpu`` into a fixed-capacity bank
-    (RT:2576-2617): free slots first, then the lowest-score slot; a promoted
-    block scores (max active score + 1) + (i + 1) * 1e-3.
-    Returns (slots, block_ids, scores, active_count)."""
-    cap = max(0, int(capacity))
-    active = max(0, min(int(active_count), int(existing_block_ids_cpu.numel()), cap))
-    if cap <= 0:
-        return torch.empty((0,), dtype=torch.long), existing_block_ids_cpu.clone(), existing_scores_cpu.clone(), active
-    ids = existing_block_ids_cpu.clone()
-    scores = existing_scores_cpu.clone()
-    novel = novel_blocks_cpu.detach().to(device="cpu", dtype=torch.long).reshape(-1)
-    if int(novel.numel()) <= 0:
-        return torch.empty((0,), dtype=torch.long), ids, scores, active
-    novel = novel[:cap]
-    cur = scores.clone()
-    base = float(cur[:active].max().item()) + 1.0 if active > 0 else 1.0
-    nxt = active
-    slots: list[int] = []
-    for i in range(int(novel.numel())):
-        if nxt < cap:
-            s = nxt
-            nxt += 1
-            active = max(active, s + 1)
-        else:
-            s = int(torch.argmin(cur[:cap]).item())
-        ids[s] = int(novel[i].item())
-        cur[s] = base + float(i + 1) * 1e-3
-        slots.append(s)
-    scores.copy_(cur)
-    return torch.tensor(slots, dtype=torch.long), ids, scores, active
-
-
-def partition_cached_block_lookup(lookup: torch.Tensor, *, ordered_blocks: torch.Tensor):
-    """Hot/cold split of ``ordered_blocks`` given their looked-up slots
-    (RT:3588-3604): a block is hot iff its slot is >= 0.
-    Returns (hot_positions or None, hot_slots or None, cold_blocks, cold_mask)."""
-    hot_mask = lookup >= 0
-    if bool(hot_mask.any()):
-        pos = torch.nonzero(hot_mask, as_tuple=False).flatten()
-        slots = lookup.index_select(0, pos).to(torch.long)
-    else:
-        pos, slots = None, None
-    cold_mask = ~hot_mask
-    return pos, slots, ordered_blocks[cold_mask], cold_mask
 
 
 def gather_row_blocks(packed: torch.Tensor | None, absmax: torch.Tensor, blocks: torch.Tensor, in_features: int,
@@ -142,6 +98,34 @@ def _host_dev_ptr(t: torch.Tensor | None) -> int | None:
     return int(out.value) if out.value is not None else None
 
 
+def _check_bank(layer_idx, layout, features, H, I, qbs, gp, ga, upk, ua, dp, da) -> None:
+    """Block-bank validation of a layer's reference-layout NF4 tensors."""
+    if layout is None:
+        layout = build_intermediate_mlp_block_bank_layout(layer_idx=layer_idx, hidden_size=H, intermediate_size=I,
+                                                          block_size=BLOCK)
+    if (int(layout.hidden_size), int(layout.intermediate_size), int(layout.block_size)) != (H, I, BLOCK):
+        raise RuntimeError(f"layer {int(layout.layer_idx)}: the block bank is {int(layout.hidden_size)} x "
+                           f"{int(layout.intermediate_size)} in blocks of {int(layout.block_size)}, the table "
+                           f"{H} x {I} in blocks of {BLOCK}")
+
+    def out_of(packed, in_f):  # out features implied by a packed [out, in] NF4 weight (-1: not whole rows)
+        n2 = 2 * int(packed.numel())
+        return n2 // in_f if n2 % in_f == 0 else -1
+
+    if features is None:
+        features = {"gate_in_features": H, "gate_out_features": out_of(gp, H), "up_in_features": H,
+                    "up_out_features": out_of(upk, H), "down_in_features": I, "down_out_features": out_of(dp, I)}
+    validate_intermediate_mlp_block_bank_params(layout=layout, **features)
+    for name, p, a in (("gate", gp, ga), ("up", upk, ua), ("down", dp, da)):
+        if int(p.numel()) * 2 != H * I:
+            raise RuntimeError(f"layer {int(layout.layer_idx)}: {name} packed has {int(p.numel())} bytes, "
+                               f"expected {H * I // 2}")
+        n_abs = int((a.q if isinstance(a, NestedAbsmax) else a).numel())
+        if n_abs != H * I // qbs:
+            raise RuntimeError(f"layer {int(layout.layer_idx)}: {name} absmax has {n_abs} entries, expected "
+                               f"{H * I // qbs} (one per {qbs} weights)")
+
+
 class SparseMlpSlotTable:
     """Device slot table of one layer's gate/up/down NF4 blocks."""
 
@@ -171,7 +155,9 @@ class SparseMlpSlotTable:
     def from_reference(cls, *, gate_packed: torch.Tensor, gate_absmax, up_packed: torch.Tensor, up_absmax,
                        down_packed: torch.Tensor, down_absmax, H: int, I: int, qbs: int = 64,
                        resident_blocks: torch.Tensor | None = None, host_copy: bool = False,
-                       capacity: int | None = None) -> "SparseMlpSlotTable":
+                       capacity: int | None = None, layer_idx: int = 0,
+                       block_bank_layout: MlpBlockBankLayout | None = None,
+                       features: dict[str, int] | None = None) -> "SparseMlpSlotTable":
         """Build from the reference layouts on the device: gate/up ``[I*H/2]``
         u8 + ``[I*H/qbs]`` absmax, down ``[H*I/2]`` u8 + ``[H*I/qbs]`` absmax.
         The absmax are fp32 tensors, or all three ``NestedAbsmax`` (the
@@ -179,8 +165,18 @@ class SparseMlpSlotTable:
         (default: all) go to HBM slots in the given order; with ``host_copy``
         every block is also kept in pinned host memory and non-resident
         blocks are served from there.  ``capacity`` (>= the resident count)
-        adds empty slots after the resident ones, for promotions."""
+        adds empty slots after the resident ones, for promotions.
+
+        The projections are checked against the layer's block bank first, as
+        the runtime does before a sparse forward (RT:5171-5172): against
+        ``block_bank_layout`` (the routing dict's, RT:906-912) or the layout
+        of (H, I, 32-row blocks), with the (in, out) features of each
+        projection from ``features`` (keys gate_in_features ... as
+        ``validate_intermediate_mlp_block_bank_params`` takes them; e.g. the
+        checkpoint's shapes) or else implied by the packed sizes."""
         device = require_device(gate_packed, "gate_packed")
+        _check_bank(layer_idx, block_bank_layout, features, int(H), int(I), int(qbs), gate_packed, gate_absmax,
+                    up_packed, up_absmax, down_packed, down_absmax)
         t = cls(H=H, I=I, qbs=qbs, device=device)
         nested = [isinstance(x, NestedAbsmax) for x in (gate_absmax, up_absmax, down_absmax)]
         if any(nested):
@@ -277,8 +273,19 @@ class SparseMlpSlotTable:
         self._struct = st
         return st
 
-    def decode(self, x: torch.Tensor, sel: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
-        """One decode token over the selected block ids ``sel`` [k]."""
+    def _checked(self, ws: torch.Tensor, what: str) -> None:
+        """Raise RuntimeError if the call just enqueued on ``ws`` reported a
+        block it could not serve (waits for it)."""
+        sw = StatusWord(self.device, what)
+        sw.take(ws)
+        sw.check()
+
+    def decode(self, x: torch.Tensor, sel: torch.Tensor, out: torch.Tensor | None = None, *,
+               check: bool = False) -> torch.Tensor:
+        """One decode token over the selected block ids ``sel`` [k].  With
+        ``check``, wait for it and raise RuntimeError if a selected block was
+        out of range or neither resident nor host-copied (the reference's
+        gather raises there, RT:4530-4578)."""
         x16 = x.reshape(-1).to(device=self.device, dtype=torch.float16).contiguous()
         s = sel.reshape(-1).to(device=self.device, dtype=torch.int32).contiguous()
         k = int(s.numel())
@@ -289,11 +296,13 @@ class SparseMlpSlotTable:
         st = self._struct if self._struct is not None else self.as_struct()
         _lib.call("nsmlp_decode_slots_f16", ctypes.byref(st), ptr(x16), ptr(s), k, ptr(out), ptr(ws), ws.numel(),
                   stream_handle(self.device))
+        if check:
+            self._checked(ws, "sparse MLP decode")
         return out
 
 
     def dense_mlp(self, x: torch.Tensor, out: torch.Tensor | None = None,
-                  residual: torch.Tensor | None = None) -> torch.Tensor:
+                  residual: torch.Tensor | None = None, *, check: bool = False) -> torch.Tensor:
         """The dense-guard prefill MLP (RT:5775-5831): every block for every
         token of ``x`` [M, H], as full-width MFMA GEMMs with the reference's
         rounding points (fp16 weights, g, silu(g), u, act); ``out`` [M, H]
@@ -312,12 +321,17 @@ class SparseMlpSlotTable:
         st = self._struct if self._struct is not None else self.as_struct()
         _lib.call("nsmlp_dense_mlp_slots_f16", ctypes.byref(st), ptr(x16), M, ptr(r16), ptr(out), ptr(ws), ws.numel(),
                   stream_handle(self.device))
+        if check:
+            self._checked(ws, "dense-guard MLP")
         return out
 
-    def prefill(self, x: torch.Tensor, sel: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
+    def prefill(self, x: torch.Tensor, sel: torch.Tensor, out: torch.Tensor | None = None, *,
+                check: bool = False) -> torch.Tensor:
         """M tokens ``x`` [M, H] with their own selected block ids ``sel``
         [M, k] (the multi-token branch, RT:4857-4908 + RT:5453): grouped MFMA
-        gate/up/down over the union of the selected blocks; ``out`` [M, H] fp16."""
+        gate/up/down over the union of the selected blocks; ``out`` [M, H] fp16.
+        ``check``: as in ``decode`` (also reports a grouped down partial
+        outside the fixed-point range)."""
         x16 = x.reshape(-1, self.H).to(device=self.device, dtype=torch.float16).contiguous()
         s = sel.to(device=self.device, dtype=torch.int32).contiguous()
         M, k = int(x16.shape[0]), int(s.shape[-1])
@@ -330,6 +344,8 @@ class SparseMlpSlotTable:
         st = self._struct if self._struct is not None else self.as_struct()
         _lib.call("nsmlp_prefill_slots_f16", ctypes.byref(st), ptr(x16), M, ptr(s), k, ptr(out), ptr(ws), ws.numel(),
                   stream_handle(self.device))
+        if check:
+            self._checked(ws, "sparse MLP prefill")
         return out
 
 
@@ -457,7 +473,13 @@ class SparseMlpLayer:
     round trip (the decode branch of RT:5833-5923)."""
 
     def __init__(self, router: SparseMlpRouter, table: SparseMlpSlotTable, top_k: int,
-                 cache: HotBlockCache | None = None):
+                 cache: HotBlockCache | None = None, *, check_blocks: bool = False):
+        """``check_blocks``: after every ``forward`` the kernels' status word
+        is handed to a pinned host word (one small kernel, no stall); the
+        next ``forward`` raises RuntimeError if a finished call selected a
+        block that is neither resident nor host-copied, and
+        ``check_status()`` waits and raises on demand (the reference's gather
+        raises for such a block, RT:4530-4578).  Not for graph capture."""
         if router.NB != table.NB:
             raise RuntimeError(f"router num_blocks {router.NB} != table num_blocks {table.NB}")
         if cache is not None and cache.table is not table:
@@ -470,6 +492,14 @@ class SparseMlpLayer:
         self._t = table.as_struct()
         self.device = table.device
         self._lookahead_done: torch.cuda.Event | None = None
+        self._status = StatusWord(self.device, "sparse MLP decode layer") if check_blocks else None
+
+    def check_status(self) -> None:
+        """Wait for the last checked ``forward`` and raise RuntimeError if a
+        checked call selected a block it could not serve (``check_blocks``)."""
+        if self._status is None:
+            raise RuntimeError("build the layer with check_blocks=True to check the status word")
+        self._status.check()
 
     def lookahead(self, hidden: torch.Tensor, stream: torch.cuda.Stream | None = None) -> torch.Tensor:
         """Prefetch for this layer before its decode (the decode loop's
@@ -512,6 +542,8 @@ class SparseMlpLayer:
             sel_out = torch.empty(self.top_k, dtype=torch.int32, device=self.device)
         if ws is None:
             ws = workspace(self.workspace_bytes(), self.device)
+        if self._status is not None:
+            self._status.poll()  # a finished earlier call's report; no wait
         if self._lookahead_done is not None:  # the promotion of a lookahead reads and writes the table
             torch.cuda.current_stream(self.device).wait_event(self._lookahead_done)
             self._lookahead_done = None
@@ -525,6 +557,8 @@ class SparseMlpLayer:
                 raise RuntimeError(f"residual must be a contiguous fp16 [{self.table.H}] tensor on {self.device}")
             _lib.call("nsmlp_decode_layer_add_f16", ctypes.byref(self._r), ctypes.byref(self._t), ptr(x16), ptr(r16),
                       self.top_k, ptr(sel_out), ptr(out), ptr(ws), ws.numel(), stream_handle(self.device))
+        if self._status is not None:
+            self._status.take(ws)
         if self.cache is not None:  # the blocks that missed take slots for the next tokens
             self.cache.promote(sel_out)
         return out, sel_out

@@ -354,23 +354,30 @@ void orc_nf4_dequant_f32(const uint8_t* packed, const float* absmax, long n, int
 
 /* bitsandbytes signed dynamic 8-bit map (create_dynamic_map(signed=True,
  * max_exponent_bits=7, total_bits=8)), restated from its published
- * construction: for exponent i in 0..6, (2^i + 1) linearly spaced boundaries
- * in [0.1, 1], their midpoints scaled by 10^(i-6), both signs; plus 0 and 1;
- * sorted ascending (256 values).                                             */
+ * construction, which runs in torch fp32: for exponent i in 0..6 the
+ * boundaries b = linspace(0.1, 1, 2^i + 1) in fp32, their midpoints
+ * fl32(fl32(b[j] + b[j+1]) / 2) scaled by fl32(10^(i-6)) in fp32, with both
+ * signs; plus 0 and 1; sorted ascending (256 values).  fp32 linspace(a, b,
+ * n) on the CPU is step = fl32(fl32(b - a) / (n - 1)), the first n/2 points
+ * fma(step, j, a) and the rest fma(-step, n - 1 - j, b) (one rounding each). */
 static int cmp_float_asc(const void* a, const void* b) {
   float x = *(const float*)a, y = *(const float*)b;
   return x < y ? -1 : (x > y ? 1 : 0);
 }
 
+static float linspace_f32(float a, float b, int n, int j) {
+  const float step = (b - a) / (float)(n - 1);
+  return j < n / 2 ? fmaf(step, (float)j, a) : fmaf(-step, (float)(n - 1 - j), b);
+}
+
 void orc_dynamic_map_signed(float* out256) {
   int n = 0;
   for (int i = 0; i < 7; ++i) {
-    int items = (1 << i) + 1;
-    float scale = (float)pow(10.0, (double)(i - 6));
+    const int items = (1 << i) + 1;
+    const float scale = (float)pow(10.0, (double)(i - 6));  /* the Python float 10**(i-6), as fp32 */
     for (int j = 0; j + 1 < items; ++j) {
-      float b0 = (float)(0.1 + (0.9 * j) / (double)(items - 1));
-      float b1 = (float)(0.1 + (0.9 * (j + 1)) / (double)(items - 1));
-      float mean = (b0 + b1) * 0.5f;
+      const float b0 = linspace_f32(0.1f, 1.0f, items, j), b1 = linspace_f32(0.1f, 1.0f, items, j + 1);
+      const float mean = (b0 + b1) / 2.0f;
       out256[n++] = scale * mean;
       out256[n++] = -scale * mean;
     }

@@ -178,3 +178,68 @@ def test_promotion_rejects_bad_tables(gpu):
     cache._state.capacity = 11
     with pytest.raises(RuntimeError, match="capacity"):
         cache.promote(torch.arange(4))
+
+
+def _fixture():
+    import json
+    import os
+
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "reference_test_expectations.json")
+    with open(path) as f:
+        return json.load(f)
+
+
+def test_fixture_slot_plan_on_device(gpu):
+    """The reference test's fixed-capacity plan (tests/test_throughput_contract.py:
+    308-321 there) through k_cache_plan: slots [10, 11, free] with scores
+    5, 1, 0 and two active, capacity 3; promoting 20, 21 takes the free slot,
+    then evicts the lowest score (block 11)."""
+    from next_step_ai_amd.slot_table import HotBlockCache
+    from next_step_ai_amd.synth import make_synthetic_layer
+
+    c = _fixture()["plan_fixed_capacity_bank_update"]
+    L = make_synthetic_layer(H=2048, I=1024, R=8, seed=67, device=gpu)
+    active = [b for b in c["existing_block_ids"] if b >= 0][: c["active_count"]]
+    t = L.slot_table(resident_blocks=torch.tensor(active), host_copy=True, capacity=c["capacity"])
+    cache = HotBlockCache(t, scores=torch.tensor(c["existing_scores"]), active_count=c["active_count"])
+    slots = cache.promote(torch.tensor(c["novel_blocks"], dtype=torch.int32), return_slots=True)
+    torch.cuda.synchronize()
+    sb, sc, act, lookup = cache.state_cpu()
+    assert act == c["expected_active_count"]
+    assert _np(slots).tolist() == c["expected_slots"]
+    assert sb.tolist() == c["expected_block_ids"]
+    for i, lo in c["expected_scores_above"].items():
+        assert float(sc[int(i)]) > lo
+    for s, b in enumerate(c["expected_block_ids"]):
+        assert int(lookup[b]) == s
+
+
+def test_fixture_hot_cold_partition_on_device(gpu):
+    """The reference tests' hot/cold rule (tests/test_prewarm_col_cache.py
+    there: hot iff lookup >= 0) as the kernels apply it: with only the hot
+    blocks in slots and no host copies, a decode over the routing reports an
+    unavailable block exactly when a cold block is routed; with host copies
+    the cold blocks are read from them and the output equals the all-resident
+    decode bit for bit."""
+    from next_step_ai_amd.synth import make_synthetic_layer
+
+    for case in _fixture()["hot_cold_partition"]["cases"]:
+        NB = case["total_blocks"]
+        L = make_synthetic_layer(H=2048, I=32 * NB, R=8, seed=71, device=gpu)
+        full = L.slot_table()
+        routing = torch.tensor(case["routing"], dtype=torch.int32)
+        hot = torch.tensor(case["hot_blocks"], dtype=torch.long)
+        y_full = full.decode(L.x, routing)
+        t_no_host = L.slot_table(resident_blocks=hot)
+        lookup = t_no_host.lookup_cpu()
+        cold = [int(b) for b in case["routing"] if int(lookup[b]) < 0]
+        assert cold == case["expected_cold"]
+        if cold:
+            with pytest.raises(RuntimeError, match="neither in an HBM slot nor host-copied"):
+                t_no_host.decode(L.x, routing, check=True)
+        else:
+            assert torch.equal(t_no_host.decode(L.x, routing, check=True), y_full)
+        t_host = L.slot_table(resident_blocks=hot, host_copy=True)
+        y_host = t_host.decode(L.x, routing, check=True)
+        torch.cuda.synchronize()
+        assert torch.equal(y_host, y_full)

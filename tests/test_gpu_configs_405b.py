@@ -1,0 +1,149 @@
+"""The partial-residency decode (405B shape, 832 of 1664 blocks in HBM slots,
+62 of the 208 selected blocks read from pinned host copies) and the
+126-layer 405B stack, at their benchmark workloads.
+
+Bars: the routed blocks bit-exact with the oracle and the MLP output within
+the decode bars (tests/test_gpu_decode.py); the partial table's decode,
+prefill and dense-guard outputs bit-identical to the all-resident table's
+(the host copies hold the same bytes, read over the host link: RT:3885-4207,
+RT:4530-4578); after promoting the misses into slots, the decode again
+bit-identical; the stack's captured-graph tokens bit-identical to eager
+launches (RT:7612-7795)."""
+import gc
+
+import numpy as np
+import pytest
+import torch
+
+from test_gpu_decode import _check_tolerance, _np, _oracle_for_layer, _u16
+
+pytestmark = pytest.mark.gpu
+
+H, I, R, K = 16384, 53248, 64, 208
+NB = I // 32
+RESIDENT, MISSES = 832, 62
+
+
+def _free():
+    gc.collect()
+    torch.cuda.synchronize()
+    torch.cuda.empty_cache()
+
+
+def test_partial_residency_405b(gpu, orc):
+    from next_step_ai_amd.slot_table import HotBlockCache, SparseMlpLayer
+    from next_step_ai_amd.synth import make_synthetic_layer, sub_seed, synth_normal_f16
+
+    print("[config 3] 405B layer, 832 resident, 62 host misses", flush=True)
+    L = make_synthetic_layer(H=H, I=I, R=R, seed=3000, device=gpu, double_quant=True)
+    full = L.layer(K)
+    y_full, sel = full.forward(L.x)
+    y_full, sel = y_full.clone(), sel.clone()
+    sel_np = _np(sel).astype(np.int64)
+    _, _, sel_o = orc.route(_u16(L.x), _u16(L.enc_w), _u16(L.enc_b), _u16(L.score_w), _u16(L.score_b), K)
+    assert np.array_equal(sel_np, np.sort(sel_o))
+    ye, yf, _ = _oracle_for_layer(orc, L, sel_np)
+    _check_tolerance(orc, _np(y_full).astype(np.float64), ye, yf, "config 3 all resident")
+
+    rng = np.random.default_rng(3000)
+    hit = sel_np[rng.permutation(K)[: K - MISSES]]
+    others = np.setdiff1d(np.arange(NB), sel_np)
+    resident = np.concatenate([hit, rng.choice(others, size=RESIDENT - hit.size, replace=False)])
+    table = L.slot_table(resident_blocks=torch.from_numpy(resident), host_copy=True)
+    lookup = table.lookup_cpu()
+    assert int((lookup[torch.from_numpy(sel_np)] < 0).sum()) == MISSES
+    part = SparseMlpLayer(L.router(), table, K, check_blocks=True)
+    y_part, sel_p = part.forward(L.x)
+    part.check_status()
+    assert torch.equal(sel_p, sel) and torch.equal(y_part, y_full)
+    print("[config 3] decode with 62 host misses bit-identical", flush=True)
+
+    # prefill and dense guard through the same table (grouped down at 4
+    # tokens, the dense down over the scattered act at 16) and the all-resident one
+    full_table = full.table
+    xs = synth_normal_f16(sub_seed(3001, "x"), (16, H), 1.0, gpu)
+    for M in (4, 16):
+        sel_m = full.router.route(xs[:M], K)
+        a = full_table.prefill(xs[:M], sel_m)
+        b = table.prefill(xs[:M], sel_m, check=True)
+        torch.cuda.synchronize()
+        assert torch.equal(a, b), f"prefill M={M}"
+    a = full_table.dense_mlp(xs[:8])
+    b = table.dense_mlp(xs[:8], check=True)
+    torch.cuda.synchronize()
+    assert torch.equal(a, b), "dense guard"
+    print("[config 3] prefill and dense guard with host-resident blocks bit-identical", flush=True)
+
+    # promote the token's misses into slots (fixed capacity: evictions), decode again
+    cache = HotBlockCache(table)
+    slots = cache.promote(sel, return_slots=True)
+    torch.cuda.synchronize()
+    assert int((slots >= 0).sum()) == MISSES
+    assert int((table.lookup_cpu()[torch.from_numpy(sel_np)] < 0).sum()) == 0
+    y_prom, sel_q = SparseMlpLayer(L.router(), table, K).forward(L.x)
+    torch.cuda.synchronize()
+    assert torch.equal(sel_q, sel) and torch.equal(y_prom, y_full)
+    del L, full, full_table, table, part, cache
+    _free()
+
+
+def test_stack_126_layers_405b(gpu, orc):
+    """The 126-layer 405B stack as the benchmark builds it (double-quantised
+    absmax, fused residual add): two tokens through eager launches and the
+    captured StackGraph, bit-identical in every layer's selection and the
+    final hidden state; token 0 of layer 0 against the oracle."""
+    from next_step_ai_amd._runtime import workspace
+    from next_step_ai_amd.decode_graph import StackGraph
+    from next_step_ai_amd.slot_table import SparseMlpLayer
+    from next_step_ai_amd.synth import make_synthetic_layer, sub_seed, synth_normal_f16
+
+    n_layers = 126
+    mlps, L0 = [], None
+    for l in range(n_layers):
+        keep = l == 0  # the oracle needs layer 0's reference layout and fp32 absmax
+        L = make_synthetic_layer(H=H, I=I, R=R, seed=5000 + l, device=gpu, double_quant=True, keep_f32_absmax=keep)
+        mlps.append(SparseMlpLayer(L.router(), L.slot_table(drop_reference_down=not keep), K))
+        if keep:
+            L0 = L
+        del L
+        if (l + 1) % 21 == 0:
+            torch.cuda.synchronize()
+            print(f"[config 5] {l + 1}/{n_layers} layers ({torch.cuda.memory_allocated(gpu) / 2**30:.1f} GiB)",
+                  flush=True)
+    tokens = [synth_normal_f16(sub_seed(5000 + t, "x"), (H,), 1.0, gpu) for t in range(2)]
+    ws = workspace(mlps[0].workspace_bytes(), gpu)
+    eager = []
+    for t, x0 in enumerate(tokens):
+        x = x0.clone()
+        sels = []
+        for i, m in enumerate(mlps):
+            y = torch.empty_like(x)
+            _, s = m.forward(x, out=y, ws=ws, residual=x)
+            sels.append(s.clone())
+            if t == 0 and i == 0:
+                mlp0, sel0 = m.forward(x0)  # layer 0 without the add, for the oracle
+                mlp0, sel0 = mlp0.clone(), sel0.clone()
+                torch.cuda.synchronize()
+                assert torch.equal(y, (x0 + mlp0)), "fused add of layer 0"
+            x = y
+        torch.cuda.synchronize()
+        eager.append((x, sels))
+    print("[config 5] eager tokens done", flush=True)
+    g = StackGraph(mlps)
+    for t, x0 in enumerate(tokens):
+        out = g.run(x0)
+        torch.cuda.synchronize()
+        x_ref, sels_ref = eager[t]
+        for i in range(n_layers):
+            assert torch.equal(g.sels[i], sels_ref[i]), f"token {t} layer {i}: selection"
+        assert torch.equal(out, x_ref), f"token {t}: final hidden state"
+    print("[config 5] graph replays bit-identical", flush=True)
+
+    sel_np = _np(sel0).astype(np.int64)
+    _, _, sel_o = orc.route(_u16(tokens[0]), _u16(L0.enc_w), _u16(L0.enc_b), _u16(L0.score_w), _u16(L0.score_b), K)
+    assert np.array_equal(sel_np, np.sort(sel_o))
+    L0.x = tokens[0]
+    ye, yf, _ = _oracle_for_layer(orc, L0, sel_np)
+    _check_tolerance(orc, _np(mlp0).astype(np.float64), ye, yf, "config 5 layer 0 token 0")
+    del mlps, g, L0, eager
+    _free()

@@ -186,3 +186,33 @@ def test_route_tiled_latent_large_terms_exact(gpu, orc):
         lat_o, sc_o, sel_o = orc.route(x16[t], w16, enc_b, swt, sb, k)
         assert np.array_equal(lat[t], lat_o), f"latent of row {t}"
         assert np.array_equal(sc[t], sc_o) and np.array_equal(sel[t], sel_o)
+
+
+def test_route_tiled_latent_one_large_output_exact(gpu, orc):
+    """Only one output of a tile (latent row 3, token 5: not the tile's first
+    lane) has terms of 65504^2 that pass 2^42 before they cancel; every other
+    output stays small.  The whole tile must take the three-part sums, so
+    that output's latent equals the oracle's."""
+    H, R, N, NB, k = 4096, 8, 8, 40, 5
+    big = np.float16(65504.0)
+    rng = np.random.default_rng(29)
+    x = (rng.standard_normal((N, H)) * 0.5).astype(np.float16)
+    w = (rng.standard_normal((R, H)) * 0.02).astype(np.float16)
+    x[5, :1280] = big
+    w[3, :1280] = big
+    x[5, 1536:2816] = big
+    w[3, 1536:2816] = -big
+    # the rest of that output's sixth 256-column wave span is zero, so the
+    # span's two-part sum is 0.5 + 2^-11 (an odd multiple of 2^-11), which a
+    # running sum above 2^42 (spacing 2^-10) would round: 0.9697 instead of 0.97
+    x[5, 1281:1536] = 0
+    x[5, 1280] = np.float16(1.0)
+    w[3, 1280] = np.float16(0.5 + 2.0 ** -11)
+    x16, w16 = x.view(np.uint16), w.view(np.uint16)
+    enc_b = np.zeros(R, dtype=np.uint16)
+    swt, sb = _rand16(rng, (NB, R), 0.02), _rand16(rng, NB, 0.02)
+    sel, lat, sc = _route_gpu(gpu, x16, w16, enc_b, swt, sb, k)
+    for t in range(N):
+        lat_o, sc_o, sel_o = orc.route(x16[t], w16, enc_b, swt, sb, k)
+        assert np.array_equal(lat[t], lat_o), f"latent of row {t}"
+        assert np.array_equal(sc[t], sc_o) and np.array_equal(sel[t], sel_o)

@@ -2,9 +2,11 @@
 oracle's quantiser checked against brute force and the mathematics, and the
 package's dynamic map against the oracle's.
 
-Parity at the bitsandbytes boundary itself (bitsandbytes==0.49.1, absent
-here) is unpinned: the map and the quantiser are restated from the published
-construction; the decode only consumes (q, absmax2, code2, offset) as data."""
+The dynamic map is pinned against bitsandbytes' published construction run
+with torch fp32 here.  The quantiser's nearest-code ties and the offset's
+last bit (bitsandbytes takes a torch fp32 mean on the weight's device) stay
+unpinned (bitsandbytes==0.49.1 is absent); the decode only consumes
+(q, absmax2, code2, offset) as data."""
 import numpy as np
 
 
@@ -12,6 +14,47 @@ def _nearest_brute(m, v):
     """Index of the nearest map entry to each v (fp32 distances, ties to the lower index)."""
     d = np.abs(m[None, :].astype(np.float32) - v[:, None].astype(np.float32))
     return np.argmin(d, axis=1)  # argmin returns the first minimum
+
+
+def _published_map_torch():
+    """bitsandbytes' create_dynamic_map(signed=True, max_exponent_bits=7,
+    total_bits=8) as published, executed with torch fp32 on the CPU: 7 - 7
+    non-sign bits left over means no additional items; level i has 2^i + 1
+    boundaries linspace(0.1, 1), their means scaled by 10^(i - 6), both
+    signs; 0 and 1 appended; sorted."""
+    import torch
+
+    data = []
+    for i in range(7):
+        boundaries = torch.linspace(0.1, 1, 2 ** i + 1)
+        means = (boundaries[:-1] + boundaries[1:]) / 2.0
+        data += ((10 ** (-6 + i)) * means).tolist()
+        data += (-(10 ** (-6 + i)) * means).tolist()
+    data.append(0)
+    data.append(1.0)
+    assert len(data) == 256
+    data.sort()
+    return torch.Tensor(data).numpy()
+
+
+def test_oracle_dynamic_map_equals_published_construction(orc):
+    """The oracle's C restatement (fp32 linspace points as single-rounding
+    fmas) equals the published construction run by torch, bit for bit; the
+    same map with the boundaries computed in double and rounded once (a
+    plausible restatement) differs in 22 entries, so the check has teeth."""
+    pub = _published_map_torch()
+    assert pub.dtype == np.float32
+    assert np.array_equal(orc.dynamic_map_signed().view(np.uint32), pub.view(np.uint32))
+    vals = []
+    for i in range(7):
+        n = (1 << i) + 1
+        b = [np.float32(0.1 + 0.9 * j / (n - 1)) for j in range(n)]
+        for j in range(n - 1):
+            m = np.float32(np.float32(b[j] + b[j + 1]) / np.float32(2.0))
+            vals += [np.float32(np.float32(10.0 ** (i - 6)) * m), np.float32(-np.float32(10.0 ** (i - 6)) * m)]
+    vals += [np.float32(0.0), np.float32(1.0)]
+    in_double = np.sort(np.array(vals, dtype=np.float32))
+    assert np.count_nonzero(in_double.view(np.uint32) != pub.view(np.uint32)) == 22
 
 
 def test_package_dynamic_map_equals_oracle(orc):

@@ -1,5 +1,7 @@
-"""The oracle and the package's host-side slot-table logic against the
-expectations the reference's own tests assert (tests/golden fixture)."""
+"""The oracle and the package's host-side layout logic against the
+expectations the reference's own tests assert (tests/golden fixture).  The
+device slot plan and the hot/cold rule are checked against the same fixture
+in tests/test_gpu_cache.py."""
 import json
 import os
 
@@ -28,18 +30,6 @@ def test_fixed_capacity_plan_oracle(orc):
                                                         c["active_count"], c["capacity"], c["novel_blocks"]))
 
 
-def test_fixed_capacity_plan_package():
-    from next_step_ai_amd.slot_table import plan_fixed_capacity_bank_update
-
-    c = _fix()["plan_fixed_capacity_bank_update"]
-    slots, ids, scores, active = plan_fixed_capacity_bank_update(
-        existing_block_ids_cpu=torch.tensor(c["existing_block_ids"], dtype=torch.long),
-        existing_scores_cpu=torch.tensor(c["existing_scores"], dtype=torch.float32),
-        active_count=c["active_count"], capacity=c["capacity"],
-        novel_blocks_cpu=torch.tensor(c["novel_blocks"], dtype=torch.long))
-    _check_plan(c, slots.tolist(), ids.tolist(), scores, active)
-
-
 def test_down_column_gather_oracle(orc):
     c = _fix()["down_column_gather"]
     p, a = orc.gather_down_columns(np.array(c["packed"], dtype=np.uint8), np.array(c["absmax"], dtype=np.float32),
@@ -48,24 +38,6 @@ def test_down_column_gather_oracle(orc):
     assert a.shape == (c["h_out"], len(c["blocks"])) and a.dtype == np.float32
     assert p.tolist() == c["expected_packed"]
     assert a.tolist() == c["expected_absmax"]
-
-
-def test_hot_cold_partition_package():
-    from next_step_ai_amd.slot_table import partition_cached_block_lookup
-
-    for case in _fix()["hot_cold_partition"]["cases"]:
-        lookup = torch.full((case["total_blocks"],), -1, dtype=torch.int32)
-        hot = torch.tensor(case["hot_blocks"], dtype=torch.long)
-        if hot.numel():
-            lookup[hot] = torch.arange(hot.numel(), dtype=torch.int32)
-        routing = torch.tensor(case["routing"], dtype=torch.long)
-        pos, slots, cold, cold_mask = partition_cached_block_lookup(lookup.index_select(0, routing),
-                                                                    ordered_blocks=routing)
-        assert cold.tolist() == case["expected_cold"]
-        n_hot = len(case["routing"]) - len(case["expected_cold"])
-        assert (0 if pos is None else int(pos.numel())) == n_hot
-        if slots is not None:
-            assert all(int(lookup[routing[int(p)]]) == int(s) for p, s in zip(pos, slots))
 
 
 def test_active_layout_oracle_and_package(orc):
