@@ -77,6 +77,11 @@ WORKLOADS = {
 }
 STACK_LAYERS = 126
 STACK_TOKENS = 64
+# gate/up weights of the stack: N(0, 0.002), so that x <- x + mlp(x) stays
+# finite over 126 layers with no norm in between (the MLP's gain grows with
+# |x|^2; at 0.02 the hidden state overflows within a few layers); down and
+# router N(0, 0.02); the bytes moved are the same
+STACK_GATE_UP_STD = 0.002
 C3_RESIDENT, C3_MISSES = 832, 62
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic_sparse_mlp_decode.json")
 
@@ -476,7 +481,7 @@ def run_stack(args) -> int:
     mlps = []
     for l in range(STACK_LAYERS):
         L = make_synthetic_layer(H=H, I=I, R=R, seed=5000 + l, device=device, double_quant=args.absmax == "dq8",
-                                 keep_f32_absmax=args.absmax == "f32")
+                                 keep_f32_absmax=args.absmax == "f32", gate_up_std=STACK_GATE_UP_STD)
         table = L.slot_table(drop_reference_down=True)
         mlps.append(SparseMlpLayer(L.router(), table, k))
         del L
@@ -514,9 +519,10 @@ def run_stack(args) -> int:
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for t in range(STACK_TOKENS):
-        token(tokens[t])
+        last = token(tokens[t])
     torch.cuda.synchronize()
     dt = time.perf_counter() - t0
+    finite = bool(torch.isfinite(last.float()).all())
     tok_s = STACK_TOKENS / dt
     us_layer = dt / (STACK_TOKENS * STACK_LAYERS) * 1e6
     layer_bytes = algorithmic_bytes(H, I, k, qbs, args.absmax) + router_bytes(H, R, I // 32)
@@ -531,6 +537,8 @@ def run_stack(args) -> int:
         "aggregate_hbm_gbs": round(layer_bytes * STACK_TOKENS * STACK_LAYERS / dt / 1e9, 2),
         "algorithmic_bytes_per_layer": layer_bytes,
         "generation_s": round(time.perf_counter() - t_gen - dt, 1),
+        "final_hidden_finite": finite,
+        "gate_up_std": STACK_GATE_UP_STD,
     })
     print(json.dumps(res), flush=True)
     return 0

@@ -118,12 +118,16 @@ class SyntheticLayer:
 
 def make_synthetic_layer(*, H: int, I: int, R: int, seed: int, device: torch.device, qbs: int = 64,
                          std: float = 0.02, double_quant: bool = False, keep_f32_absmax: bool = True,
-                         dq_block: int = 256) -> SyntheticLayer:
+                         dq_block: int = 256, gate_up_std: float | None = None) -> SyntheticLayer:
+    """``gate_up_std`` (default ``std``): the gate/up weights' deviation; a
+    stack of layers chained as x <- x + mlp(x) with no norm in between stays
+    finite when it is small (the MLP's gain grows with |x|^2)."""
     if I % 32 != 0 or (I * H) % qbs != 0:
         raise RuntimeError("I must be a multiple of 32 and I*H a multiple of qbs")
     NB = I // 32
-    gp, ga = synth_nf4(sub_seed(seed, "gate"), I * H, qbs, std, device)
-    upk, ua = synth_nf4(sub_seed(seed, "up"), I * H, qbs, std, device)
+    gu_std = std if gate_up_std is None else float(gate_up_std)
+    gp, ga = synth_nf4(sub_seed(seed, "gate"), I * H, qbs, gu_std, device)
+    upk, ua = synth_nf4(sub_seed(seed, "up"), I * H, qbs, gu_std, device)
     dp, da = synth_nf4(sub_seed(seed, "down"), H * I, qbs, std, device)
     nested = None
     if double_quant:

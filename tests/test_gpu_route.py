@@ -198,6 +198,9 @@ def test_route_tiled_latent_one_large_output_exact(gpu, orc):
     rng = np.random.default_rng(29)
     x = (rng.standard_normal((N, H)) * 0.5).astype(np.float16)
     w = (rng.standard_normal((R, H)) * 0.02).astype(np.float16)
+    for cols in (slice(0, 1280), slice(1536, 2816)):  # only row 3 and token 5 meet the large values
+        x[:, cols] = 0
+        w[:, cols] = 0
     x[5, :1280] = big
     w[3, :1280] = big
     x[5, 1536:2816] = big
