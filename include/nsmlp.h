@@ -193,6 +193,27 @@ int nsmlp_decode_layer_add_f16(const nsmlp_router* router, const nsmlp_slot_tabl
                                const void* residual, int k, int32_t* sel_out, void* out, void* ws, size_t ws_bytes,
                                void* stream);
 
+/* No-allocation variant of nsmlp_decode_layer_f16 / _add_f16 (version >= 103).
+ * No counterpart in the reference: it is for callers that cannot allocate
+ * device memory (code under HIP graph capture, tight serving loops, hosts that
+ * forbid hipMalloc).  It takes no workspace: its scratch is a file-scope
+ * device array of the library, 256 KiB per device (each GPU holds its own
+ * copy until the process ends), whose address is looked up once per device;
+ * it calls no hipMalloc, hipFree or allocating library routine.  Same
+ * kernels and results as nsmlp_decode_layer_f16 (with residual != NULL, as
+ * nsmlp_decode_layer_add_f16), for the streaming shapes: hidden size a
+ * multiple of 2048 up to 16384, num_blocks <= 4096, k <= 2048, and a scratch
+ * need of at most 256 KiB (k up to about 1800); other shapes fail with
+ * NSMLP_EINVAL and a message.  status_out (nullable, device or pinned host
+ * memory, zeroed once by the caller): the call's status word is ORed into it
+ * (see nsmlp_workspace_take_status) and the scratch's word cleared.  Every
+ * call on a device shares that device's scratch, which keeps the last call's
+ * contents: calls that overlap on one GPU (other streams, other threads)
+ * race. */
+int nsmlp_decode_layer_noalloc_f16(const nsmlp_router* router, const nsmlp_slot_table* table, const void* x,
+                                   const void* residual, int k, int32_t* sel_out, void* out, int32_t* status_out,
+                                   void* stream);
+
 /* --------------------------------------- reference-signature entry points
  * Replaces TSM:1378-1509 (triton_sparse_mlp_decode_4bit_single_kernel_sm75):
  * x [H] fp16; gathered gate/up packed [top_k][32][H/2] u8 with absmax

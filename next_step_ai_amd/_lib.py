@@ -94,6 +94,8 @@ SIGNATURES: dict[str, tuple] = {
     "nsmlp_decode_layer_f16": (I32, [ctypes.POINTER(Router), ctypes.POINTER(SlotTable), P, I32, P, P, P, SZ, P]),
     "nsmlp_decode_layer_add_f16": (I32, [ctypes.POINTER(Router), ctypes.POINTER(SlotTable), P, P, I32, P, P, P, SZ,
                                          P]),
+    "nsmlp_decode_layer_noalloc_f16": (I32, [ctypes.POINTER(Router), ctypes.POINTER(SlotTable), P, P, I32, P, P, P,
+                                             P]),
     "nsmlp_prefill_workspace_bytes": (SZ, [I32, I32, I32, I32]),
     "nsmlp_prefill_slots_f16": (I32, [ctypes.POINTER(SlotTable), P, I32, P, I32, P, P, SZ, P]),
     "nsmlp_dense_mlp_workspace_bytes": (SZ, [I32, I32, I32]),

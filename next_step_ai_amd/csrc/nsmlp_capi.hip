@@ -362,6 +362,43 @@ int gather_down_impl(const uint8_t* src_packed, const AbsT* src_absmax, const in
 }  // namespace
 }  // namespace nsmlp
 
+// ------------------------------------------------ no-allocation decode layer
+// The scratch of nsmlp_decode_layer_noalloc_f16: one array per device (each
+// GPU holds its own copy), used through the address hipGetSymbolAddress
+// gives for it on that device, never through its name in host code.
+constexpr size_t kScratchBytes = (size_t)256 << 10;
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+namespace nsmlp {
+namespace {
+
+std::mutex g_scratch_mu;
+char* g_scratch_ptr[256] = {nullptr};
+
+// The calling thread's current device's scratch; on the first call for a
+// device its address is looked up (with that device current) and its status
+// word cleared by a fill kernel on `s` (no memset).
+int device_scratch(hipStream_t s, char** out) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 256) return set_error(NSMLP_ENODEV, "no HIP device");
+  std::lock_guard<std::mutex> lk(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || p == nullptr)
+      return set_error(NSMLP_EHIP, "scratch address on device %d: %s", dev, hipGetErrorString(e));
+    launch_zero_u32((uint32_t*)p, (long long)(kAlign / 4), s);
+    const int rc = check_launch("scratch status clear");
+    if (rc) return rc;
+    g_scratch_ptr[dev] = (char*)p;
+  }
+  *out = g_scratch_ptr[dev];
+  return NSMLP_OK;
+}
+
+}  // namespace
+}  // namespace nsmlp
+
 extern "C" {
 
 const char* nsmlp_last_error(void) { return g_err; }
@@ -498,6 +535,77 @@ int nsmlp_decode_layer_add_f16(const nsmlp_router* router, const nsmlp_slot_tabl
                                void* stream) {
   if (residual == nullptr) return set_error(NSMLP_EINVAL, "residual must be non-NULL");
   return decode_layer(router, table, x, residual, k, sel_out, out, ws, ws_bytes, stream);
+}
+
+int nsmlp_decode_layer_noalloc_f16(const nsmlp_router* router, const nsmlp_slot_table* table, const void* x,
+                                   const void* residual, int k, int32_t* sel_out, void* out, int32_t* status_out,
+                                   void* stream) {
+  if (router == nullptr) return set_error(NSMLP_EINVAL, "router is NULL");
+  DecodeArgs a;
+  int rc = table_to_args(table, a);
+  if (rc) return rc;
+  rc = validate_decode_shape(a.H, a.qbs, k);
+  if (rc) return rc;
+  rc = validate_route(1, a.H, router->R, router->NB, k, router->flags);
+  if (rc) return rc;
+  if (router->NB != a.NB)
+    return set_error(NSMLP_EINVAL, "router num_blocks %d != intermediate blocks %d", router->NB, a.NB);
+  if (!x || !out || !router->enc_w || !router->score_w)
+    return set_error(NSMLP_EINVAL, "x, out, enc_w and score_w must be non-NULL");
+  if (!aligned16(x)) return set_error(NSMLP_EINVAL, "x must be 16-byte aligned");
+  a.x = (const uint16_t*)x;
+  a.k = k;
+  a.out = (uint16_t*)out;
+  a.residual = (const uint16_t*)residual;
+  fill_decode_tiling(a);
+  if (a.st_gu_wgs <= 0 || !streaming_can_select(a.NB, k))
+    return set_error(NSMLP_EINVAL,
+                     "no-allocation decode covers the streaming kernels only: hidden size a multiple of 2048 up to "
+                     "16384, num_blocks <= 4096, k <= 2048 (got H=%d, num_blocks=%d, k=%d)",
+                     a.H, a.NB, k);
+  // scratch layout: status word, the gate/up kernel's activations and block
+  // references, the down partials (more than one block group), latent, scores
+  size_t off = kAlign;
+  const size_t o_act = off;
+  off += align_up((size_t)k * 32 * sizeof(float));
+  const size_t o_enc = off;
+  off += align_up((size_t)k * sizeof(uint32_t));
+  const size_t o_bid = off;
+  off += align_up((size_t)k * sizeof(int32_t));
+  const size_t o_part = off;
+  if (a.st_dn_gx > 1) off += align_up((size_t)a.st_dn_gx * a.H * sizeof(float));
+  const size_t o_route = off;
+  off = route_ws_layout(o_route, 1, a.H, router->R, router->NB).total;
+  if (off > kScratchBytes)
+    return set_error(NSMLP_EINVAL, "no-allocation decode needs %zu bytes of scratch for H=%d, k=%d, num_blocks=%d; "
+                     "the per-device scratch holds %zu (use nsmlp_decode_layer_f16 with a workspace)",
+                     off, a.H, k, a.NB, kScratchBytes);
+  hipStream_t s = (hipStream_t)stream;
+  char* base = nullptr;
+  rc = device_scratch(s, &base);
+  if (rc) return rc;
+  a.status = (int*)base;
+  a.st_act = (float*)(base + o_act);
+  a.st_enc = (uint32_t*)(base + o_enc);
+  a.st_bid = (int32_t*)(base + o_bid);
+  a.outpart = (float*)(base + o_part);
+  RouteArgs r;
+  fill_route(r, x, 1, a.H, router->enc_w, router->enc_b, router->R, router->basis_top_k, router->score_w,
+             router->score_b, router->down_block_norm, router->NB, router->flags & NSMLP_ROUTE_LEGACY_ABS, k, nullptr,
+             nullptr, nullptr, base, o_route);
+  launch_route_scores(r, s);
+  rc = check_launch("route");
+  if (rc) return rc;
+  a.sel = nullptr;
+  a.sel_scores = r.scores;
+  a.sel_out = sel_out;
+  rc = run_decode(a, s);
+  if (rc) return rc;
+  if (status_out != nullptr) {
+    launch_take_status(a.status, status_out, s);
+    rc = check_launch("take status");
+  }
+  return rc;
 }
 
 static int dense_guard_splits(int H, int NB, int M) {
