@@ -45,17 +45,31 @@ __device__ __forceinline__ void cpair_fill(uint32_t* cpair, const float* code, i
     cpair[e] = (uint32_t)f2h(code[e >> 4]) | ((uint32_t)f2h(code[e & 15]) << 16);
 }
 
-// 8 consecutive NF4 elements (4 bytes, even element in the high nibble) as
-// fp16(code * absmax), the reference fallback's rounding of the weights.
-__device__ __forceinline__ half8_t deq8(uint32_t word, float am, const float* code) {
-  half8_t h;
+// fp32 code pairs per packed byte: entry e = (code[e >> 4], code[e & 15]),
+// the (even, odd) elements of byte e.
+__device__ __forceinline__ void fpair_fill(float2* cp, const float* code, int tid, int nthr) {
+  for (int e = tid; e < 256; e += nthr) cp[e] = make_float2(code[e >> 4], code[e & 15]);
+}
+
+// 16 consecutive NF4 elements of two rows (words w0, w1: 4 bytes each, even
+// element in the high nibble) as fp16(code * absmax), the reference
+// fallback's rounding of the weights.  All eight pair lookups go out before
+// any is used.
+__device__ __forceinline__ void deq8x2(uint32_t w0, float am0, uint32_t w1, float am1, const float2* cp,
+                                       half8_t& h0, half8_t& h1) {
+  float2 p[8];
 #pragma unroll
   for (int m = 0; m < 4; ++m) {
-    const uint32_t byte = (word >> (8 * m)) & 0xFFu;
-    h[2 * m] = (_Float16)(code[byte >> 4] * am);
-    h[2 * m + 1] = (_Float16)(code[byte & 15u] * am);
+    p[m] = cp[(w0 >> (8 * m)) & 0xFFu];
+    p[4 + m] = cp[(w1 >> (8 * m)) & 0xFFu];
   }
-  return h;
+#pragma unroll
+  for (int m = 0; m < 4; ++m) {
+    h0[2 * m] = (_Float16)(p[m].x * am0);
+    h0[2 * m + 1] = (_Float16)(p[m].y * am0);
+    h1[2 * m] = (_Float16)(p[4 + m].x * am1);
+    h1[2 * m + 1] = (_Float16)(p[4 + m].y * am1);
+  }
 }
 
 // 8 consecutive NF4 elements (4 bytes, even element in the high nibble) as
@@ -186,7 +200,7 @@ __global__ void __launch_bounds__(kPfThreads, 4) k_pf_gu(PrefillArgs p) {  // 4 
   __shared__ __attribute__((aligned(16))) uint8_t xs[2][kGuTok * kXRow];  // token rows, fp16
   __shared__ __attribute__((aligned(16))) uint8_t wsr[2][64 * kWRow];     // NF4 rows (gate 0-31, up 32-63)
   __shared__ float ams[2][64][8];                                          // absmax per row and 16 columns
-  __shared__ float code_s[16];
+  __shared__ float2 cpair_s[256];
   __shared__ float c2_s[2][256];
   const DecodeArgs& d = p.d;
   const int b = blockIdx.x;
@@ -194,7 +208,7 @@ __global__ void __launch_bounds__(kPfThreads, 4) k_pf_gu(PrefillArgs p) {  // 4 
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int beg = p.offsets[b], cnt = p.offsets[b + 1] - beg;
   if (cnt == 0) return;
-  if (tid < 16) code_s[tid] = d.code[tid];
+  fpair_fill(cpair_s, d.code, tid, kPfThreads);
   if constexpr (DQ) c2_s[tid >> 8][tid & 255] = (tid < 256 ? d.gate.code2 : d.up.code2)[tid & 255];
   const BlockRef br = resolve_id(d, b);
   if (!br.ok && tid == 0) atomicOr(d.status, 1);
@@ -286,11 +300,11 @@ __global__ void __launch_bounds__(kPfThreads, 4) k_pf_gu(PrefillArgs p) {  // 4 
     // other buffer; unrolled by two so the register stages are named
     auto step = [&](int c, int bi, GuRegs& Rn) {
       half8_t bf[2];
-#pragma unroll
-      for (int q = 0; q < 2; ++q) {
-        const int row = proj * 32 + q * 16 + j;
-        const uint32_t word = *reinterpret_cast<const uint32_t*>(&wsr[bi][row * kWRow + 16 * s + 4 * g]);
-        bf[q] = deq8(word, ams[bi][row][2 * s + (g >> 1)], code_s);
+      {
+        const int r0 = proj * 32 + j, r1 = r0 + 16;
+        const uint32_t w0 = *reinterpret_cast<const uint32_t*>(&wsr[bi][r0 * kWRow + 16 * s + 4 * g]);
+        const uint32_t w1 = *reinterpret_cast<const uint32_t*>(&wsr[bi][r1 * kWRow + 16 * s + 4 * g]);
+        deq8x2(w0, ams[bi][r0][2 * s + (g >> 1)], w1, ams[bi][r1][2 * s + (g >> 1)], cpair_s, bf[0], bf[1]);
       }
 #pragma unroll
       for (int tt = 0; tt < kGuTiles; ++tt) {
