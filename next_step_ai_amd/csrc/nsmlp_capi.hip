@@ -66,7 +66,7 @@ int ensure_midpoints() {
 // Columns per gate/up split: the largest of {2048, 1024, 512, 256} dividing
 // H that still gives >= 1024 workgroups (k * H / cs), else 256.
 int choose_cs(int H, int k) {
-  int forced = env_int("NSMLP_GU_COLS", 0);
+  static const int forced = env_int("NSMLP_GU_COLS", 0);  // measurement switch, read once
   if (forced == 256 || forced == 512 || forced == 1024 || forced == 2048)
     if (H % forced == 0) return forced;
   const int cands[4] = {2048, 1024, 512, 256};
@@ -80,7 +80,7 @@ int choose_cs(int H, int k) {
 int choose_groups(int H, int k) {
   int chunks = (H + kRowsPerChunk - 1) / kRowsPerChunk;
   int g = (1024 + chunks - 1) / chunks;
-  int forced = env_int("NSMLP_DOWN_GROUPS", 0);
+  static const int forced = env_int("NSMLP_DOWN_GROUPS", 0);  // measurement switch, read once
   if (forced > 0) g = forced;
   int cap = k < kMaxGroups ? k : kMaxGroups;
   if (g < 1) g = 1;
@@ -183,7 +183,8 @@ void fill_decode_tiling(DecodeArgs& a) {
   a.rows_per_chunk = kRowsPerChunk;
   a.chunks = (a.H + kRowsPerChunk - 1) / kRowsPerChunk;
   a.st_gu_wgs = 0;
-  if (env_int("NSMLP_DECODE_SPLIT", 0) == 0) plan_streaming(a, device_cus());
+  static const int generic_only = env_int("NSMLP_DECODE_SPLIT", 0);  // measurement switch, read once
+  if (generic_only == 0) plan_streaming(a, device_cus());
 }
 
 int run_decode(const DecodeArgs& a, hipStream_t s) {

@@ -326,6 +326,7 @@ __global__ void __launch_bounds__(kPfThreads, 4) k_pf_gu(PrefillArgs p) {  // 4 
     }
     // step partials summed in step order into [kGuTok tok][64 rows] fp32
     // (rows: gate 0-31, up 32-63), reusing the token staging buffer
+    mfma_drain();
     float* cs = reinterpret_cast<float*>(&xs[0][0]);
     for (int ss = 0; ss < 4; ++ss) {
       if (s == ss) {

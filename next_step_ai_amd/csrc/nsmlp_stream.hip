@@ -762,7 +762,7 @@ bool plan_streaming(DecodeArgs& a, int cus) {
   const int NS = kWaves / S;
   // gate/up: rounds of NS items per workgroup, balanced over the workgroups
   const long long items = 16LL * a.k;
-  const int gu_per_cu = env_or("NSMLP_GU_WGS_PER_CU", 1) > 1 ? 2 : 1;
+  static const int gu_per_cu = env_or("NSMLP_GU_WGS_PER_CU", 1) > 1 ? 2 : 1;  // measurement switch, read once
   const long long per_round = (long long)cus * gu_per_cu * NS;
   const long long R = (items + per_round - 1) / per_round;
   if (R > kMaxItems) return false;
@@ -770,7 +770,7 @@ bool plan_streaming(DecodeArgs& a, int cus) {
   // down: 64-row chunks x GX block groups, at least one workgroup per CU
   const long long chunks = a.H / kWave;
   long long GX = (cus + chunks - 1) / chunks;
-  const long long forced = env_or("NSMLP_DOWN_GX", 0);
+  static const long long forced = env_or("NSMLP_DOWN_GX", 0);  // measurement switch, read once
   if (forced > 0) GX = forced;
   if (GX > a.k) GX = a.k;
   if (GX > 64) GX = 64;

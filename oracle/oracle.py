@@ -277,6 +277,19 @@ def gather_down_columns(packed_flat, absmax_flat, blocks, out_features, in_featu
     return packed, absmax
 
 
+def partition_by_lookup(lookup, selected):
+    """The hot/cold split of a selection (RT:3588-3604): a selected block is hot
+    when its slot lookup is >= 0.  Returns (positions of the hot entries in
+    the selection, their slots, the cold block ids in selection order, the
+    cold mask)."""
+    lk = np.asarray(lookup, dtype=np.int64)
+    sel = np.asarray(selected, dtype=np.int64)
+    slot = lk[sel]
+    hot = slot >= 0
+    pos = np.flatnonzero(hot)
+    return pos, slot[pos], sel[~hot], ~hot
+
+
 def plan_fixed_capacity_bank_update(existing_block_ids, existing_scores, active_count, capacity, novel_blocks):
     """Restates _plan_fixed_capacity_bank_update (RT:2576-2617): fill free slots
     first, then replace the lowest-score slot; a new block's score is

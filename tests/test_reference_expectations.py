@@ -68,3 +68,17 @@ def test_active_layout_oracle_and_package(orc):
         assert po.tolist() == ordered.tolist()
         assert pl.numpy().tolist() == local.tolist()
         assert np.array_equal(pm.numpy(), mask)
+
+
+def test_hot_cold_partition_oracle(orc):
+    """The oracle's hot/cold split against the reference tests' cases: hot iff
+    the lookup is >= 0 (slot 0 is hot: a `> 0` rule fails the first case)."""
+    for case in _fix()["hot_cold_partition"]["cases"]:
+        lookup = -np.ones(case["total_blocks"], dtype=np.int64)
+        for slot, b in enumerate(case["hot_blocks"]):
+            lookup[b] = slot
+        pos, slots, cold, cold_mask = orc.partition_by_lookup(lookup, case["routing"])
+        assert cold.tolist() == case["expected_cold"]
+        assert [int(case["routing"][p]) for p in pos] == [b for b in case["routing"] if b not in case["expected_cold"]]
+        assert [int(s) for s in slots] == [int(lookup[case["routing"][p]]) for p in pos]
+        assert int(cold_mask.sum()) == len(case["expected_cold"])
