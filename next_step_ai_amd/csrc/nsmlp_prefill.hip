@@ -26,6 +26,7 @@
 // chunk's four MFMA steps) so that each lane reads contiguous bytes; A and B
 // use the same permutation, which leaves the dot products unchanged.
 #include <cstring>
+#include <mutex>
 
 #include "nsmlp_internal.h"
 
@@ -169,47 +170,81 @@ __global__ void __launch_bounds__(256) k_pf_list(PrefillArgs p) {
 }
 
 // Gate/up of one block for all its tokens, as a staged GEMM.  A pass takes
-// up to kGuTok tokens (tiles of 16); K goes in 128-column chunks.  Per chunk
-// the 512 threads load the pass's token rows (16 B pieces, 256 B per row),
-// the block's 64 NF4 rows (8 B pieces, 64 B per row) and their absmax with
-// coalesced loads two chunks ahead, and stage them in LDS (the absmax
-// resolved to fp32 per row and 64 columns).  Wave w takes MFMA step
-// s = w % 4 of every chunk (columns 32 s .. 32 s + 31) for projection
-// w / 4 (gate or up, 2 N-tiles of 16 rows): it decodes its B fragments once
-// per chunk to fp16(code * absmax) and multiplies them with every token
-// tile's A fragment.  The four step partials are summed in LDS in step
-// order at the end of the pass; act = fp16(silu(gate) * up).
-constexpr int kGuChunk = 128;             // columns per chunk
-constexpr int kGuTok = 64;                // tokens per pass
+// up to kGuTok tokens (tiles of 16); K goes in 128-column chunks through a
+// ring of kGuNS stages in LDS, filled by buffer loads straight into LDS
+// (no registers), kGuNS - 1 chunks ahead: per chunk each thread issues the
+// same loads (two 16-byte pieces of token rows, two dwords of the block's
+// 64 NF4 rows, its absmax entry), so one s_waitcnt per chunk (the loads of
+// the next kGuNS - 2 chunks may stay in flight) and one barrier hand a chunk
+// to the waves.  Such a load puts lane l's bytes at a fixed LDS slot (16 l or
+// 4 l from the wave's base); each lane picks the piece of global memory for
+// its slot, so the rows are stored XOR-swizzled and the fragment reads below
+// hit distinct banks.  Wave w takes MFMA step s = w % 4 of every chunk
+// (columns 32 s .. 32 s + 31) for projection w / 4 (gate or up, 2 N-tiles of
+// 16 rows): it decodes its B fragments to fp16(code * absmax) and multiplies
+// them with every token tile's A fragment.  The four step partials are
+// summed in LDS in step order at the end of the pass; act = fp16(silu(gate)
+// * up).
+constexpr int kGuChunk = 128;              // columns per chunk
+constexpr int kGuTok = 64;                 // tokens per pass
 constexpr int kGuTiles = kGuTok / 16;      // MFMA token tiles per pass
-constexpr int kXPieces = kGuTok * 16 / kPfThreads;  // 16-byte token-row pieces per thread and chunk
-static_assert(kXPieces >= 1 && kGuTok * 16 == kXPieces * kPfThreads, "token pieces must cover the pass");
-static_assert(kGuTok * 64 * 4 <= kGuTok * (kGuChunk * 2 + 16), "gate/up sums must fit the token buffer");
-constexpr int kXRow = kGuChunk * 2 + 16;  // bytes per staged token row (padded)
-constexpr int kWRow = kGuChunk / 2 + 16;  // bytes per staged NF4 row (padded)
-
-struct GuRegs {
-  uint4 x[kXPieces];  // 16-byte pieces of token rows
-  uint2 w;        // 16 nibbles of one weight row
-  float am;       // fp32 absmax, or the absmax2 (double-quantised)
-  uint32_t qa;    // u8 absmax code (double-quantised)
+constexpr int kGuNS = 3;                   // LDS stages (chunks): 76 KB, two workgroups per CU
+constexpr int kGuXBytes = kGuTok * kGuChunk * 2;   // token rows of a stage: [64][16 pieces of 16 B]
+constexpr int kGuWBytes = 64 * kGuChunk / 2;       // NF4 rows of a stage: [64][16 dwords]
+constexpr int kGuAux = 64 * 8;                     // absmax entries of a stage: [64 rows][8 pieces of 16 columns]
+struct GuLds {
+  uint8_t x[kGuNS][kGuXBytes];
+  uint8_t w[kGuNS][kGuWBytes];
+  uint32_t qa[kGuNS][kGuAux];  // double-quantised: u8 code (low byte); fp32: the absmax bits
+  float a2[kGuNS][kGuAux];     // double-quantised: the entry's absmax2
+  float2 cpair[256];
+  float c2[2][256];
 };
+static_assert(kGuTok * 64 * 4 <= kGuNS * kGuXBytes, "gate/up sums must fit the token stages");
+static_assert(kGuTok * 16 == 2 * kPfThreads && 64 * 16 == 2 * kPfThreads && kGuAux == kPfThreads,
+              "loads per chunk: two token pieces, two weight dwords, one absmax entry per thread");
+
+// Buffer loads into LDS (lane l's bytes at LDS address base + 16 l, or 4 l
+// for the dword and byte forms; the byte form zero-extends to a dword).
+// Written as asm: the compiler then neither counts them in its own wait
+// counts (which only makes those waits longer than needed, never shorter)
+// nor waits for them before every later LDS read; the kernel waits for
+// them itself.  `base` is the wave's LDS byte address (uniform).
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(uintptr_t)p);
+}
+__device__ __forceinline__ void ld_lds16(rsrc_t r, const void* lds, uint32_t voff) {
+  asm volatile("s_mov_b32 m0, %1\n\tbuffer_load_dwordx4 %0, %2, 0 offen lds" ::"v"(voff), "s"(lds_addr(lds)), "s"(r)
+               : "memory", "m0");
+}
+__device__ __forceinline__ void ld_lds4(rsrc_t r, const void* lds, uint32_t voff) {
+  asm volatile("s_mov_b32 m0, %1\n\tbuffer_load_dword %0, %2, 0 offen lds" ::"v"(voff), "s"(lds_addr(lds)), "s"(r)
+               : "memory", "m0");
+}
+__device__ __forceinline__ void ld_lds1(rsrc_t r, const void* lds, uint32_t voff) {
+  asm volatile("s_mov_b32 m0, %1\n\tbuffer_load_ubyte %0, %2, 0 offen lds" ::"v"(voff), "s"(lds_addr(lds)), "s"(r)
+               : "memory", "m0");
+}
+// Workgroup barrier after this wave's LDS accesses (no memory fence: the
+// loads into LDS are waited for explicitly).
+__device__ __forceinline__ void pf_barrier() {
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
 
 template <bool DQ>
 __global__ void __launch_bounds__(kPfThreads, 4) k_pf_gu(PrefillArgs p) {  // 4 waves per SIMD: two workgroups per CU
-  __shared__ __attribute__((aligned(16))) uint8_t xs[2][kGuTok * kXRow];  // token rows, fp16
-  __shared__ __attribute__((aligned(16))) uint8_t wsr[2][64 * kWRow];     // NF4 rows (gate 0-31, up 32-63)
-  __shared__ float ams[2][64][8];                                          // absmax per row and 16 columns
-  __shared__ float2 cpair_s[256];
-  __shared__ float c2_s[2][256];
+  extern __shared__ __attribute__((aligned(16))) uint8_t pf_lds[];
+  GuLds& L = *reinterpret_cast<GuLds*>(pf_lds);
   const DecodeArgs& d = p.d;
   const int b = blockIdx.x;
   const int tid = threadIdx.x, lane = tid & (kWave - 1);
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int beg = p.offsets[b], cnt = p.offsets[b + 1] - beg;
   if (cnt == 0) return;
-  fpair_fill(cpair_s, d.code, tid, kPfThreads);
-  if constexpr (DQ) c2_s[tid >> 8][tid & 255] = (tid < 256 ? d.gate.code2 : d.up.code2)[tid & 255];
+  fpair_fill(L.cpair, d.code, tid, kPfThreads);
+  if constexpr (DQ) L.c2[tid >> 8][tid & 255] = (tid < 256 ? d.gate.code2 : d.up.code2)[tid & 255];
   const BlockRef br = resolve_id(d, b);
   if (!br.ok && tid == 0) atomicOr(d.status, 1);
   const int H = d.H;
@@ -234,10 +269,18 @@ __global__ void __launch_bounds__(kPfThreads, 4) k_pf_gu(PrefillArgs p) {  // 4 
   const rsrc_t rx = make_rsrc(p.x, (int)((long long)p.M * H * 2));
   const rsrc_t rtok = make_rsrc(p.tokens + beg, cnt * 4);
   const int nchunks = H / kGuChunk;
-  // this thread's staged weight row (0..31 gate, 32..63 up) and 16-column piece
-  const int wr = tid >> 3, wpart = tid & 7;
-  const bool wup = wr >= 32;
-  const uint32_t wrow = (uint32_t)(wr & 31);
+  // loads of this thread per chunk (instruction i = 2 wave + h of 16 per
+  // chunk, lane l): token row 4 i + l / 16, LDS slot l % 16 <- global piece
+  // (l % 16) ^ (row % 16); weight row 4 i + l / 16 (gate rows 0-31 from waves
+  // 0-3), LDS dword l % 16 <- global dword (l % 16) ^ 4 ((row / 4) % 4);
+  // absmax entry tid = (row tid / 8, 16-column piece tid % 8)
+  const int xslot = lane & 15;
+  const bool wup = wave >= 4;
+  const uint32_t wdw[2] = {(uint32_t)((lane & 15) ^ (((((8 * wave + 4 * 0 + (lane >> 4)) & 31) >> 2) & 3) << 2)),
+                           (uint32_t)((lane & 15) ^ (((((8 * wave + 4 * 1 + (lane >> 4)) & 31) >> 2) & 3) << 2))};
+  const uint32_t wrow_b[2] = {(uint32_t)((8 * wave + (lane >> 4)) & 31), (uint32_t)((8 * wave + 4 + (lane >> 4)) & 31)};
+  const int ar = tid >> 3, apart = tid & 7;
+  const uint32_t arow = (uint32_t)(ar & 31);
   // this wave's MFMA step and projection; lane (j, g)
   const int s = wave & 3, proj = wave >> 2;
   const int j = lane & 15, g = lane >> 4;
@@ -246,88 +289,93 @@ __global__ void __launch_bounds__(kPfThreads, 4) k_pf_gu(PrefillArgs p) {  // 4 
   for (int t0 = 0; t0 < cnt; t0 += kGuTok) {
     const int T = min(kGuTok, cnt - t0);
     const int ntiles = (T + 15) >> 4;
-    int xtok[kXPieces];
+    int xtok[2];
 #pragma unroll
-    for (int h = 0; h < kXPieces; ++h) {
-      const int tt = (tid + h * kPfThreads) >> 4;
-      xtok[h] = tt < T ? buf_ldic(rtok, (uint32_t)(t0 + tt) * 4u, 0) : -1;
+    for (int h = 0; h < 2; ++h) {
+      const int tr = 8 * wave + 4 * h + (lane >> 4);
+      xtok[h] = tr < T ? buf_ldic(rtok, (uint32_t)(t0 + tr) * 4u, 0) : -1;
     }
-    auto load = [&](GuRegs& R, int c) {
+    // chunk c into stage c % kGuNS (a chunk past the end loads zeros)
+    auto issue = [&](int c) {
       const bool live = c < nchunks;
+      const int st = c % kGuNS;
       const uint32_t col0 = (uint32_t)(live ? c : 0) * kGuChunk;
 #pragma unroll
-      for (int h = 0; h < kXPieces; ++h) {
-        const uint32_t part = (uint32_t)((tid + h * kPfThreads) & 15);
-        const uint32_t xo = (live && xtok[h] >= 0) ? ((uint32_t)xtok[h] * (uint32_t)H + col0 + part * 8u) * 2u
-                                                   : kOffNone;
-        R.x[h] = buf_ld16c(rx, xo, 0);
+      for (int h = 0; h < 2; ++h) {
+        const int i = 2 * wave + h;
+        const int tr = 4 * i + (lane >> 4);
+        const uint32_t pc = (uint32_t)(xslot ^ (tr & 15));
+        const uint32_t xo = (live && xtok[h] >= 0) ? ((uint32_t)xtok[h] * (uint32_t)H + col0 + pc * 8u) * 2u : kOffNone;
+        ld_lds16(rx, &L.x[st][i * 1024], xo);
       }
-      const uint32_t col = col0 + 16u * (uint32_t)wpart;
-      const uint32_t ce = col >> d.qbs_shift;
-      const u32x2_t wv = __builtin_amdgcn_raw_buffer_load_b64(wup ? ru : rg, (int)(live ? wrow * rs + (col >> 1)
-                                                                                         : kOffNone), 0, 0);
-      R.w = make_uint2(wv.x, wv.y);
-      if constexpr (DQ) {
-        R.qa = buf_ldu8(wup ? ruq : rgq, live ? ((wrow >> 1) * A + ce) * 2u + (wrow & 1u) : kOffNone, 0);
-        const uint32_t f = (32u * (uint32_t)b + wrow) * A + ce;
-        R.am = buf_ldfc(wup ? ru2 : rg2, live ? (f >> d.dq_shift) * 4u : kOffNone, 0);
-      } else {
-        R.qa = 0;
-        R.am = buf_ldf(wup ? rua : rga, live ? (wrow * A + ce) * 4u : kOffNone, 0);
-      }
-    };
-    auto store = [&](int bi, const GuRegs& R) {
 #pragma unroll
-      for (int h = 0; h < kXPieces; ++h) {
-        const int piece = tid + h * kPfThreads;
-        *reinterpret_cast<uint4*>(&xs[bi][(piece >> 4) * kXRow + (piece & 15) * 16]) = R.x[h];
+      for (int h = 0; h < 2; ++h) {
+        const int i = 2 * wave + h;
+        const uint32_t wo = live ? wrow_b[h] * rs + (col0 >> 1) + wdw[h] * 4u : kOffNone;
+        ld_lds4(wup ? ru : rg, &L.w[st][i * 256], wo);
       }
-      *reinterpret_cast<uint2*>(&wsr[bi][wr * kWRow + wpart * 8]) = R.w;
-      float am = R.am;
-      if constexpr (DQ) am = dq_absmax(c2_s[wup ? 1 : 0][R.qa], R.am, wup ? d.up.offset : d.gate.offset);
-      ams[bi][wr][wpart] = am;  // the absmax of this thread's 16 columns
+      const uint32_t ce = (col0 + 16u * (uint32_t)apart) >> d.qbs_shift;
+      if constexpr (DQ) {
+        ld_lds1(wup ? ruq : rgq, &L.qa[st][wave * 64], live ? ((arow >> 1) * A + ce) * 2u + (arow & 1u) : kOffNone);
+        const uint32_t f = (32u * (uint32_t)b + arow) * A + ce;
+        ld_lds4(wup ? ru2 : rg2, &L.a2[st][wave * 64], live ? (f >> d.dq_shift) * 4u : kOffNone);
+      } else {
+        ld_lds4(wup ? rua : rga, &L.qa[st][wave * 64], live ? (arow * A + ce) * 4u : kOffNone);
+      }
     };
     float4_t acc[kGuTiles][2];
 #pragma unroll
     for (int tt = 0; tt < kGuTiles; ++tt) acc[tt][0] = acc[tt][1] = float4_t{0.0f, 0.0f, 0.0f, 0.0f};
-    GuRegs R[2];
-    load(R[0], 0);
-    load(R[1], 1);
-    store(0, R[0]);
-    load(R[0], 2);
-    __syncthreads();
-    // chunk c computes from buffer c & 1 while the next chunk goes into the
-    // other buffer; unrolled by two so the register stages are named
-    auto step = [&](int c, int bi, GuRegs& Rn) {
+#pragma unroll
+    for (int c = 0; c < kGuNS - 1; ++c) issue(c);
+    for (int c = 0; c < nchunks; ++c) {
+      // this thread's loads of chunk c have landed (those of the next
+      // kGuNS - 2 chunks may not), then every thread's
+      if constexpr (DQ)
+        asm volatile("s_waitcnt vmcnt(6)" ::: "memory");  // (kGuNS - 2) chunks x 6 loads
+      else
+        asm volatile("s_waitcnt vmcnt(5)" ::: "memory");  // (kGuNS - 2) chunks x 5 loads
+      pf_barrier();  // also: every wave is done with chunk c - 1, whose stage the next issue refills
+      issue(c + kGuNS - 1);
+      const int st = c % kGuNS;
       half8_t bf[2];
       {
         const int r0 = proj * 32 + j, r1 = r0 + 16;
-        const uint32_t w0 = *reinterpret_cast<const uint32_t*>(&wsr[bi][r0 * kWRow + 16 * s + 4 * g]);
-        const uint32_t w1 = *reinterpret_cast<const uint32_t*>(&wsr[bi][r1 * kWRow + 16 * s + 4 * g]);
-        deq8x2(w0, ams[bi][r0][2 * s + (g >> 1)], w1, ams[bi][r1][2 * s + (g >> 1)], cpair_s, bf[0], bf[1]);
+        const int a0 = r0 * 8 + 2 * s + (g >> 1), a1 = r1 * 8 + 2 * s + (g >> 1);
+        const uint32_t w0 = *reinterpret_cast<const uint32_t*>(
+            &L.w[st][r0 * 64 + ((uint32_t)(4 * s + g) ^ ((((uint32_t)(r0 & 31) >> 2) & 3u) << 2)) * 4]);
+        const uint32_t w1 = *reinterpret_cast<const uint32_t*>(
+            &L.w[st][r1 * 64 + ((uint32_t)(4 * s + g) ^ ((((uint32_t)(r1 & 31) >> 2) & 3u) << 2)) * 4]);
+        float am0, am1;
+        if constexpr (DQ) {
+          const float* c2 = L.c2[proj];
+          const float off = proj ? d.up.offset : d.gate.offset;
+          am0 = dq_absmax(c2[L.qa[st][a0] & 0xFFu], L.a2[st][a0], off);
+          am1 = dq_absmax(c2[L.qa[st][a1] & 0xFFu], L.a2[st][a1], off);
+        } else {
+          am0 = __uint_as_float(L.qa[st][a0]);
+          am1 = __uint_as_float(L.qa[st][a1]);
+        }
+        deq8x2(w0, am0, w1, am1, L.cpair, bf[0], bf[1]);
       }
 #pragma unroll
       for (int tt = 0; tt < kGuTiles; ++tt) {
         if (tt < ntiles) {
-          const half8_t af = as_h8(*reinterpret_cast<const uint4*>(&xs[bi][(tt * 16 + j) * kXRow + (32 * s + 8 * g) * 2]));
+          const int row = tt * 16 + j;
+          const half8_t af = as_h8(*reinterpret_cast<const uint4*>(
+              &L.x[st][row * 256 + ((uint32_t)(4 * s + g) ^ (uint32_t)(row & 15)) * 16]));
           acc[tt][0] = mfma16(af, bf[0], acc[tt][0]);
           acc[tt][1] = mfma16(af, bf[1], acc[tt][1]);
         }
       }
-      if (c + 1 < nchunks) {
-        store(bi ^ 1, Rn);
-        load(Rn, c + 3);
-      }
-      __syncthreads();
-    };
-    for (int c = 0; c < nchunks; c += 2) {
-      step(c, 0, R[1]);
-      if (c + 1 < nchunks) step(c + 1, 1, R[0]);
     }
-    // step partials summed in step order into [kGuTok tok][64 rows] fp32
-    // (rows: gate 0-31, up 32-63), reusing the token staging buffer
+    // the stages are free once every load (the zeros past the end too) has
+    // landed; step partials summed in step order into [kGuTok tok][64 rows]
+    // fp32 (rows: gate 0-31, up 32-63), reusing the token stages
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
     mfma_drain();
-    float* cs = reinterpret_cast<float*>(&xs[0][0]);
+    float* cs = reinterpret_cast<float*>(&L.x[0][0]);
     for (int ss = 0; ss < 4; ++ss) {
       if (s == ss) {
 #pragma unroll
@@ -565,10 +613,15 @@ void launch_prefill(const PrefillArgs& p, hipStream_t s) {
   k_pf_scan<<<dim3(1), dim3(1024), 0, s>>>(p);
   k_pf_list<<<dim3((unsigned)((p.d.NB + 255) / 256)), dim3(256), 0, s>>>(p);
   if (p.act_dense != nullptr) launch_zero_u32(reinterpret_cast<uint32_t*>(p.act_dense), (long long)p.M * p.d.NB * 16, s);
+  static std::once_flag gu_once;
+  std::call_once(gu_once, [] {
+    for (const void* f : {reinterpret_cast<const void*>(k_pf_gu<true>), reinterpret_cast<const void*>(k_pf_gu<false>)})
+      (void)hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, (int)sizeof(GuLds));
+  });
   if (p.d.dq)
-    k_pf_gu<true><<<dim3(p.d.NB), dim3(kPfThreads), 0, s>>>(p);
+    k_pf_gu<true><<<dim3(p.d.NB), dim3(kPfThreads), sizeof(GuLds), s>>>(p);
   else
-    k_pf_gu<false><<<dim3(p.d.NB), dim3(kPfThreads), 0, s>>>(p);
+    k_pf_gu<false><<<dim3(p.d.NB), dim3(kPfThreads), sizeof(GuLds), s>>>(p);
   if (p.act_dense != nullptr) {
     // every token's act is zero outside its own blocks, so the dense down GEMM
     // over the scattered act is the per-token sum over the selected blocks
