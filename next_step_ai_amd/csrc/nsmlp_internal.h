@@ -433,12 +433,19 @@ struct TopkLds {
   unsigned wsum[16];
 };
 
+// Inclusive prefix sum over the 64 lanes (all active) with DPP moves: a
+// Hillis-Steele scan inside each row of 16 lanes (row_shr 1, 2, 4, 8; lanes
+// shifted in from before the row read 0), then the row totals carried over
+// (row_bcast:15 adds lane 15 to row 1 and lane 47 to row 3; row_bcast:31
+// adds lane 31 to rows 2 and 3).  No LDS round trip per step.
 __device__ __forceinline__ unsigned wave_incl_scan(unsigned v, int lane) {
-#pragma unroll
-  for (int d = 1; d < kWave; d <<= 1) {
-    const unsigned o = __shfl_up(v, d, kWave);
-    if (lane >= d) v += o;
-  }
+  (void)lane;
+  v += (unsigned)__builtin_amdgcn_update_dpp(0, (int)v, 0x111, 0xF, 0xF, false);  // row_shr:1
+  v += (unsigned)__builtin_amdgcn_update_dpp(0, (int)v, 0x112, 0xF, 0xF, false);  // row_shr:2
+  v += (unsigned)__builtin_amdgcn_update_dpp(0, (int)v, 0x114, 0xF, 0xF, false);  // row_shr:4
+  v += (unsigned)__builtin_amdgcn_update_dpp(0, (int)v, 0x118, 0xF, 0xF, false);  // row_shr:8
+  v += (unsigned)__builtin_amdgcn_update_dpp(0, (int)v, 0x142, 0xA, 0xF, false);  // row_bcast:15
+  v += (unsigned)__builtin_amdgcn_update_dpp(0, (int)v, 0x143, 0xC, 0xF, false);  // row_bcast:31
   return v;
 }
 
@@ -485,19 +492,19 @@ __device__ __forceinline__ void topk_threshold(const uint32_t (&key)[KPT], int i
     // share one bin: they are counted per wave and added once, instead of
     // contending on one LDS counter.
     constexpr uint32_t kZeroKey = 0x8000u;  // order key of +0.0
-    unsigned nzero = 0;
+    unsigned nzero = 0;  // this wave's zero keys of the pass (ballot counts: uniform over the wave)
 #pragma unroll
     for (int m = 0; m < KPT; ++m) {
-      if (i0 + m >= NB) continue;
-      if (key[m] == kZeroKey) {
-        nzero += pass == 0 || (T >> 8) == (kZeroKey >> 8);
-      } else if (pass == 0) {
+      const bool in = i0 + m < NB;
+      const bool isz = in && key[m] == kZeroKey;
+      nzero += (unsigned)__popcll(__ballot(isz && (pass == 0 || (T >> 8) == (kZeroKey >> 8))));
+      if (!in || isz) continue;
+      if (pass == 0) {
         atomicAdd(&L.hist[0][key[m] >> 8], 1u);
       } else if ((key[m] >> 8) == (T >> 8)) {
         atomicAdd(&L.hist[1][key[m] & 0xFFu], 1u);
       }
     }
-    nzero = wave_sum(nzero);
     if (lane == 0 && nzero != 0)
       atomicAdd(&L.hist[pass][pass == 0 ? (kZeroKey >> 8) : (kZeroKey & 0xFFu)], nzero);
     __syncthreads();
