@@ -12,9 +12,9 @@ Reported (one JSON line):
                 sparse MLP per layer, 126 layers per token)
   ms_per_step   wall time per layer (router + MLP), inputs resident in HBM
   roofline      the sparse-MLP decode launch pair (k_gu_rep + k_down_rep),
-                timed with HIP events on its launch stream: algorithmic bytes
-                per launch (selected packed NF4 + their absmax in the stored
-                format + x + out) / duration.  traffic: HBM bytes per launch from the rocprofv3
+                timed with one pair of HIP events on its launch stream around
+                all steps: algorithmic bytes per launch (selected packed NF4 +
+                their absmax in the stored format + x + out) / mean duration.  traffic: HBM bytes per launch from the rocprofv3
                 FETCH_SIZE / WRITE_SIZE summary committed for this workload,
                 scaled by the same counters on a plain copy (null without it)
   cpu_baseline  the oracle's restatement of the reference PyTorch path
@@ -243,6 +243,22 @@ def copy_calibration(nbytes: int) -> int:
     return 0
 
 
+def timed_loop_us(launch, steps: int) -> float:
+    """Mean µs per step of `launch(i)` for i < steps: one pair of HIP events
+    on the current stream (the stream the C ABI is given) brackets the whole
+    loop, so no event marker sits between two steps' kernels."""
+    import torch
+
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    start.record()
+    for i in range(steps):
+        launch(i)
+    end.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) * 1e3 / steps
+
+
 def base_result(args, value: float, us_per_layer: float, H: int, I: int, R: int, k: int, qbs: int) -> dict:
     return {
         "metric": METRIC,
@@ -383,14 +399,11 @@ def run_prefill(args) -> int:
         L.table.prefill(L.xs, routers[i % n].route(L.xs, k), out=outs[i % n])
     torch.cuda.synchronize()
     step_us = (time.perf_counter() - t0) / steps * 1e6
-    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
-    for i in range(steps):
+    def mlp(i: int) -> None:
         L = layers[i % n]
-        ev[i][0].record()
         L.table.prefill(L.xs, L.sel, out=outs[i % n])
-        ev[i][1].record()
-    torch.cuda.synchronize()
-    mlp_us = statistics.mean(a.elapsed_time(b) for a, b in ev) * 1e3
+
+    mlp_us = timed_loop_us(mlp, steps)
     union = [int(torch.unique(L.sel).numel()) for L in layers]
     per_block = algorithmic_bytes(H, I, 1, qbs, args.absmax) - algorithmic_bytes(H, I, 0, qbs, args.absmax)
     ubytes = int(statistics.mean(union)) * per_block + 2 * 2 * M * H
@@ -440,16 +453,9 @@ def run_dense_guard(args) -> int:
     for i in range(max(1, args.warmup // 10)):
         layers[i % n].table.dense_mlp(layers[i % n].xs, out=outs[i % n])
     torch.cuda.synchronize()
-    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
     t0 = time.perf_counter()
-    for i in range(steps):
-        L = layers[i % n]
-        ev[i][0].record()
-        L.table.dense_mlp(L.xs, out=outs[i % n])
-        ev[i][1].record()
-    torch.cuda.synchronize()
+    us = timed_loop_us(lambda i: layers[i % n].table.dense_mlp(layers[i % n].xs, out=outs[i % n]), steps)
     step_us = (time.perf_counter() - t0) / steps * 1e6
-    us = statistics.mean(a.elapsed_time(b) for a, b in ev) * 1e3
     flop = 2.0 * 3 * M * I * H
     res = base_result(args, M / (step_us * 1e-6), step_us, H, I, R, I // 32, qbs)
     res["metric"] = f"dense-guard prefill MLP tok/s per layer + MFMA TFLOP/s vs peak, 405B shape, {M} tokens"
@@ -574,15 +580,9 @@ def run_lm_head(args) -> int:
     for i in range(args.warmup):
         dense_linear_nf4(xs[i % 4], packed, absmax, code, V, H, qbs)
     torch.cuda.synchronize()
-    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(args.steps)]
     t0 = time.perf_counter()
-    for i in range(args.steps):
-        ev[i][0].record()
-        dense_linear_nf4(xs[i % 4], packed, absmax, code, V, H, qbs)
-        ev[i][1].record()
-    torch.cuda.synchronize()
+    us = timed_loop_us(lambda i: dense_linear_nf4(xs[i % 4], packed, absmax, code, V, H, qbs), args.steps)
     wall_us = (time.perf_counter() - t0) / args.steps * 1e6
-    us = statistics.mean(a.elapsed_time(b) for a, b in ev) * 1e3
     nbytes = lm_head_bytes(V, H, qbs, args.absmax)
     gbs = nbytes / (us * 1e-6) / 1e9
     res = base_result(args, 1e6 / wall_us, wall_us, H, 0, 0, 0, qbs)
@@ -699,18 +699,15 @@ def main() -> int:
     print(f"[bench] {args.steps} steps: {us_per_layer:.2f} us/layer (router + MLP)", file=sys.stderr, flush=True)
 
     # Sparse-MLP decode launch pair alone, HIP events on its launch stream
-    # (torch's current stream, the one the C ABI is given).
+    # (torch's current stream, the one the C ABI is given) around all steps.
     for j in range(n):
         layers[j].table.decode(layers[j].x, sels[j], out=outs[j])
-    torch.cuda.synchronize()
-    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(args.steps)]
-    for i in range(args.steps):
+
+    def pair(i: int) -> None:
         j = i % n
-        ev[i][0].record()
         layers[j].table.decode(layers[j].x, sels[j], out=outs[j])
-        ev[i][1].record()
-    torch.cuda.synchronize()
-    mlp_us = statistics.mean(a.elapsed_time(b) for a, b in ev) * 1e3
+
+    mlp_us = timed_loop_us(pair, args.steps)
     route_us = max(0.0, us_per_layer - mlp_us)
 
     abytes = algorithmic_bytes(H, I, k, qbs, args.absmax)
