@@ -684,7 +684,8 @@ int nsmlp_prefill_slots_f16(const nsmlp_slot_table* table, const void* x, int M,
   off += align_up((size_t)p.d.NB * (p.TG + 1) * 4);
   p.tokens = (int32_t*)(base + off);
   off += align_up(nk * 4);
-  if (prefill_dense_down(p.d.H, p.d.NB, M, k)) {
+  // the grouped down fits in the dense path's workspace (M k <= M NB)
+  if (prefill_dense_down(p.d.H, p.d.NB, M, k) && dense_down_fits(p.d, dense_guard_splits(p.d.H, p.d.NB, M))) {
     p.act_dense = (uint16_t*)(base + off);
     off += align_up((size_t)M * p.d.NB * 64);
     p.part = (float*)(base + off);
@@ -728,6 +729,8 @@ int nsmlp_dense_mlp_slots_f16(const nsmlp_slot_table* table, const void* x, int 
   g.x = (const uint16_t*)x;
   g.M = M;
   g.S = dense_guard_splits(H, g.d.NB, M);
+  if (!dense_down_fits(g.d, g.S))
+    return set_error(NSMLP_EINVAL, "dense MLP: the down weights of %d slots at H=%d exceed 31-bit offsets", g.d.n_slots, H);
   size_t off = align_up(kCounterBytes);
   g.act = (uint16_t*)(base + off);
   off += align_up((size_t)M * I * 2);

@@ -310,97 +310,347 @@ __global__ void __launch_bounds__(kDgThreads, 2) k_dg_gu(DenseGuardArgs g) {
   }
 }
 
-template <bool DQ, int MT>
-__global__ void __launch_bounds__(kDgThreads, 2) k_dg_down(DenseGuardArgs g) {
-  extern __shared__ __attribute__((aligned(16))) uint8_t dg_lds[];
-  _Float16* As = reinterpret_cast<_Float16*>(dg_lds);  // [2][256][72] act rows
-  _Float16* Bs = As + 2 * kDgStage;                      // [2][256][72] down rows
-  float2* cp = reinterpret_cast<float2*>(Bs + 2 * kDgStage);  // [256 x 4] down code pairs
-  float* c2s = reinterpret_cast<float*>(cp + 1024);
+// ------------------------------------------------------------- down GEMM --
+// part[s][t][o] = sum over the blocks of range s of act[t][i] * Wd[o][i],
+// Wd = fp16(code * absmax).  A workgroup of 4 waves takes 256 output rows,
+// 256 tokens and one block range; wave w owns rows 64 w .. + 63 and keeps
+// all 256 tokens x 64 rows in 256 fp32 accumulators (AGPRs), so each decoded
+// weight feeds 16 MFMAs and every weight is read from HBM once.  A step
+// covers 2 blocks (64 columns):
+//   - lane (n = l % 16, q = l / 16) loads, for each of its 4 16-row groups,
+//     8 packed bytes of row n: bytes 8 (q / 2) .. + 7 of block 2 c + q % 2.
+//     Dword j of them is the lane's B fragment for MFMA step j, so K slots
+//     8 q .. 8 q + 7 of step j are columns 16 (q / 2) + 8 j .. + 7 of block
+//     2 c + q % 2.  The weights are decoded in registers (each row by one
+//     wave, no LDS staging) through a lane-replicated fp32 code-pair table:
+//     two fp32 products rounded to fp16 by one v_cvt_pk_f16_f32;
+//   - the 256 token rows of the 64 columns (128 bytes each) go into an LDS
+//     stage by loads straight into LDS; row r's 16-byte piece p lands in
+//     slot p ^ ((r / 2) % 8), so 16 rows read at one piece hit 16 different
+//     16-byte bank groups;
+//   - every wave runs 2 MFMA steps x 4 row groups x 16 token groups.
+// One wave per SIMD: 256 accumulators leave no room for a second.  A wave
+// does not overlap its own VALU work with its MFMAs (measured on this GPU:
+// one wave reaches 72% of the MFMA peak with no other work, 49% with two
+// VALU ops per MFMA), so the decode is kept to about one VALU op per MFMA
+// (each decoded weight feeds 16 MFMAs) and issued between the MFMAs, and
+// every LDS read is issued a unit of MFMAs before its use (see the step
+// schedule below).
+constexpr int kDnThreads = 256;
+constexpr int kDnTok = 256;                            // tokens per tile
+constexpr int kDnRows = 256;                           // output rows per workgroup (64 per wave)
+constexpr int kDnCopies = 32;                          // code-pair table copies (lane % 32)
+constexpr uint32_t kDnTab = 256u * kDnCopies * 8u;     // 64 KB at LDS address 0
+constexpr uint32_t kDnStage = kDnTok * 128u;           // 256 rows x 64 fp16
+constexpr uint32_t kDnC2 = kDnTab + 2u * kDnStage;     // second-level code book [256]
+constexpr uint32_t kDnRefs = kDnC2 + 256u * 4u;        // block references of the range
+constexpr int kDnRefHost = 1 << 30;                    // reference bit: host copy
+constexpr uint32_t kDnLdsMax = 160u * 1024u;
+
+typedef float dn_f2_t __attribute__((ext_vector_type(2)));
+typedef const __attribute__((address_space(3))) dn_f2_t* lds_f2_ptr;
+typedef const __attribute__((address_space(3))) half8_t* lds_h8_ptr;
+__device__ __forceinline__ dn_f2_t lds_ld_f2(uint32_t byte_addr) {
+  return *reinterpret_cast<lds_f2_ptr>(static_cast<uintptr_t>(byte_addr));
+}
+__device__ __forceinline__ half8_t lds_ld_h8(uint32_t byte_addr) {
+  return *reinterpret_cast<lds_h8_ptr>(static_cast<uintptr_t>(byte_addr));
+}
+
+// 8 NF4 codes (one packed dword, even element in the high nibble) ->
+// 8 fp16(code * am) in element order, in two halves so that the table
+// lookups can go out a unit ahead of their use: dn_lookup4 reads the four
+// code pairs, dn_finish8 scales them and rounds to fp16.  ad[i] holds this
+// lane's copy offset (copy * 8) in its low byte; the packed byte goes into
+// bits 8..15.
+struct DnPairs {
+  dn_f2_t p[4];
+};
+__device__ __forceinline__ DnPairs dn_lookup4(uint32_t v, uint32_t (&ad)[4]) {
+  NSMLP_SET_BYTE1(ad[0], v, "BYTE_0");
+  NSMLP_SET_BYTE1(ad[1], v, "BYTE_1");
+  NSMLP_SET_BYTE1(ad[2], v, "BYTE_2");
+  NSMLP_SET_BYTE1(ad[3], v, "BYTE_3");
+  return DnPairs{{lds_ld_f2(ad[0]), lds_ld_f2(ad[1]), lds_ld_f2(ad[2]), lds_ld_f2(ad[3])}};
+}
+__device__ __forceinline__ half8_t dn_finish8(const DnPairs& pr, float am) {
+  uint32_t o[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const float2_t w = {pr.p[i].x * am, pr.p[i].y * am};
+    o[i] = __builtin_bit_cast(uint32_t, __builtin_convertvector(w, half2_t));
+  }
+  return as_h8(make_uint4(o[0], o[1], o[2], o[3]));
+}
+
+// Bytes spanned by the packed rows (abs = false, 16 bytes per row and block)
+// or the absmax entries (elem bytes each) of `blocks` slots of a down view.
+__host__ __device__ inline long long dn_extent(const ProjView& v, int blocks, int H, bool abs, int elem) {
+  if (blocks <= 0) return 0;
+  const long long bs = abs ? v.abs_blk_stride : v.blk_stride, rs = abs ? v.abs_row_stride : v.row_stride;
+  return abs ? ((blocks - 1) * bs + (long long)(H - 1) * rs + 1) * elem : (blocks - 1) * bs + (long long)(H - 1) * rs + elem;
+}
+
+// One step's weight loads: 8 packed bytes per 16-row group and their absmax
+// (u8 code + second-level scale, or fp32).
+struct DnW {
+  uint2 w[4];
+  uint32_t qa[4];
+  float a[4];
+  int ok;  // the lane's block is valid (its absmax is forced to zero otherwise)
+};
+
+template <bool DQ, bool HOST>
+__global__ void __launch_bounds__(kDnThreads, 1) k_dg_down(DenseGuardArgs g) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t dn_lds[];  // no static LDS: dn_lds is LDS address 0
   const DecodeArgs& d = g.d;
   const int tid = threadIdx.x, lane = tid & (kWave - 1);
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int H = d.H, NB = d.NB, I = NB * 32, M = g.M, S = g.S;
-  const int ntiles = H / 256;
-  // XCD-aware: the workgroups of one block range (which read the same act
-  // columns) share XCDs when the grid allows it
-  int nt, s;
-  if (S * ntiles == 256 && S <= 8 && 8 % S == 0) {
-    const int xcd = blockIdx.x & 7, slot = blockIdx.x >> 3, per = 8 / S;
-    s = xcd / per;
-    nt = (xcd % per) * 32 + slot;
-  } else {
-    nt = blockIdx.x % ntiles;
-    s = blockIdx.x / ntiles;
+  // XCD-aware order: workgroups go to the 8 XCDs round-robin; when the grid
+  // divides by 8, XCD x runs the consecutive tiles x N/8 .. (x+1) N/8 - 1:
+  // row tiles of one (range, token tile), which read the same act columns
+  // through the XCD's L2
+  const int RT = (H + kDnRows - 1) / kDnRows, N = (int)gridDim.x;
+  int idx = (int)blockIdx.x;
+  if ((N & 7) == 0) idx = (idx & 7) * (N >> 3) + (idx >> 3);
+  const int rt = idx % RT, combo = idx / RT, s = combo % S, tt = combo / S;
+  const int t0 = g.t_base + tt * kDnTok;
+  const int G = NB / 2;  // 2-block steps
+  const int g_lo = (int)((long long)s * G / S), g_hi = (int)((long long)(s + 1) * G / S);
+  const int nst = g_hi - g_lo, b_lo = 2 * g_lo;
+  float* c2s = reinterpret_cast<float*>(dn_lds + kDnC2);
+  int32_t* refs = reinterpret_cast<int32_t*>(dn_lds + kDnRefs);
+
+  // code-pair table: thread e writes the 32 copies of entry e (code[e >> 4],
+  // code[e & 15]), 256 contiguous bytes
+  {
+    const float hi = d.code_down[tid >> 4], lo = d.code_down[tid & 15];
+    uint4* dst = reinterpret_cast<uint4*>(dn_lds + tid * 256);
+    const uint4 v = make_uint4(__float_as_uint(hi), __float_as_uint(lo), __float_as_uint(hi), __float_as_uint(lo));
+#pragma unroll
+    for (int i = 0; i < 16; ++i) dst[i] = v;
   }
-  const int t0 = g.t_base + (int)blockIdx.y * 64 * MT, o0 = nt * 256;
-  const int C = NB / 2;  // chunks of two blocks
-  const int c_lo = (int)((long long)s * C / S), c_hi = (int)((long long)(s + 1) * C / S);
-  dg_pairs(cp, d.code_down, tid, 4);
-  dg_pairs(cp, d.code_down, tid + 512, 4);
-  if constexpr (DQ) {
-    if (tid < 256) c2s[tid] = d.down.code2[tid];
-  }
-  // staged down row o = o0 + tid % 256 of block 2 c + tid / 256 (uniform over the wave)
-  const int orow = tid & 255, hb = wave >> 2;
-  const uint32_t o = (uint32_t)(o0 + orow);
-  const uint32_t Ad = (uint32_t)I >> d.qbs_shift;
+  if constexpr (DQ) c2s[tid] = d.down.code2[tid];
+  // block references: slot, or the block id with kDnRefHost for a host copy,
+  // or -1 (out of the table, or no tokens when the block lists are given)
   const bool have_host = d.host_down.packed != nullptr;
-  const rsrc_t rx = make_rsrc(g.act, (int)((long long)M * I * 2));
-  const rsrc_t r2 = DQ ? make_rsrc(d.down.absmax2, (int)((((long long)H * Ad + (1 << d.dq_shift) - 1) >> d.dq_shift) * 4))
-                       : rx;
-  auto load_x = [&](uint4 (&X)[MT], int c) {
-    const bool live = c < c_hi;
-    dg_load_rows(X, rx, tid, t0, M, (uint32_t)I, (uint32_t)(live ? c : c_lo) * kDgK, live);
-  };
-  auto load_w = [&](DgW& W, int c) {
-    const bool live = c < c_hi;
-    const int b = 2 * (live ? c : c_lo) + hb;
+  for (int i = tid; i < 2 * nst; i += kDnThreads) {
+    const int b = b_lo + i;
     const int slot = d.lookup ? d.lookup[b] : b;
-    const bool dev = slot >= 0;
     const bool used = g.offsets == nullptr || g.offsets[b + 1] > g.offsets[b];
-    const bool ok = live && used && (dev ? slot < d.n_slots : have_host);
-    const long long q = ok ? (dev ? slot : b) : 0;
-    const rsrc_t rw = make_rsrc((dev ? d.down.packed : d.host_down.packed) + q * d.down.blk_stride, ok ? H * 16 : 0);
-    W.w = buf_ld16(rw, o * 16u, 0);
-    if constexpr (DQ) {
-      const rsrc_t ra = make_rsrc((dev ? d.down.qabsmax : d.host_down.qabsmax) + q * d.down.abs_blk_stride, ok ? H : 0);
-      W.qa = buf_ldu8(ra, o, 0);
-      const uint32_t f = o * Ad + ((32u * (uint32_t)b) >> d.qbs_shift);
-      W.am = buf_ldfc(r2, ok ? (f >> d.dq_shift) * 4u : kOffNone, 0);
-    } else {
-      const rsrc_t ra = make_rsrc((dev ? d.down.absmax : d.host_down.absmax) + q * d.down.abs_blk_stride,
-                                  ok ? H * 4 : 0);
-      W.qa = 0;
-      W.am = buf_ldf(ra, o * 4u, 0);
+    const bool dev = slot >= 0;
+    const bool ok = used && (dev ? slot < d.n_slots : have_host);
+    refs[i] = !ok ? -1 : (dev ? slot : (kDnRefHost | b));
+  }
+  __syncthreads();
+
+  const int n = lane & 15, q = lane >> 4, qb = q & 1, qh = q >> 1;
+  const uint32_t o0 = (uint32_t)(rt * kDnRows + wave * 64 + n);  // row of group 0; group rg: o0 + 16 rg
+  const uint32_t rs = (uint32_t)d.down.row_stride, bs = (uint32_t)d.down.blk_stride;
+  const uint32_t ars = (uint32_t)d.down.abs_row_stride, abs_ = (uint32_t)d.down.abs_blk_stride;
+  const uint32_t Ad = (uint32_t)I >> d.qbs_shift;
+  const rsrc_t rw = make_rsrc(d.down.packed, (int)dn_extent(d.down, d.n_slots, H, false, 16));
+  const rsrc_t rwh = HOST ? make_rsrc(d.host_down.packed, (int)dn_extent(d.down, NB, H, false, 16)) : rw;
+  const rsrc_t ra = DQ ? make_rsrc(d.down.qabsmax, (int)dn_extent(d.down, d.n_slots, H, true, 1))
+                       : make_rsrc(d.down.absmax, (int)dn_extent(d.down, d.n_slots, H, true, 4));
+  const rsrc_t rah = !HOST ? ra
+                     : DQ  ? make_rsrc(d.host_down.qabsmax, (int)dn_extent(d.down, NB, H, true, 1))
+                           : make_rsrc(d.host_down.absmax, (int)dn_extent(d.down, NB, H, true, 4));
+  const rsrc_t r2 = DQ ? make_rsrc(d.down.absmax2, (int)((((long long)H * Ad + (1 << d.dq_shift) - 1) >> d.dq_shift) * 4))
+                       : ra;
+  const rsrc_t rx = make_rsrc(g.act, (int)((long long)M * I * 2));
+
+  // Offsets: a lane's row in 16-row group rg is o0 + 16 rg, so the group's
+  // part of every weight and absmax offset is a uniform constant that goes
+  // into the load's scalar offset; the rows of a wave (64, H % 256 == 0) are
+  // all inside H or all outside.  Every offset is computed, then selected:
+  // a select between two registers (an arm with arithmetic becomes a
+  // branch, which splits the step into blocks the scheduler and the register
+  // allocator see separately).
+  const bool wrows = (int)(rt * kDnRows + wave * 64) < H;
+  auto issue_w = [&](DnW& W, int c) {
+    const int cc = max(0, min(c, nst - 1));  // clamped: the reference read stays in the range
+    const int enc = refs[2 * cc + qb];
+    const bool ok = (c < nst) & (enc >= 0) & wrows;
+    const bool host = HOST & ((enc & kDnRefHost) != 0);
+    const uint32_t qq = (uint32_t)(enc & (kDnRefHost - 1));
+    const uint32_t b = (uint32_t)(b_lo + 2 * cc + qb);
+    const bool dv = ok & !host, hv = ok & host;
+    const uint32_t wo_d = qq * bs + o0 * rs + 8u * (uint32_t)qh, ao_d = qq * abs_ + o0 * ars;
+    const uint32_t wo_h = b * bs + o0 * rs + 8u * (uint32_t)qh, ao_h = b * abs_ + o0 * ars;
+    const uint32_t ab = DQ ? 1u : 4u;
+    const uint32_t wo = dv ? wo_d : kOffNone, ao = dv ? ao_d * ab : kOffNone;
+    const uint32_t who = hv ? wo_h : kOffNone, aho = hv ? ao_h * ab : kOffNone;
+    const uint32_t f0 = o0 * Ad + ((32u * b) >> d.qbs_shift);
+    W.ok = ok;
+#pragma unroll
+    for (int rg = 0; rg < 4; ++rg) {
+      const uint32_t so_w = 16u * (uint32_t)rg * rs, so_a = 16u * (uint32_t)rg * ars * ab;
+      W.w[rg] = buf_ld8(rw, wo, so_w);
+      if constexpr (HOST) {
+        const uint2 h = buf_ld8(rwh, who, so_w);
+        W.w[rg] = make_uint2(W.w[rg].x | h.x, W.w[rg].y | h.y);
+      }
+      if constexpr (DQ) {
+        W.qa[rg] = buf_ldu8(ra, ao, so_a);
+        if constexpr (HOST) W.qa[rg] |= buf_ldu8(rah, aho, so_a);
+        const uint32_t fo = ((f0 + 16u * (uint32_t)rg * Ad) >> d.dq_shift) * 4u;
+        W.a[rg] = buf_ldfc(r2, ok ? fo : kOffNone, 0);
+      } else {
+        W.a[rg] = buf_ldf(ra, ao, so_a);
+        if constexpr (HOST) W.a[rg] = __uint_as_float(__float_as_uint(W.a[rg]) | __float_as_uint(buf_ldf(rah, aho, so_a)));
+      }
     }
   };
-  auto store_x = [&](int bi, const uint4 (&X)[MT]) { dg_store_rows<MT>(As + bi * kDgStage, X, tid); };
-  auto store_w = [&](int bi, const DgW& W) {
-    float am = W.am;
-    if constexpr (DQ) am = dq_absmax(c2s[W.qa], W.am, d.down.offset);
-    dg_decode32<4>(Bs + bi * kDgStage + orow * kDgRow + 32 * hb, W.w, am, cp + (lane & 3));
+  // token rows of step c into stage c & 1: load i of wave w fills rows
+  // 32 i + 8 w .. + 7 (lane l: row + l / 8, slot l % 8); row i's offset is
+  // load 0's plus 32 i rows (a scalar offset)
+  const int arow = 8 * wave + (lane >> 3);  // row of load 0 ((row / 2) % 8 is the same for every load)
+  const uint32_t apiece = (uint32_t)((lane & 7) ^ ((arow >> 1) & 7));
+  const uint32_t xrow = ((uint32_t)(t0 + arow) * (uint32_t)I + 8u * apiece) * 2u;
+  auto issue_x = [&](int c) {
+    const int tlim = c < nst ? M - t0 - arow : 0;  // rows 32 i with 32 i < tlim are tokens of this call
+    const uint32_t xo = xrow + (uint32_t)(64 * (b_lo + 2 * c));
+    const uint32_t sb = kDnTab + (uint32_t)(c & 1) * kDnStage;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const uint32_t xi = 32 * i < tlim ? xo : kOffNone;
+      ld_lds16s(rx, dn_lds + sb + (32 * i + 8 * wave) * 128, xi, 64u * (uint32_t)i * (uint32_t)I);
+    }
   };
-  const int mq = wave & 3, nh = wave >> 2;
-  auto brow = [nh](int ni) { return 128 * nh + 16 * ni; };
-  float4_t acc[MT][8];
+
+  // 256 accumulators, kept in AGPRs: pinned there at the start and after
+  // every step (otherwise part of them crosses the loop in VGPRs, which the
+  // loads in flight and the decode need)
+  float4_t acc[16][4];
 #pragma unroll
-  for (int mi = 0; mi < MT; ++mi)
+  for (int mi = 0; mi < 16; ++mi)
 #pragma unroll
-    for (int ni = 0; ni < 8; ++ni) acc[mi][ni] = float4_t{0.0f, 0.0f, 0.0f, 0.0f};
-  auto mma = [&](int bi) { dg_mma(acc, As + bi * kDgStage, Bs + bi * kDgStage, mq, lane, brow); };
-  dg_pipeline<MT>(c_lo, c_hi, load_x, load_w, store_x, store_w, mma);
+    for (int rg = 0; rg < 4; ++rg) {
+      acc[mi][rg] = float4_t{0.0f, 0.0f, 0.0f, 0.0f};
+      asm volatile("" : "+a"(acc[mi][rg]));
+    }
+  uint32_t ad[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) ad[i] = (uint32_t)(lane & (kDnCopies - 1)) * 8u;
+  // A fragment (token group mi, MFMA step j) of step c: token row 16 mi + n,
+  // piece 4 (q % 2) + 2 (q / 2) + j, in slot piece ^ ((row / 2) % 8)
+  auto read_a = [&](half8_t (&a)[8], int c, int j, int h) {
+    const uint32_t piece = (uint32_t)(4 * qb + 2 * qh + j);
+    const uint32_t base = kDnTab + (uint32_t)(c & 1) * kDnStage + (uint32_t)n * 128u +
+                          ((piece ^ (uint32_t)((n >> 1) & 7)) << 4) + (uint32_t)h * 16384u;
+#pragma unroll
+    for (int mi = 0; mi < 8; ++mi) a[mi] = lds_ld_h8(base + (uint32_t)mi * 2048u);
+  };
+  auto am_of = [&](const DnW& W, float (&am)[4]) {
+#pragma unroll
+    for (int rg = 0; rg < 4; ++rg) {
+      float v = W.a[rg];
+      if constexpr (DQ) v = dq_absmax(c2s[W.qa[rg]], W.a[rg], d.down.offset);
+      am[rg] = W.ok ? v : 0.0f;
+    }
+  };
+  auto lookup4 = [&](DnPairs (&pr)[4], const DnW& W, int j) {
+#pragma unroll
+    for (int rg = 0; rg < 4; ++rg) pr[rg] = dn_lookup4(j == 0 ? W.w[rg].x : W.w[rg].y, ad);
+  };
+  auto finish4 = [&](half8_t (&b)[4], const DnPairs (&pr)[4], const float (&am)[4]) {
+#pragma unroll
+    for (int rg = 0; rg < 4; ++rg) b[rg] = dn_finish8(pr[rg], am[rg]);
+  };
+  // 32 MFMAs: token groups 8 h .. 8 h + 7 x the 4 row groups
+  auto mfma_unit = [&](const half8_t (&a)[8], const half8_t (&b)[4], int h) {
+#pragma unroll
+    for (int rg = 0; rg < 4; ++rg)
+#pragma unroll
+      for (int mi = 0; mi < 8; ++mi) acc[8 * h + mi][rg] = mfma16(a[mi], b[rg], acc[8 * h + mi][rg]);
+    // each MFMA followed by an LDS read and a VALU op of the work ahead
+#pragma unroll
+    for (int i = 0; i < 32; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  auto step_sync = [] {
+    __builtin_amdgcn_s_waitcnt(0);  // vmcnt(0) expcnt(0) lgkmcnt(0)
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+  };
+
+  // A step is 4 units (MFMA step j, token half h) of 32 MFMAs; while unit
+  // (j, h) runs, the A fragments of the next unit are read and the B
+  // fragments of the next MFMA step are looked up (h = 0) or finished
+  // (h = 1).  Before the last unit the wave waits for step c + 1's loads and
+  // meets the others at the barrier (every wave has read its last A
+  // fragments of stage c & 1), sends step c + 2's loads into that stage and
+  // reads step c + 1's first A fragments.  Three weight register sets:
+  // decoded, arrived, in flight (moved down one set per step).
+  DnW W0, W1, W2;
+  half8_t ax[8], ay[8], b0[4], b1[4];
+  DnPairs pr[4];
+  float am_c[4], am_n[4];
+  issue_w(W0, 0);
+  issue_x(0);
+  issue_w(W1, 1);
+  issue_x(1);
+  __builtin_amdgcn_s_waitcnt(0);
+  __builtin_amdgcn_s_barrier();  // step 0's token rows are in LDS (and step 1's)
+  asm volatile("" ::: "memory");
+  am_of(W0, am_c);
+  read_a(ax, 0, 0, 0);
+  lookup4(pr, W0, 0);
+  finish4(b0, pr, am_c);
+  __builtin_amdgcn_sched_barrier(0);
+
+  auto step = [&](int c, const DnW& Wc, const DnW& Wn, DnW& Wf) {
+    // unit (0, 0): B fragments of MFMA step 1 looked up
+    read_a(ay, c, 0, 1);
+    lookup4(pr, Wc, 1);
+    mfma_unit(ax, b0, 0);
+    // unit (0, 1): ... and finished
+    read_a(ax, c, 1, 0);
+    finish4(b1, pr, am_c);
+    mfma_unit(ay, b0, 1);
+    // unit (1, 0): the next step's MFMA step 0 looked up (its weights are in)
+    read_a(ay, c, 1, 1);
+    am_of(Wn, am_n);
+    lookup4(pr, Wn, 0);
+    mfma_unit(ax, b1, 0);
+    // unit (1, 1)
+    step_sync();
+    issue_w(Wf, c + 2);
+    issue_x(c + 2);
+    read_a(ax, c + 1, 0, 0);
+    finish4(b0, pr, am_n);
+    mfma_unit(ay, b1, 1);
+#pragma unroll
+    for (int rg = 0; rg < 4; ++rg) am_c[rg] = am_n[rg];
+#pragma unroll
+    for (int mi = 0; mi < 16; ++mi)
+#pragma unroll
+      for (int rg = 0; rg < 4; ++rg) asm volatile("" : "+a"(acc[mi][rg]));
+  };
+  for (int c = 0; c < nst; ++c) {
+    step(c, W0, W1, W2);
+    W0 = W1;
+    W1 = W2;
+  }
+  __builtin_amdgcn_s_waitcnt(0);
   mfma_drain();
-  const int j = lane & 15, gq = lane >> 4;
   float* part = g.part + (long long)s * M * H;
+  if (wrows) {
 #pragma unroll
-  for (int mi = 0; mi < MT; ++mi) {
+    for (int mi = 0; mi < 16; ++mi) {
 #pragma unroll
-    for (int rr = 0; rr < 4; ++rr) {
-      const int t = t0 + 16 * MT * mq + 16 * mi + 4 * gq + rr;
-      if (t < M) {
+      for (int r = 0; r < 4; ++r) {
+        const int t = t0 + 16 * mi + 4 * q + r;
+        if (t < M) {
 #pragma unroll
-        for (int ni = 0; ni < 8; ++ni) part[(long long)t * H + o0 + 128 * nh + 16 * ni + j] = acc[mi][ni][rr];
+          for (int rg = 0; rg < 4; ++rg) part[(long long)t * H + o0 + 16u * (uint32_t)rg] = acc[mi][rg][r];
+        }
       }
     }
   }
@@ -424,8 +674,9 @@ using DgFn = void (*)(DenseGuardArgs);
 // [dq][MT - 1 of the 64 MT-token tile]
 const DgFn kDgGu[2][4] = {{k_dg_gu<false, 1>, k_dg_gu<false, 2>, k_dg_gu<false, 3>, k_dg_gu<false, 4>},
                           {k_dg_gu<true, 1>, k_dg_gu<true, 2>, k_dg_gu<true, 3>, k_dg_gu<true, 4>}};
-const DgFn kDgDown[2][4] = {{k_dg_down<false, 1>, k_dg_down<false, 2>, k_dg_down<false, 3>, k_dg_down<false, 4>},
-                            {k_dg_down<true, 1>, k_dg_down<true, 2>, k_dg_down<true, 3>, k_dg_down<true, 4>}};
+// [dq][host copies]
+const DgFn kDgDown[2][2] = {{k_dg_down<false, false>, k_dg_down<false, true>},
+                            {k_dg_down<true, false>, k_dg_down<true, true>}};
 
 // Token tiles: whole 256-token tiles, then the rest of the prompt in the
 // smallest tile of 64, 128 or 192 tokens that holds it (a 256-token tile would
@@ -451,20 +702,37 @@ void dg_set_lds() {
       for (int m = 0; m < 4; ++m) {
         (void)hipFuncSetAttribute(reinterpret_cast<const void*>(kDgGu[q][m]),
                                   hipFuncAttributeMaxDynamicSharedMemorySize, (int)kDgLds);
-        (void)hipFuncSetAttribute(reinterpret_cast<const void*>(kDgDown[q][m]),
-                                  hipFuncAttributeMaxDynamicSharedMemorySize, (int)kDgLds);
       }
+    for (int q = 0; q < 2; ++q)
+      for (int h = 0; h < 2; ++h)
+        (void)hipFuncSetAttribute(reinterpret_cast<const void*>(kDgDown[q][h]),
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, (int)kDnLdsMax);
   });
 }
 
 }  // namespace
 
+int dense_down_refs(int NB, int S) { return 2 * ((NB / 2 + S - 1) / S); }
+
+bool dense_down_fits(const DecodeArgs& d, int S) {
+  const long long lim = (1LL << 31) - 1;
+  const int ab = d.dq ? 1 : 4;
+  if (d.NB % 4 != 0 || S < 1) return false;
+  if (kDnRefs + 4LL * dense_down_refs(d.NB, S) > (long long)kDnLdsMax) return false;
+  if (dn_extent(d.down, d.n_slots, d.H, false, 16) > lim || dn_extent(d.down, d.n_slots, d.H, true, ab) > lim)
+    return false;
+  return d.host_down.packed == nullptr ||
+         (dn_extent(d.down, d.NB, d.H, false, 16) <= lim && dn_extent(d.down, d.NB, d.H, true, ab) <= lim);
+}
+
 void launch_dense_down(const DenseGuardArgs& g, hipStream_t st) {
   dg_set_lds();
-  dg_token_tiles(g, [&](const DenseGuardArgs& a, int mt_idx, int tiles) {
-    kDgDown[a.d.dq ? 1 : 0][mt_idx]<<<dim3((unsigned)(a.d.H / 256 * a.S), (unsigned)tiles), dim3(kDgThreads), kDgLds,
-                                      st>>>(a);
-  });
+  DenseGuardArgs a = g;
+  a.t_base = 0;
+  const int RT = (g.d.H + kDnRows - 1) / kDnRows, TT = (g.M + kDnTok - 1) / kDnTok;
+  const size_t lds = kDnRefs + 4u * (size_t)dense_down_refs(g.d.NB, g.S);
+  const bool host = g.d.host_down.packed != nullptr;
+  kDgDown[g.d.dq ? 1 : 0][host ? 1 : 0]<<<dim3((unsigned)(RT * TT * g.S)), dim3(kDnThreads), lds, st>>>(a);
   const long long n = (long long)g.M * g.d.H;
   k_dg_fin<<<dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st>>>(g);
 }

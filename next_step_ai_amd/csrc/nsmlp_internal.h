@@ -398,6 +398,10 @@ __device__ __forceinline__ uint4 buf_ld16(rsrc_t r, uint32_t voff, uint32_t soff
   const u32x4_t t = __builtin_amdgcn_raw_buffer_load_b128(r, (int)voff, (int)soff, kNontemporal);
   return make_uint4(t.x, t.y, t.z, t.w);
 }
+__device__ __forceinline__ uint2 buf_ld8(rsrc_t r, uint32_t voff, uint32_t soff) {
+  const u32x2_t t = __builtin_amdgcn_raw_buffer_load_b64(r, (int)voff, (int)soff, kNontemporal);
+  return make_uint2(t.x, t.y);
+}
 __device__ __forceinline__ float buf_ldf(rsrc_t r, uint32_t voff, uint32_t soff) {
   return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, (int)voff, (int)soff, kNontemporal));
 }
@@ -418,6 +422,41 @@ __device__ __forceinline__ float buf_ldfc(rsrc_t r, uint32_t voff, uint32_t soff
 constexpr uint32_t kOffNone = 0x80000000u;  // an offset past every extent: the load returns zeros
 __device__ __forceinline__ uint32_t buf_ldu16(rsrc_t r, uint32_t voff, uint32_t soff) {
   return (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(r, (int)voff, (int)soff, kNontemporal);
+}
+
+// Buffer loads into LDS (lane l's bytes at LDS address base + 16 l, or 4 l
+// for the dword and byte forms; the byte form zero-extends to a dword).
+// Written as asm: the compiler then neither counts them in its own wait
+// counts (which only makes those waits longer than needed, never shorter)
+// nor waits for them before every later LDS read; the kernel waits for
+// them itself.  `base` is the wave's LDS byte address (uniform).
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(uintptr_t)p);
+}
+__device__ __forceinline__ void ld_lds16(rsrc_t r, const void* lds, uint32_t voff) {
+  asm volatile("s_mov_b32 m0, %1\n\tbuffer_load_dwordx4 %0, %2, 0 offen lds" ::"v"(voff), "s"(lds_addr(lds)), "s"(r)
+               : "memory", "m0");
+}
+// Same, with a uniform byte offset added to every lane's (an SGPR operand).
+__device__ __forceinline__ void ld_lds16s(rsrc_t r, const void* lds, uint32_t voff, uint32_t soff) {
+  asm volatile("s_mov_b32 m0, %1\n\tbuffer_load_dwordx4 %0, %2, %3 offen lds" ::"v"(voff), "s"(lds_addr(lds)), "s"(r),
+               "s"(soff)
+               : "memory", "m0");
+}
+__device__ __forceinline__ void ld_lds4(rsrc_t r, const void* lds, uint32_t voff) {
+  asm volatile("s_mov_b32 m0, %1\n\tbuffer_load_dword %0, %2, 0 offen lds" ::"v"(voff), "s"(lds_addr(lds)), "s"(r)
+               : "memory", "m0");
+}
+__device__ __forceinline__ void ld_lds1(rsrc_t r, const void* lds, uint32_t voff) {
+  asm volatile("s_mov_b32 m0, %1\n\tbuffer_load_ubyte %0, %2, 0 offen lds" ::"v"(voff), "s"(lds_addr(lds)), "s"(r)
+               : "memory", "m0");
+}
+// Workgroup barrier after this wave's LDS accesses: waits for the LDS
+// counter only (no memory fence, no wait for vector loads in flight).
+__device__ __forceinline__ void lds_barrier() {
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
 }
 
 // ------------------------------------------------------------------ top-k --
@@ -710,6 +749,10 @@ struct DenseGuardArgs {
 void launch_dense_guard(const DenseGuardArgs& g, hipStream_t s);
 // The down GEMM and the final sum alone, over g.act (the prefill's dense path).
 void launch_dense_down(const DenseGuardArgs& g, hipStream_t s);
+// Whether the down GEMM takes this table with S block ranges: every slot and
+// host copy addressable by 31-bit offsets, the range's block references in LDS.
+bool dense_down_fits(const DecodeArgs& d, int S);
+int dense_down_refs(int NB, int S);
 
 // Dense NF4 rows (the LM head): y[t][o] = sum_i W[o][i] x[t][i] over a
 // row-major [out][in] NF4 matrix, in % 32 == 0, in <= 16384.

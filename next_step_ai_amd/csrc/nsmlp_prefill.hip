@@ -204,35 +204,6 @@ static_assert(kGuTok * 64 * 4 <= kGuNS * kGuXBytes, "gate/up sums must fit the t
 static_assert(kGuTok * 16 == 2 * kPfThreads && 64 * 16 == 2 * kPfThreads && kGuAux == kPfThreads,
               "loads per chunk: two token pieces, two weight dwords, one absmax entry per thread");
 
-// Buffer loads into LDS (lane l's bytes at LDS address base + 16 l, or 4 l
-// for the dword and byte forms; the byte form zero-extends to a dword).
-// Written as asm: the compiler then neither counts them in its own wait
-// counts (which only makes those waits longer than needed, never shorter)
-// nor waits for them before every later LDS read; the kernel waits for
-// them itself.  `base` is the wave's LDS byte address (uniform).
-__device__ __forceinline__ uint32_t lds_addr(const void* p) {
-  return (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(uintptr_t)p);
-}
-__device__ __forceinline__ void ld_lds16(rsrc_t r, const void* lds, uint32_t voff) {
-  asm volatile("s_mov_b32 m0, %1\n\tbuffer_load_dwordx4 %0, %2, 0 offen lds" ::"v"(voff), "s"(lds_addr(lds)), "s"(r)
-               : "memory", "m0");
-}
-__device__ __forceinline__ void ld_lds4(rsrc_t r, const void* lds, uint32_t voff) {
-  asm volatile("s_mov_b32 m0, %1\n\tbuffer_load_dword %0, %2, 0 offen lds" ::"v"(voff), "s"(lds_addr(lds)), "s"(r)
-               : "memory", "m0");
-}
-__device__ __forceinline__ void ld_lds1(rsrc_t r, const void* lds, uint32_t voff) {
-  asm volatile("s_mov_b32 m0, %1\n\tbuffer_load_ubyte %0, %2, 0 offen lds" ::"v"(voff), "s"(lds_addr(lds)), "s"(r)
-               : "memory", "m0");
-}
-// Workgroup barrier after this wave's LDS accesses (no memory fence: the
-// loads into LDS are waited for explicitly).
-__device__ __forceinline__ void pf_barrier() {
-  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-  __builtin_amdgcn_s_barrier();
-  asm volatile("" ::: "memory");
-}
-
 template <bool DQ>
 __global__ void __launch_bounds__(kPfThreads, 4) k_pf_gu(PrefillArgs p) {  // 4 waves per SIMD: two workgroups per CU
   extern __shared__ __attribute__((aligned(16))) uint8_t pf_lds[];
@@ -335,7 +306,7 @@ __global__ void __launch_bounds__(kPfThreads, 4) k_pf_gu(PrefillArgs p) {  // 4 
         asm volatile("s_waitcnt vmcnt(6)" ::: "memory");  // (kGuNS - 2) chunks x 6 loads
       else
         asm volatile("s_waitcnt vmcnt(5)" ::: "memory");  // (kGuNS - 2) chunks x 5 loads
-      pf_barrier();  // also: every wave is done with chunk c - 1, whose stage the next issue refills
+      lds_barrier();  // also: every wave is done with chunk c - 1, whose stage the next issue refills
       issue(c + kGuNS - 1);
       const int st = c % kGuNS;
       half8_t bf[2];

@@ -83,14 +83,6 @@ __device__ __forceinline__ uint32_t lane_value(uint32_t v, int lane) {
   return (uint32_t)__builtin_amdgcn_readlane((int)v, lane);
 }
 
-// Wait for this wave's LDS traffic, then the workgroup barrier.  Loads from
-// global memory that are in flight stay in flight.
-__device__ __forceinline__ void lds_barrier() {
-  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-  __builtin_amdgcn_s_barrier();
-  asm volatile("" ::: "memory");
-}
-
 // Replicated pair table, filled by 512 threads in 8 passes of one 16-byte LDS
 // write each: pass ps writes entry e = 32 ps + tid / 16, copies 4 (tid % 16)
 // .. +3 (copies 0..31 decode code_a, 32..63 code_b).  The entry's low half is
