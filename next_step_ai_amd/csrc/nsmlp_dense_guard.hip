@@ -400,7 +400,9 @@ struct DnW {
   int ok;  // the lane's block is valid (its absmax is forced to zero otherwise)
 };
 
-template <bool DQ, bool HOST>
+// MT token groups of 16 per tile (16: 256 tokens; 4, 8 or 12 for the tokens
+// past the last whole 256-token tile).
+template <bool DQ, bool HOST, int MT>
 __global__ void __launch_bounds__(kDnThreads, 1) k_dg_down(DenseGuardArgs g) {
   extern __shared__ __attribute__((aligned(16))) uint8_t dn_lds[];  // no static LDS: dn_lds is LDS address 0
   const DecodeArgs& d = g.d;
@@ -415,7 +417,7 @@ __global__ void __launch_bounds__(kDnThreads, 1) k_dg_down(DenseGuardArgs g) {
   int idx = (int)blockIdx.x;
   if ((N & 7) == 0) idx = (idx & 7) * (N >> 3) + (idx >> 3);
   const int rt = idx % RT, combo = idx / RT, s = combo % S, tt = combo / S;
-  const int t0 = g.t_base + tt * kDnTok;
+  const int t0 = g.t_base + tt * 16 * MT;
   const int G = NB / 2;  // 2-block steps
   const int g_lo = (int)((long long)s * G / S), g_hi = (int)((long long)(s + 1) * G / S);
   const int nst = g_hi - g_lo, b_lo = 2 * g_lo;
@@ -514,7 +516,7 @@ __global__ void __launch_bounds__(kDnThreads, 1) k_dg_down(DenseGuardArgs g) {
     const uint32_t xo = xrow + (uint32_t)(64 * (b_lo + 2 * c));
     const uint32_t sb = kDnTab + (uint32_t)(c & 1) * kDnStage;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
+    for (int i = 0; i < MT / 2; ++i) {  // 16 MT rows of 128 bytes: MT / 2 loads per wave
       const uint32_t xi = 32 * i < tlim ? xo : kOffNone;
       ld_lds16s(rx, dn_lds + sb + (32 * i + 8 * wave) * 128, xi, 64u * (uint32_t)i * (uint32_t)I);
     }
@@ -523,9 +525,9 @@ __global__ void __launch_bounds__(kDnThreads, 1) k_dg_down(DenseGuardArgs g) {
   // 256 accumulators, kept in AGPRs: pinned there at the start and after
   // every step (otherwise part of them crosses the loop in VGPRs, which the
   // loads in flight and the decode need)
-  float4_t acc[16][4];
+  float4_t acc[MT][4];
 #pragma unroll
-  for (int mi = 0; mi < 16; ++mi)
+  for (int mi = 0; mi < MT; ++mi)
 #pragma unroll
     for (int rg = 0; rg < 4; ++rg) {
       acc[mi][rg] = float4_t{0.0f, 0.0f, 0.0f, 0.0f};
@@ -536,12 +538,12 @@ __global__ void __launch_bounds__(kDnThreads, 1) k_dg_down(DenseGuardArgs g) {
   for (int i = 0; i < 4; ++i) ad[i] = (uint32_t)(lane & (kDnCopies - 1)) * 8u;
   // A fragment (token group mi, MFMA step j) of step c: token row 16 mi + n,
   // piece 4 (q % 2) + 2 (q / 2) + j, in slot piece ^ ((row / 2) % 8)
-  auto read_a = [&](half8_t (&a)[8], int c, int j, int h) {
+  auto read_a = [&](half8_t (&a)[MT / 2], int c, int j, int h) {
     const uint32_t piece = (uint32_t)(4 * qb + 2 * qh + j);
     const uint32_t base = kDnTab + (uint32_t)(c & 1) * kDnStage + (uint32_t)n * 128u +
-                          ((piece ^ (uint32_t)((n >> 1) & 7)) << 4) + (uint32_t)h * 16384u;
+                          ((piece ^ (uint32_t)((n >> 1) & 7)) << 4) + (uint32_t)h * 1024u * MT;
 #pragma unroll
-    for (int mi = 0; mi < 8; ++mi) a[mi] = lds_ld_h8(base + (uint32_t)mi * 2048u);
+    for (int mi = 0; mi < MT / 2; ++mi) a[mi] = lds_ld_h8(base + (uint32_t)mi * 2048u);
   };
   auto am_of = [&](const DnW& W, float (&am)[4]) {
 #pragma unroll
@@ -559,15 +561,15 @@ __global__ void __launch_bounds__(kDnThreads, 1) k_dg_down(DenseGuardArgs g) {
 #pragma unroll
     for (int rg = 0; rg < 4; ++rg) b[rg] = dn_finish8(pr[rg], am[rg]);
   };
-  // 32 MFMAs: token groups 8 h .. 8 h + 7 x the 4 row groups
-  auto mfma_unit = [&](const half8_t (&a)[8], const half8_t (&b)[4], int h) {
+  // 2 MT MFMAs: token groups MT / 2 h .. + MT / 2 - 1 x the 4 row groups
+  auto mfma_unit = [&](const half8_t (&a)[MT / 2], const half8_t (&b)[4], int h) {
 #pragma unroll
     for (int rg = 0; rg < 4; ++rg)
 #pragma unroll
-      for (int mi = 0; mi < 8; ++mi) acc[8 * h + mi][rg] = mfma16(a[mi], b[rg], acc[8 * h + mi][rg]);
+      for (int mi = 0; mi < MT / 2; ++mi) acc[MT / 2 * h + mi][rg] = mfma16(a[mi], b[rg], acc[MT / 2 * h + mi][rg]);
     // each MFMA followed by an LDS read and a VALU op of the work ahead
 #pragma unroll
-    for (int i = 0; i < 32; ++i) {
+    for (int i = 0; i < 2 * MT; ++i) {
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
       __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
       __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);
@@ -589,7 +591,7 @@ __global__ void __launch_bounds__(kDnThreads, 1) k_dg_down(DenseGuardArgs g) {
   // reads step c + 1's first A fragments.  Three weight register sets:
   // decoded, arrived, in flight (moved down one set per step).
   DnW W0, W1, W2;
-  half8_t ax[8], ay[8], b0[4], b1[4];
+  half8_t ax[MT / 2], ay[MT / 2], b0[4], b1[4];
   DnPairs pr[4];
   float am_c[4], am_n[4];
   issue_w(W0, 0);
@@ -629,7 +631,7 @@ __global__ void __launch_bounds__(kDnThreads, 1) k_dg_down(DenseGuardArgs g) {
 #pragma unroll
     for (int rg = 0; rg < 4; ++rg) am_c[rg] = am_n[rg];
 #pragma unroll
-    for (int mi = 0; mi < 16; ++mi)
+    for (int mi = 0; mi < MT; ++mi)
 #pragma unroll
       for (int rg = 0; rg < 4; ++rg) asm volatile("" : "+a"(acc[mi][rg]));
   };
@@ -643,7 +645,7 @@ __global__ void __launch_bounds__(kDnThreads, 1) k_dg_down(DenseGuardArgs g) {
   float* part = g.part + (long long)s * M * H;
   if (wrows) {
 #pragma unroll
-    for (int mi = 0; mi < 16; ++mi) {
+    for (int mi = 0; mi < MT; ++mi) {
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int t = t0 + 16 * mi + 4 * q + r;
@@ -674,9 +676,12 @@ using DgFn = void (*)(DenseGuardArgs);
 // [dq][MT - 1 of the 64 MT-token tile]
 const DgFn kDgGu[2][4] = {{k_dg_gu<false, 1>, k_dg_gu<false, 2>, k_dg_gu<false, 3>, k_dg_gu<false, 4>},
                           {k_dg_gu<true, 1>, k_dg_gu<true, 2>, k_dg_gu<true, 3>, k_dg_gu<true, 4>}};
-// [dq][host copies]
-const DgFn kDgDown[2][2] = {{k_dg_down<false, false>, k_dg_down<false, true>},
-                            {k_dg_down<true, false>, k_dg_down<true, true>}};
+// [dq][host copies][MT / 4 - 1 of the 16 MT-token tile]
+const DgFn kDgDown[2][2][4] = {
+    {{k_dg_down<false, false, 4>, k_dg_down<false, false, 8>, k_dg_down<false, false, 12>, k_dg_down<false, false, 16>},
+     {k_dg_down<false, true, 4>, k_dg_down<false, true, 8>, k_dg_down<false, true, 12>, k_dg_down<false, true, 16>}},
+    {{k_dg_down<true, false, 4>, k_dg_down<true, false, 8>, k_dg_down<true, false, 12>, k_dg_down<true, false, 16>},
+     {k_dg_down<true, true, 4>, k_dg_down<true, true, 8>, k_dg_down<true, true, 12>, k_dg_down<true, true, 16>}}};
 
 // Token tiles: whole 256-token tiles, then the rest of the prompt in the
 // smallest tile of 64, 128 or 192 tokens that holds it (a 256-token tile would
@@ -705,8 +710,9 @@ void dg_set_lds() {
       }
     for (int q = 0; q < 2; ++q)
       for (int h = 0; h < 2; ++h)
-        (void)hipFuncSetAttribute(reinterpret_cast<const void*>(kDgDown[q][h]),
-                                  hipFuncAttributeMaxDynamicSharedMemorySize, (int)kDnLdsMax);
+        for (int m = 0; m < 4; ++m)
+          (void)hipFuncSetAttribute(reinterpret_cast<const void*>(kDgDown[q][h][m]),
+                                    hipFuncAttributeMaxDynamicSharedMemorySize, (int)kDnLdsMax);
   });
 }
 
@@ -727,12 +733,21 @@ bool dense_down_fits(const DecodeArgs& d, int S) {
 
 void launch_dense_down(const DenseGuardArgs& g, hipStream_t st) {
   dg_set_lds();
-  DenseGuardArgs a = g;
-  a.t_base = 0;
-  const int RT = (g.d.H + kDnRows - 1) / kDnRows, TT = (g.M + kDnTok - 1) / kDnTok;
+  const int RT = (g.d.H + kDnRows - 1) / kDnRows;
   const size_t lds = kDnRefs + 4u * (size_t)dense_down_refs(g.d.NB, g.S);
   const bool host = g.d.host_down.packed != nullptr;
-  kDgDown[g.d.dq ? 1 : 0][host ? 1 : 0]<<<dim3((unsigned)(RT * TT * g.S)), dim3(kDnThreads), lds, st>>>(a);
+  // whole 256-token tiles, then the rest in the smallest 64-, 128- or
+  // 192-token tile that holds it (per token the same sums, bit for bit)
+  const int full = g.M / kDnTok, rest = g.M - full * kDnTok;
+  DenseGuardArgs a = g;
+  if (full > 0) {
+    a.t_base = 0;
+    kDgDown[g.d.dq ? 1 : 0][host ? 1 : 0][3]<<<dim3((unsigned)(RT * full * g.S)), dim3(kDnThreads), lds, st>>>(a);
+  }
+  if (rest > 0) {
+    a.t_base = full * kDnTok;
+    kDgDown[g.d.dq ? 1 : 0][host ? 1 : 0][(rest + 63) / 64 - 1]<<<dim3((unsigned)(RT * g.S)), dim3(kDnThreads), lds, st>>>(a);
+  }
   const long long n = (long long)g.M * g.d.H;
   k_dg_fin<<<dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st>>>(g);
 }
