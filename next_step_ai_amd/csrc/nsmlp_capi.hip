@@ -108,7 +108,7 @@ DecodeWs decode_ws_layout(int H, int k) {
 }
 
 struct RouteWs {
-  size_t lat16, scores, total;
+  size_t lat16, scores, lat_part, total;
 };
 
 RouteWs route_ws_layout(size_t base, int rows, int H, int R, int NB) {
@@ -118,6 +118,8 @@ RouteWs route_ws_layout(size_t base, int rows, int H, int R, int NB) {
   off += align_up((size_t)rows * R * sizeof(uint16_t));
   w.scores = off;
   off += align_up((size_t)rows * NB * sizeof(uint16_t));
+  w.lat_part = off;
+  if (rows < kLatSplitRows) off += align_up((size_t)rows * R * kLatParts * 3 * sizeof(double));
   w.total = off;
   return w;
 }
@@ -234,6 +236,7 @@ int fill_route(RouteArgs& r, const void* x, int rows, int H, const void* enc_w, 
   r.lat16 = (uint16_t*)(base + L.lat16);
   r.scores = (uint16_t*)(base + L.scores);
   r.status = (int*)(base + kStatusOff);
+  r.lat_part = rows < kLatSplitRows ? (double*)(base + L.lat_part) : nullptr;
   return NSMLP_OK;
 }
 

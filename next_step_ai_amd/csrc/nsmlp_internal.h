@@ -835,7 +835,13 @@ struct RouteArgs {
   uint16_t* lat16;         // [rows][R] fp16 latent
   uint16_t* scores;        // [rows][NB]
   int* status;
+  // fewer than kLatSplitRows rows: the latent's exact sums in kLatParts
+  // column ranges [rows][R][kLatParts] x (a0, a1, a2), merged and rounded by
+  // the scores kernel; nullptr otherwise
+  double* lat_part;
 };
+constexpr int kLatSplitRows = 8;
+constexpr int kLatParts = 4;
 
 void launch_route(const RouteArgs& a, hipStream_t s);
 // The latent and score kernels only (the top-k runs inside the decode).

@@ -3,6 +3,9 @@
 // RT:4311-4352), as three gfx950 kernels:
 //   1. latent          : one workgroup per latent row: exact fp16 dot product
 //                        of x with the enc_w row (Exact3), one fp16 rounding;
+//                        for fewer than 8 tokens one workgroup per 1/4 of a
+//                        row (k_latent_part), the parts added and rounded by
+//                        the scores kernel;
 //                        from 8 tokens on, one workgroup per 8 x 8 tile of
 //                        latent rows and tokens (k_latent_tiled).
 //   2. scores          : fp16 latent (+ the basis_top_k mask) -> exact score
@@ -169,10 +172,72 @@ __global__ void __launch_bounds__(kLtThreads) k_latent_tiled(RouteArgs a) {
   if (r < a.R && t < a.rows) a.lat16[(long long)t * a.R + r] = exact_to_f16(sum);
 }
 
+// Fewer than kLatSplitRows rows: one workgroup per (latent row, column range,
+// token), kLatParts ranges per row, so a decode token's R rows fill the chip
+// (R kLatParts workgroups).  Each writes the exact partial sum of its range
+// (Exact3 parts; the bias goes into range 0); k_scores adds the parts (exact
+// in any grouping) and rounds once, so the fp16 latent equals k_latent's.
+constexpr int kLpThreads = 256;
+static_assert(kLtTok == kLatSplitRows, "the tiled latent takes the rows the split latent does not");
+
+template <bool kVec>
+__global__ void __launch_bounds__(kLpThreads) k_latent_part(RouteArgs a) {
+  const int r = blockIdx.x, p = blockIdx.y, row = blockIdx.z;
+  const int tid = threadIdx.x, wave = tid / kWave, lane = tid % kWave;
+  const uint16_t* __restrict__ x = a.x + (long long)row * a.H;
+  const uint16_t* __restrict__ w = a.enc_w + (long long)r * a.H;
+  const int span = (a.H + kLatParts * 8 - 1) / (kLatParts * 8) * 8;  // columns per range, a multiple of 8
+  const int c_lo = p * span, c_hi = min(a.H, c_lo + span);
+  // the bias goes out with the first loads (an unconditional load: x[0]
+  // stands in when there is no bias)
+  const bool has_b = a.enc_b != nullptr;
+  const uint16_t eb = (has_b ? a.enc_b : x)[has_b ? r : 0];
+  Exact3 acc = exact_zero();
+  if (kVec) {
+#pragma unroll 2
+    for (int c0 = c_lo + tid * 8; c0 < c_hi; c0 += kLpThreads * 8) {
+      const uint4 xv = *reinterpret_cast<const uint4*>(x + c0);
+      const uint4 wv = *reinterpret_cast<const uint4*>(w + c0);
+      const uint32_t xs[4] = {xv.x, xv.y, xv.z, xv.w};
+      const uint32_t ws[4] = {wv.x, wv.y, wv.z, wv.w};
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        exact_add(acc, (double)(h2f((uint16_t)(xs[q] & 0xFFFFu)) * h2f((uint16_t)(ws[q] & 0xFFFFu))));
+        exact_add(acc, (double)(h2f((uint16_t)(xs[q] >> 16)) * h2f((uint16_t)(ws[q] >> 16))));
+      }
+    }
+  } else {
+    for (int c = c_lo + tid; c < c_hi; c += kLpThreads) exact_add(acc, (double)(h2f(x[c]) * h2f(w[c])));
+  }
+  if (tid == 0 && has_b && p == 0) exact_add(acc, (double)h2f(eb));
+  acc = wave_sum_exact(acc);
+  __shared__ double red[kLpThreads / kWave][3];
+  if (lane == 0) {
+    red[wave][0] = acc.a0;
+    red[wave][1] = acc.a1;
+    red[wave][2] = acc.a2;
+  }
+  __syncthreads();
+  if (tid < 3) {  // part tid of the Exact3 sum: the wave sums' parts add exactly
+    double v = 0.0;
+#pragma unroll
+    for (int v4 = 0; v4 < kLpThreads / kWave; ++v4) v += red[v4][tid];
+    a.lat_part[(((long long)row * a.R + r) * kLatParts + p) * 3 + tid] = v;
+  }
+}
+
 void launch_latent(const RouteArgs& a, hipStream_t s) {
   if (a.vec && a.rows >= kLtTok) {
     const dim3 g((a.R + kLtRows - 1) / kLtRows, (a.rows + kLtTok - 1) / kLtTok);
     hipLaunchKernelGGL(k_latent_tiled, g, dim3(kLtThreads), 0, s, a);
+    return;
+  }
+  if (a.lat_part != nullptr) {
+    const dim3 g(a.R, kLatParts, a.rows);
+    if (a.vec)
+      hipLaunchKernelGGL(k_latent_part<true>, g, dim3(kLpThreads), 0, s, a);
+    else
+      hipLaunchKernelGGL(k_latent_part<false>, g, dim3(kLpThreads), 0, s, a);
     return;
   }
   const dim3 g1(a.R, a.rows);
@@ -220,7 +285,21 @@ __global__ void __launch_bounds__(kScoreThreads) k_scores(RouteArgs a) {
     const int r = part + i * kScoreLanes;
     wv[i] = r < a.R ? w[r] : (uint16_t)0;
   }
-  for (int i = tid; i < nrow * a.R; i += kScoreThreads) lat16[i] = a.lat16[(long long)row0 * a.R + i];
+  if (a.lat_part != nullptr) {
+    // the latent from its range parts: add them (exact) and round once;
+    // workgroup 0 also keeps the fp16 latent in the workspace
+    for (int i = tid; i < nrow * a.R; i += kScoreThreads) {
+      const double* pp = a.lat_part + ((long long)row0 * a.R + i) * (kLatParts * 3);
+      Exact3 e = exact_zero();
+#pragma unroll
+      for (int q = 0; q < kLatParts; ++q) exact_merge(e, Exact3{pp[3 * q], pp[3 * q + 1], pp[3 * q + 2]});
+      const uint16_t v = exact_to_f16(e);
+      lat16[i] = v;
+      if (blockIdx.x == 0) a.lat16[(long long)row0 * a.R + i] = v;
+    }
+  } else {
+    for (int i = tid; i < nrow * a.R; i += kScoreThreads) lat16[i] = a.lat16[(long long)row0 * a.R + i];
+  }
   __syncthreads();
   // basis_top_k mask over |latent| per token (RT:4233-4238); ties keep the
   // lower index
