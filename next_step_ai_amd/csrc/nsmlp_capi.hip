@@ -230,6 +230,7 @@ int fill_route(RouteArgs& r, const void* x, int rows, int H, const void* enc_w, 
   r.sorted = (flags & NSMLP_ROUTE_SORTED) ? 1 : 0;
   r.k = k;
   r.vec = (H % 8 == 0) && aligned16(x) && aligned16(enc_w);
+  r.svec = (R % 8 == 0) && aligned16(score_w);
   r.sel = sel;
   r.latent_out = (uint16_t*)latent_out;
   r.scores_out = (uint16_t*)scores_out;

@@ -386,6 +386,37 @@ __device__ __forceinline__ void mfma_drain() {
 // order decides which waits drain the weight stream).
 __device__ __forceinline__ void sched_fence() { __builtin_amdgcn_sched_barrier(0); }
 
+// Kernel arguments are read from memory (the kernarg segment), and the
+// compiler places each field's load where the field is first used, so a field
+// first used after a global load costs a round trip of its own.  Reading every
+// 64-byte line of the arguments at the start of a kernel (one batch of scalar
+// loads, data discarded) puts them in the scalar cache; the compiler's own
+// loads of the fields then hit it wherever they are placed.
+template <int kBytes>
+__device__ __forceinline__ void kernarg_warm() {
+  static_assert(kBytes >= 64 && kBytes <= 4096 && kBytes % 4 == 0, "argument block size");
+  // whole 64-byte pieces, then one piece ending at the block's end (it
+  // overlaps the previous one): no load reads past the argument block
+  constexpr int kFull = kBytes / 64;
+  constexpr int kTail = kBytes % 64 != 0 ? kBytes - 64 : -1;
+  const auto kp = __builtin_amdgcn_kernarg_segment_ptr();
+  typedef int v16i __attribute__((ext_vector_type(16)));
+  v16i d;
+  asm volatile(
+      ".set .Lnsmlp_kw, 0\n\t"
+      ".rept %2\n\t"
+      "s_load_dwordx16 %0, %1, .Lnsmlp_kw\n\t"
+      ".set .Lnsmlp_kw, .Lnsmlp_kw + 64\n\t"
+      ".endr\n\t"
+      ".if %3 >= 0\n\t"
+      "s_load_dwordx16 %0, %1, %3\n\t"
+      ".endif\n\t"
+      "s_waitcnt lgkmcnt(0)"
+      : "=&s"(d)
+      : "s"(kp), "i"(kFull), "i"(kTail)
+      : "memory");
+}
+
 // Raw buffer descriptors (gfx9 family dword format) and nontemporal loads.
 typedef __amdgpu_buffer_rsrc_t rsrc_t;
 constexpr int kRsrcWord3 = 0x00020000;
@@ -828,6 +859,7 @@ struct RouteArgs {
   const uint16_t* dbn;     // [NB] fp16 or nullptr
   int NB, legacy_abs, sorted, k;
   int vec;                 // 16-byte loads allowed for x / enc_w
+  int svec;                // 16-byte loads allowed for score_w rows (R % 8 == 0, aligned)
   int32_t* sel;            // [rows][k]
   uint16_t* latent_out;    // [rows][R] or nullptr
   uint16_t* scores_out;    // [rows][NB] or nullptr

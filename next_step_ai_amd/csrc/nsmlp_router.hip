@@ -182,6 +182,7 @@ static_assert(kLtTok == kLatSplitRows, "the tiled latent takes the rows the spli
 
 template <bool kVec>
 __global__ void __launch_bounds__(kLpThreads) k_latent_part(RouteArgs a) {
+  kernarg_warm<sizeof(RouteArgs)>();
   const int r = blockIdx.x, p = blockIdx.y, row = blockIdx.z;
   const int tid = threadIdx.x, wave = tid / kWave, lane = tid % kWave;
   const uint16_t* __restrict__ x = a.x + (long long)row * a.H;
@@ -262,7 +263,18 @@ __host__ __device__ inline int scores_tokens_per_wg(int rows, int R) {
   return rows >= kScTok && R * kScTok <= 4 * kScoreThreads ? kScTok : 1;
 }
 
+// Basis term r of prefetch slot i of a lane (lane `part` of a block's 8).
+// kVecW: 16-byte score_w rows; the lane takes terms 8 part .. 8 part + 7 of
+// each group of 64 (one 16-byte load per group).  Otherwise every 8th term.
+// Either way the 8 lanes cover terms 0 .. 8 kPre - 1 once.
+template <bool kVecW>
+__device__ __forceinline__ int score_term(int part, int i) {
+  return kVecW ? (i / 8) * 64 + part * 8 + (i % 8) : part + i * kScoreLanes;
+}
+
+template <bool kVecW>
 __global__ void __launch_bounds__(kScoreThreads) k_scores(RouteArgs a) {
+  kernarg_warm<sizeof(RouteArgs)>();
   const int tpw = scores_tokens_per_wg(a.rows, a.R);  // tokens of this workgroup
   const int row0 = (int)blockIdx.y * tpw;
   const int nrow = min(tpw, a.rows - row0);
@@ -278,12 +290,26 @@ __global__ void __launch_bounds__(kScoreThreads) k_scores(RouteArgs a) {
   const bool has_b = !a.legacy_abs && a.score_b != nullptr, has_n = a.dbn != nullptr;
   const uint16_t sb = (has_b ? a.score_b : a.score_w)[has_b ? jj : 0];
   const uint16_t sn = (has_n ? a.dbn : a.score_w)[has_n ? jj : 0];
+  // Every load is unconditional (clamped offsets, the value zeroed after the
+  // load): a load under a condition would be waited for on its own.
   constexpr int kPre = 16;  // prefetched terms per lane (R <= 128)
   uint16_t wv[kPre];
+  if constexpr (kVecW) {
 #pragma unroll
-  for (int i = 0; i < kPre; ++i) {
-    const int r = part + i * kScoreLanes;
-    wv[i] = r < a.R ? w[r] : (uint16_t)0;
+    for (int g = 0; g < kPre / 8; ++g) {
+      const int r0 = g * 64 + part * 8;  // R % 8 == 0: all 8 terms or none
+      const uint4 t = *reinterpret_cast<const uint4*>(w + (r0 < a.R ? r0 : 0));
+      const uint32_t tw[4] = {t.x, t.y, t.z, t.w};
+#pragma unroll
+      for (int m = 0; m < 8; ++m) wv[8 * g + m] = r0 < a.R ? (uint16_t)(tw[m / 2] >> (16 * (m % 2))) : (uint16_t)0;
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < kPre; ++i) {
+      const int r = part + i * kScoreLanes;
+      const uint16_t t = w[r < a.R ? r : 0];
+      wv[i] = r < a.R ? t : (uint16_t)0;
+    }
   }
   if (a.lat_part != nullptr) {
     // the latent from its range parts: add them (exact) and round once;
@@ -331,7 +357,7 @@ __global__ void __launch_bounds__(kScoreThreads) k_scores(RouteArgs a) {
     Exact3 acc = exact_zero();
 #pragma unroll
     for (int i = 0; i < kPre; ++i) {
-      const int r = part + i * kScoreLanes;
+      const int r = score_term<kVecW>(part, i);
       if (r < a.R) exact_add(acc, (double)(h2f((uint16_t)(lt[r] & amask)) * h2f(wv[i])));
     }
     for (int r = part + kPre * kScoreLanes; r < a.R; r += kScoreLanes) {
@@ -356,7 +382,11 @@ __global__ void __launch_bounds__(kScoreThreads) k_scores(RouteArgs a) {
 void launch_scores(const RouteArgs& a, hipStream_t s) {
   const int tpw = scores_tokens_per_wg(a.rows, a.R);
   const dim3 g((a.NB + kScoresPerWg - 1) / kScoresPerWg, (a.rows + tpw - 1) / tpw);
-  hipLaunchKernelGGL(k_scores, g, dim3(kScoreThreads), (size_t)a.R * tpw * sizeof(uint16_t), s, a);
+  const size_t lds = (size_t)a.R * tpw * sizeof(uint16_t);
+  if (a.svec)
+    hipLaunchKernelGGL(k_scores<true>, g, dim3(kScoreThreads), lds, s, a);
+  else
+    hipLaunchKernelGGL(k_scores<false>, g, dim3(kScoreThreads), lds, s, a);
 }
 
 // Top-k of one token's scores (keys: fp16 order key, ties to the lower block

@@ -7,10 +7,11 @@
 //               packed NF4, 16 bytes per lane and row), the token's split held
 //               in registers as fp16 pairs.  Items stream through a register
 //               pipeline of kGuStages rounds.  Each wave reduces its 4 row sums
-//               over its lanes; the split sums meet in LDS behind one s_barrier
-//               per round (LDS counter only: the loads in flight are not
-//               drained) and two lanes write silu(gate) * up of rows 2p, 2p+1
-//               (fp32, splits added in order).  Gate/up biases and the flat
+//               over its lanes into LDS slots of its own for that round, so
+//               the waves never wait for each other during the stream; after
+//               the last round one barrier joins them and silu(gate) * up of
+//               every round's rows 2p, 2p+1 is written (fp32, splits added in
+//               order).  Gate/up biases and the flat
 //               mask are applied there, in a separate instantiation, so that
 //               the plain path has no loads outside the weight stream.  The
 //               kernel also publishes the resolved block references.
@@ -51,10 +52,12 @@ constexpr int kDnStages = 2;
 constexpr int kMaxItems = 64;      // items per wave resolved up front (one per lane)
 constexpr int kMaxDnBlocks = 512;  // blocks per down workgroup (activations in LDS)
 constexpr int kLutWords = kRepLutBytes / 4;
-// dynamic LDS: table, split sums [2][8][4]; with double-quantised absmax the
-// gate and up second-level code books [2][256]; with the in-kernel top-k also
-// the selection state and the selected ids [k]
-constexpr int kGuCode2Word = kLutWords + 2 * kWaves * 4;
+// dynamic LDS: table, split sums of every round [kMaxItems][8][4] and the
+// validity of every round's item [kMaxItems][8]; with double-quantised absmax
+// the gate and up second-level code books [2][256]; with the in-kernel top-k
+// also the selection state and the selected ids [k]
+constexpr int kGuOkWord = kLutWords + kMaxItems * kWaves * 4;
+constexpr int kGuCode2Word = kGuOkWord + kMaxItems * kWaves;
 constexpr size_t kGuLds = (size_t)kGuCode2Word * 4;
 constexpr size_t kGuDqLds = kGuLds + 2 * 256 * sizeof(float);
 constexpr int kGuTopkWord = (int)(kGuDqLds / 4);
@@ -189,6 +192,7 @@ template <bool AFFINE, int SKPT, bool DQ>
 __global__ void __launch_bounds__(kThreads8, 2) k_gu_rep(DecodeArgs a) {
   extern __shared__ __attribute__((aligned(16))) uint32_t lds[];
   float* comb = reinterpret_cast<float*>(lds + kLutWords);
+  int* okl = reinterpret_cast<int*>(lds + kGuOkWord);
   const int tid = threadIdx.x, lane = tid & (kWave - 1);
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform per wave
   const int S = a.splits;                                     // 1, 2, 4 or 8
@@ -326,37 +330,44 @@ __global__ void __launch_bounds__(kThreads8, 2) k_gu_rep(DecodeArgs a) {
       gu_issue<DQ>(a, rn < R ? lane_value(enc_v, rl) : kBad, ((rn * nwg + wg) * NS + q) & 15, cb, ca, st[i]);
       if (live) {
         const float v = reduce4(acc, lane);
-        if ((lane & 15) == 0) comb[(r & 1) * (kWaves * 4) + wave * 4 + (lane >> 4)] = v;
-        lds_barrier();
-        const int id = (r * nwg + wg) * NS + q;
-        if (s == 0 && lane < 2 && id < n_items) {
-          // row 2p + lane: gate and up sums, splits added in order
-          const float* cs = comb + (r & 1) * (kWaves * 4) + q * S * 4;
-          float g = 0.0f, u = 0.0f;
-          for (int sp = 0; sp < S; ++sp) {
-            g += cs[sp * 4 + lane];
-            u += cs[sp * 4 + 2 + lane];
-          }
-          const int j = id >> 4;
-          const int n = 2 * (id & 15) + lane;
-          if constexpr (AFFINE) {
-            const uint32_t enc = lane_value(enc_v, r);
-            if (!(enc & kBad)) {
-              const int bj = SKPT > 0 ? sel_l[j] : (a.sel ? a.sel[j] : j);
-              const long long bn = (long long)bj * 32 + n;
-              if (a.gate_bias != nullptr) g += h2f(a.gate_bias[bn]);
-              if (a.up_bias != nullptr) u += h2f(a.up_bias[bn]);
-              if (a.mask != nullptr) {
-                const float m = h2f(a.mask[bn]);
-                g *= m;
-                u *= m;
-              }
-            }
-          }
-          a.st_act[(long long)j * 32 + n] = silu_mul(g, u);
+        if ((lane & 15) == 0) comb[r * (kWaves * 4) + wave * 4 + (lane >> 4)] = v;
+        if constexpr (AFFINE) {
+          if (s == 0 && lane == 0) okl[r * kWaves + q] = !(lane_value(enc_v, r) & kBad);
         }
       }
     }
+  }
+  // The split sums of every round meet once, after the stream (each round
+  // has its own LDS slots, so the waves never wait for each other before):
+  // entry e = (round, item slot q, row of the pair); gate and up sums of row
+  // 2p + (e & 1), splits added in order.
+  lds_barrier();
+  for (int e = tid; e < R * NS * 2; e += kThreads8) {
+    const int ln = e & 1, qq = (e >> 1) % NS, r = (e >> 1) / NS;
+    const int id = (r * nwg + wg) * NS + qq;
+    if (id >= n_items) continue;
+    const float* cs = comb + r * (kWaves * 4) + qq * S * 4;
+    float g = 0.0f, u = 0.0f;
+    for (int sp = 0; sp < S; ++sp) {
+      g += cs[sp * 4 + ln];
+      u += cs[sp * 4 + 2 + ln];
+    }
+    const int j = id >> 4;
+    const int n = 2 * (id & 15) + ln;
+    if constexpr (AFFINE) {
+      if (okl[r * kWaves + qq]) {
+        const int bj = SKPT > 0 ? sel_l[j] : (a.sel ? a.sel[j] : j);
+        const long long bn = (long long)bj * 32 + n;
+        if (a.gate_bias != nullptr) g += h2f(a.gate_bias[bn]);
+        if (a.up_bias != nullptr) u += h2f(a.up_bias[bn]);
+        if (a.mask != nullptr) {
+          const float m = h2f(a.mask[bn]);
+          g *= m;
+          u *= m;
+        }
+      }
+    }
+    a.st_act[(long long)j * 32 + n] = silu_mul(g, u);
   }
 }
 
