@@ -185,11 +185,99 @@ __device__ __forceinline__ float reduce4(const float (&v)[4], int lane) {
   return k;
 }
 
+// Kernel arguments are read from memory, and the compiler loads each field
+// where it is first used: a field first used after a global load that it waits
+// for costs a round trip of its own (the gate/up kernel had two before its
+// first loads and three between the selection and its weight stream).  The
+// kernels therefore pass their fields through empty asm statements ("+s":
+// the field must be loaded before the statement, and its value afterwards is
+// opaque, so it stays in SGPRs instead of being loaded again) in two batches:
+// those the first global loads need, at the start, and the rest right after
+// those loads are issued (behind a scheduling fence), so that their round
+// trip overlaps the loads'.  Pointers go through as global pointers (through
+// a generic pointer the loads would be flat loads, which also count as LDS
+// operations in the wait counters).
+template <typename T>
+__device__ __forceinline__ __attribute__((address_space(1))) T* gptr(T* p) {
+  return (__attribute__((address_space(1))) T*)p;
+}
+
+// Gate/up, first batch: the token, the selection or scores, the code books.
+__device__ __forceinline__ void pin_gu_first(DecodeArgs& a, int& nwg) {
+  nwg = (int)gridDim.x;
+  auto x = gptr(a.x);
+  auto sel = gptr(a.sel);
+  auto sel_scores = gptr(a.sel_scores);
+  auto code = gptr(a.code), code_up = gptr(a.code_up);
+  auto gc2 = gptr(a.gate.code2), uc2 = gptr(a.up.code2);
+  asm volatile(""
+               : "+s"(nwg), "+s"(x), "+s"(sel), "+s"(sel_scores), "+s"(code), "+s"(code_up), "+s"(gc2), "+s"(uc2),
+                 "+s"(a.splits), "+s"(a.NB), "+s"(a.k), "+s"(a.st_gu_rounds));
+  a.x = (const uint16_t*)x;
+  a.sel = (const int32_t*)sel;
+  a.sel_scores = (const uint16_t*)sel_scores;
+  a.code = (const float*)code;
+  a.code_up = (const float*)code_up;
+  a.gate.code2 = (const float*)gc2;
+  a.up.code2 = (const float*)uc2;
+}
+
+// Gate/up, second batch: block references, weight views, workspace.
+template <bool DQ>
+__device__ __forceinline__ void pin_gu_rest(DecodeArgs& a) {
+  auto sel_out = gptr(a.sel_out);
+  auto lookup = gptr(a.lookup);
+  auto status = gptr(a.status);
+  auto st_enc = gptr(a.st_enc);
+  auto st_bid = gptr(a.st_bid);
+  auto st_act = gptr(a.st_act);
+  auto gp = gptr(a.gate.packed), up = gptr(a.up.packed);
+  auto hgp = gptr(a.host_gate.packed), hup = gptr(a.host_up.packed);
+  auto ga = gptr(DQ ? a.gate.qabsmax : reinterpret_cast<const uint8_t*>(a.gate.absmax));
+  auto ua = gptr(DQ ? a.up.qabsmax : reinterpret_cast<const uint8_t*>(a.up.absmax));
+  auto hga = gptr(DQ ? a.host_gate.qabsmax : reinterpret_cast<const uint8_t*>(a.host_gate.absmax));
+  auto hua = gptr(DQ ? a.host_up.qabsmax : reinterpret_cast<const uint8_t*>(a.host_up.absmax));
+  auto g2 = gptr(a.gate.absmax2), u2 = gptr(a.up.absmax2);
+  asm volatile(""
+               : "+s"(sel_out), "+s"(lookup), "+s"(status), "+s"(st_enc), "+s"(st_bid), "+s"(st_act), "+s"(gp),
+                 "+s"(up), "+s"(hgp), "+s"(hup), "+s"(ga), "+s"(ua), "+s"(hga), "+s"(hua), "+s"(g2), "+s"(u2),
+                 "+s"(a.n_slots), "+s"(a.skip_negative), "+s"(a.st_gu_bytes), "+s"(a.st_gu_abytes),
+                 "+s"(a.gate.blk_stride), "+s"(a.up.blk_stride), "+s"(a.gate.row_stride), "+s"(a.gate.abs_blk_stride),
+                 "+s"(a.up.abs_blk_stride), "+s"(a.gate.abs_row_stride), "+s"(a.gate.offset), "+s"(a.up.offset),
+                 "+s"(a.qbs_shift), "+s"(a.dq_shift));
+  a.sel_out = (int32_t*)sel_out;
+  a.lookup = (const int32_t*)lookup;
+  a.status = (int*)status;
+  a.st_enc = (uint32_t*)st_enc;
+  a.st_bid = (int32_t*)st_bid;
+  a.st_act = (float*)st_act;
+  a.gate.packed = (const uint8_t*)gp;
+  a.up.packed = (const uint8_t*)up;
+  a.host_gate.packed = (const uint8_t*)hgp;
+  a.host_up.packed = (const uint8_t*)hup;
+  if constexpr (DQ) {
+    a.gate.qabsmax = (const uint8_t*)ga;
+    a.up.qabsmax = (const uint8_t*)ua;
+    a.host_gate.qabsmax = (const uint8_t*)hga;
+    a.host_up.qabsmax = (const uint8_t*)hua;
+  } else {
+    a.gate.absmax = (const float*)ga;
+    a.up.absmax = (const float*)ua;
+    a.host_gate.absmax = (const float*)hga;
+    a.host_up.absmax = (const float*)hua;
+  }
+  a.gate.absmax2 = (const float*)g2;
+  a.up.absmax2 = (const float*)u2;
+}
+
 // SKPT > 0: the workgroup first selects the top k of a.sel_scores itself (SKPT
 // scores per thread; ascending ids, ties to the lower id), so the selection
 // needs no launch of its own; workgroup 0 also writes the ids to a.sel_out.
 template <bool AFFINE, int SKPT, bool DQ>
-__global__ void __launch_bounds__(kThreads8, 2) k_gu_rep(DecodeArgs a) {
+__global__ void __launch_bounds__(kThreads8, 2) k_gu_rep(DecodeArgs args) {
+  DecodeArgs a = args;
+  int nwg;
+  pin_gu_first(a, nwg);
   extern __shared__ __attribute__((aligned(16))) uint32_t lds[];
   float* comb = reinterpret_cast<float*>(lds + kLutWords);
   int* okl = reinterpret_cast<int*>(lds + kGuOkWord);
@@ -199,7 +287,7 @@ __global__ void __launch_bounds__(kThreads8, 2) k_gu_rep(DecodeArgs a) {
   const int NS = kWaves / S;
   const int s = wave & (S - 1), q = wave / S;
   const int R = a.st_gu_rounds;
-  const int nwg = (int)gridDim.x, wg = (int)blockIdx.x;
+  const int wg = (int)blockIdx.x;
   const int n_items = 16 * a.k;
   const uint32_t col = (uint32_t)(s * kSplit + lane * 32);
   const uint32_t cb = col >> 1, ca = col >> a.qbs_shift;
@@ -240,6 +328,7 @@ __global__ void __launch_bounds__(kThreads8, 2) k_gu_rep(DecodeArgs a) {
     }
   }
   sched_fence();
+  pin_gu_rest<DQ>(a);
   lut_store(lds, codes, tid);
   if constexpr (DQ) lds[kGuCode2Word + tid] = __float_as_uint(c2v);
   int32_t* sel_l = reinterpret_cast<int32_t*>(lds + kGuSelWord);
@@ -398,8 +487,61 @@ __device__ __forceinline__ void dn_issue(const DecodeArgs& a, uint32_t enc, uint
   }
 }
 
+// Down, first batch: what the first loads need (block references, code
+// books, absmax2, activations) and the chunk geometry.
+__device__ __forceinline__ void pin_dn_first(DecodeArgs& a) {
+  auto st_enc = gptr(a.st_enc);
+  auto st_bid = gptr(a.st_bid);
+  auto st_act = gptr(a.st_act);
+  auto code = gptr(a.code_down);
+  auto c2 = gptr(a.down.code2), a2 = gptr(a.down.absmax2);
+  asm volatile(""
+               : "+s"(st_enc), "+s"(st_bid), "+s"(st_act), "+s"(code), "+s"(c2), "+s"(a2), "+s"(a.st_dn_gx),
+                 "+s"(a.st_dn_per), "+s"(a.st_dn_a2n), "+s"(a.k), "+s"(a.H), "+s"(a.NB), "+s"(a.qbs_shift),
+                 "+s"(a.dq_shift), "+s"(a.down.row_stride), "+s"(a.down.abs_row_stride));
+  a.st_enc = (uint32_t*)st_enc;
+  a.st_bid = (int32_t*)st_bid;
+  a.st_act = (float*)st_act;
+  a.code_down = (const float*)code;
+  a.down.code2 = (const float*)c2;
+  a.down.absmax2 = (const float*)a2;
+}
+
+// Down, second batch: weight views and outputs.
 template <bool DQ>
-__global__ void __launch_bounds__(kThreads8, 2) k_down_rep(DecodeArgs a) {
+__device__ __forceinline__ void pin_dn_rest(DecodeArgs& a) {
+  auto dp = gptr(a.down.packed), hdp = gptr(a.host_down.packed);
+  auto da = gptr(DQ ? a.down.qabsmax : reinterpret_cast<const uint8_t*>(a.down.absmax));
+  auto hda = gptr(DQ ? a.host_down.qabsmax : reinterpret_cast<const uint8_t*>(a.host_down.absmax));
+  auto out = gptr(a.out);
+  auto out_f32 = gptr(a.out_f32);
+  auto bias = gptr(a.down_bias);
+  auto residual = gptr(a.residual);
+  auto outpart = gptr(a.outpart);
+  asm volatile(""
+               : "+s"(dp), "+s"(hdp), "+s"(da), "+s"(hda), "+s"(out), "+s"(out_f32), "+s"(bias), "+s"(residual),
+                 "+s"(outpart), "+s"(a.down.blk_stride), "+s"(a.down.abs_blk_stride), "+s"(a.down.offset),
+                 "+s"(a.st_dn_bytes), "+s"(a.st_dn_abytes));
+  a.down.packed = (const uint8_t*)dp;
+  a.host_down.packed = (const uint8_t*)hdp;
+  if constexpr (DQ) {
+    a.down.qabsmax = (const uint8_t*)da;
+    a.host_down.qabsmax = (const uint8_t*)hda;
+  } else {
+    a.down.absmax = (const float*)da;
+    a.host_down.absmax = (const float*)hda;
+  }
+  a.out = (uint16_t*)out;
+  a.out_f32 = (float*)out_f32;
+  a.down_bias = (const uint16_t*)bias;
+  a.residual = (const uint16_t*)residual;
+  a.outpart = (float*)outpart;
+}
+
+template <bool DQ>
+__global__ void __launch_bounds__(kThreads8, 2) k_down_rep(DecodeArgs args) {
+  DecodeArgs a = args;
+  pin_dn_first(a);
   extern __shared__ __attribute__((aligned(16))) uint32_t lds[];
   uint32_t* actp = lds + kLutWords;                                    // [512][16] fp16 pairs
   float* ascale = reinterpret_cast<float*>(actp + kMaxDnBlocks * 16);  // [512]
@@ -463,6 +605,7 @@ __global__ void __launch_bounds__(kThreads8, 2) k_down_rep(DecodeArgs a) {
     for (int i = 0; i < 8; ++i) av[i] = ap[i];
   }
   sched_fence();
+  pin_dn_rest<DQ>(a);
   if (lane >= nbv) enc_v = kBad;
   DnStage st[kDnStages];
 #pragma unroll
