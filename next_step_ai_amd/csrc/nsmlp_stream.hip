@@ -329,27 +329,25 @@ __global__ void __launch_bounds__(kThreads8, 2) k_gu_rep(DecodeArgs args) {
   }
   sched_fence();
   pin_gu_rest<DQ>(a);
-  lut_store(lds, codes, tid);
-  if constexpr (DQ) lds[kGuCode2Word + tid] = __float_as_uint(c2v);
   int32_t* sel_l = reinterpret_cast<int32_t*>(lds + kGuSelWord);
   if constexpr (SKPT > 0) {
     TopkLds& tl = *reinterpret_cast<TopkLds*>(lds + kGuTopkWord);
     uint32_t T;
     unsigned need, gt, eq;
     topk_threshold<kThreads8, SKPT>(skey, i0, a.NB, a.k, tl, T, need, gt, eq);
-    int32_t* sel_out = wg == 0 ? a.sel_out : nullptr;
+    // keys past NB are padding (the last thread's, after its real keys): the
+    // counts they add come after every real key
 #pragma unroll
     for (int m = 0; m < SKPT; ++m) {
-      if (i0 + m >= a.NB) continue;
       const int pos = topk_position(skey[m], T, need, gt, eq);
       gt += skey[m] > T;
       eq += skey[m] == T;
-      if (pos < 0 || pos >= a.k) continue;
-      sel_l[pos] = i0 + m;
-      if (sel_out != nullptr) sel_out[pos] = i0 + m;
+      if (i0 + m < a.NB && pos >= 0 && pos < a.k) sel_l[pos] = i0 + m;
     }
     lds_barrier();
     b_id = sel_l[jb];
+    if (wg == 0 && a.sel_out != nullptr)
+      for (int j = tid; j < a.k; j += kThreads8) a.sel_out[j] = sel_l[j];
   }
   // Block references (slot lookup).  Split 0 of row pair 0 reports an
   // invalid block and publishes the reference for the down kernel.
@@ -384,6 +382,10 @@ __global__ void __launch_bounds__(kThreads8, 2) k_gu_rep(DecodeArgs args) {
   // publishes the code table.
   GuStage st[kGuStages];
   gu_issue<DQ>(a, R > 0 ? lane_value(enc_v, 0) : kBad, (wg * NS + q) & 15, cb, ca, st[0]);
+  // the code table goes into LDS behind the first weight loads (its codes
+  // were loaded before them, so waiting for them drains none of the stage)
+  lut_store(lds, codes, tid);
+  if constexpr (DQ) lds[kGuCode2Word + tid] = __float_as_uint(c2v);
   lds_barrier();
 #pragma unroll
   for (int i = 1; i < kGuStages; ++i)
