@@ -593,8 +593,11 @@ __device__ __forceinline__ void topk_threshold(const uint32_t (&key)[KPT], int i
   const unsigned incl = wave_incl_scan(cnt, lane);
   if (lane == kWave - 1) L.wsum[wave] = incl;
   __syncthreads();
+  // the earlier waves' totals: every wave reads all of them at once (a loop
+  // of dependent reads up to the wave index made the last wave the slowest)
   unsigned before = incl - cnt;
-  for (int w = 0; w < wave; ++w) before += L.wsum[w];
+#pragma unroll
+  for (int w = 0; w < NTHR / kWave; ++w) before += w < wave ? L.wsum[w] : 0u;
   gt = before >> 16;
   eq = before & 0xFFFFu;
 }
@@ -603,9 +606,10 @@ __device__ __forceinline__ void topk_threshold(const uint32_t (&key)[KPT], int i
 // eq count the keys above / equal to T before it.  The caller advances them
 // (gt += key > T, eq += key == T): plain values, so nothing goes to scratch.
 __device__ __forceinline__ int topk_position(uint32_t key, uint32_t T, unsigned need, unsigned gt, unsigned eq) {
-  if (key > T) return (int)(gt + (eq < need ? eq : need));
-  if (key == T && eq < need) return (int)(gt + eq);
-  return -1;
+  // selects, not branches: every key of every thread goes through it
+  const int p = (int)(gt + (eq < need ? eq : need));  // above T, or equal and among the first `need`
+  const bool take = key > T || (key == T && eq < need);
+  return take ? p : -1;
 }
 
 // ------------------------------------------------------------- launches --

@@ -284,8 +284,9 @@ __global__ void __launch_bounds__(kThreads8, 2) k_gu_rep(DecodeArgs args) {
   const int tid = threadIdx.x, lane = tid & (kWave - 1);
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform per wave
   const int S = a.splits;                                     // 1, 2, 4 or 8
-  const int NS = kWaves / S;
-  const int s = wave & (S - 1), q = wave / S;
+  const int sh = __builtin_ctz((unsigned)S);  // S is a power of two
+  const int NS = kWaves >> sh;
+  const int s = wave & (S - 1), q = wave >> sh;
   const int R = a.st_gu_rounds;
   const int wg = (int)blockIdx.x;
   const int n_items = 16 * a.k;
