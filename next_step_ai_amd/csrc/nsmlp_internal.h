@@ -549,14 +549,19 @@ __device__ __forceinline__ void topk_find_digit(const unsigned* hist, unsigned r
   above = (unsigned)__shfl((int)cum, src, kWave);
 }
 
+// Clears both histograms; the caller puts a barrier between this and
+// topk_threshold (best while the keys are still being loaded).
+template <int NTHR>
+__device__ __forceinline__ void topk_clear(TopkLds& L) {
+  for (int i = threadIdx.x; i < 2 * 256; i += NTHR) (&L.hist[0][0])[i] = 0;
+}
+
 template <int NTHR, int KPT>
 __device__ __forceinline__ void topk_threshold(const uint32_t (&key)[KPT], int i0, int NB, int k, TopkLds& L,
                                                uint32_t& T, unsigned& need, unsigned& gt, unsigned& eq) {
   const int tid = threadIdx.x, lane = tid % kWave, wave = tid / kWave;
   T = 0;
   unsigned remaining = (unsigned)k;
-  for (int i = tid; i < 2 * 256; i += NTHR) (&L.hist[0][0])[i] = 0;
-  __syncthreads();
   for (int pass = 0; pass < 2; ++pass) {
     // Scores clamped at zero are common (about half at the 405B shape) and
     // share one bin: they are counted per wave and added once, instead of

@@ -407,6 +407,8 @@ __global__ void __launch_bounds__(kSelThreads) k_select(RouteArgs a) {
   uint32_t key[KPT];
 #pragma unroll
   for (int m = 0; m < KPT; ++m) key[m] = i0 + m < NB ? f16_order_key(sc[i0 + m]) : 0u;
+  topk_clear<kSelThreads>(L);
+  lds_barrier();
   uint32_t T;
   unsigned need, gt, eq;
   topk_threshold<kSelThreads, KPT>(key, i0, NB, k, L, T, need, gt, eq);

@@ -333,6 +333,8 @@ __global__ void __launch_bounds__(kThreads8, 2) k_gu_rep(DecodeArgs args) {
   int32_t* sel_l = reinterpret_cast<int32_t*>(lds + kGuSelWord);
   if constexpr (SKPT > 0) {
     TopkLds& tl = *reinterpret_cast<TopkLds*>(lds + kGuTopkWord);
+    topk_clear<kThreads8>(tl);  // while the scores are loaded
+    lds_barrier();
     uint32_t T;
     unsigned need, gt, eq;
     topk_threshold<kThreads8, SKPT>(skey, i0, a.NB, a.k, tl, T, need, gt, eq);
@@ -379,19 +381,17 @@ __global__ void __launch_bounds__(kThreads8, 2) k_gu_rep(DecodeArgs args) {
     a2_v[3] = a.up.absmax2[g1];
     sched_fence();  // before the weight stream: their wait then drains nothing of it
   }
-  // Stage 0 of every wave goes out before any later stage; the barrier also
-  // publishes the code table.
+  // The pipeline's stages go out first; the code table goes into LDS behind
+  // them (its codes were loaded before them, so waiting for the codes drains
+  // none of the stages) and one barrier publishes it.
   GuStage st[kGuStages];
-  gu_issue<DQ>(a, R > 0 ? lane_value(enc_v, 0) : kBad, (wg * NS + q) & 15, cb, ca, st[0]);
-  // the code table goes into LDS behind the first weight loads (its codes
-  // were loaded before them, so waiting for them drains none of the stage)
+#pragma unroll
+  for (int i = 0; i < kGuStages; ++i)
+    gu_issue<DQ>(a, i < R ? lane_value(enc_v, i) : kBad, ((i * nwg + wg) * NS + q) & 15, cb, ca, st[i]);
+  sched_fence();
   lut_store(lds, codes, tid);
   if constexpr (DQ) lds[kGuCode2Word + tid] = __float_as_uint(c2v);
   lds_barrier();
-#pragma unroll
-  for (int i = 1; i < kGuStages; ++i)
-    gu_issue<DQ>(a, i < R ? lane_value(enc_v, i) : kBad, ((i * nwg + wg) * NS + q) & 15, cb, ca, st[i]);
-  sched_fence();
 
   uint32_t adg[4], adu[4];
 #pragma unroll
