@@ -50,6 +50,7 @@ SHAPES = [
     (1024, 4096, 16, 40, 2),
     (4096, 14336, 64, 64, 1000),     # 8B-shaped layer, top-k 64
     (16384, 53248, 64, 208, 2000),   # 405B-shaped layer, top-k 208
+    (8192, 32768, 64, 1024, 3000),   # every block: 32 gate/up rounds of 2 items per workgroup (streaming path)
 ]
 
 
