@@ -587,22 +587,30 @@ __global__ void __launch_bounds__(kThreads8, 2) k_down_rep(DecodeArgs args) {
   sched_fence();
   LutCodes codes;
   lut_codes_load(a.code_down, a.code_down, tid, codes);
+  // Waves with nothing to stage skip the loads (wave-uniform tests): the
+  // prologue's loads queue per CU, and the barrier after the staging waits
+  // for the last wave's.
   float c2v = 0.0f, a2v[2] = {0.0f, 0.0f};
   if constexpr (DQ) {
-    c2v = a.down.code2[tid & 255];
+    if (wave * kWave < 256) c2v = a.down.code2[tid & 255];
     // entries g_lo .. g_lo + st_dn_a2n - 1 (clamped: unconditional loads)
     const uint32_t last = min((uint32_t)((((long long)a.H * Ad) - 1) >> a.dq_shift), g_lo + a.st_dn_a2n - 1);
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
-      const uint32_t g = min(g_lo + (uint32_t)(tid + h * kThreads8), last);
-      a2v[h] = a.down.absmax2[g];
+      if (wave * kWave + h * kThreads8 < a.st_dn_a2n) {
+        const uint32_t g = min(g_lo + (uint32_t)(tid + h * kThreads8), last);
+        a2v[h] = a.down.absmax2[g];
+      }
     }
   }
   const bool own = tid < nbw;
-  uint32_t my_enc = encs[own ? tid : 0];
-  if (!own) my_enc = kBad;
+  uint32_t my_enc = kBad;
   float4 av[8];
-  {
+#pragma unroll
+  for (int i = 0; i < 8; ++i) av[i] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+  if (wave * kWave < nbw) {
+    my_enc = encs[own ? tid : 0];
+    if (!own) my_enc = kBad;
     const float4* ap = reinterpret_cast<const float4*>(a.st_act + (long long)(jb0 + (own ? tid : 0)) * 32);
 #pragma unroll
     for (int i = 0; i < 8; ++i) av[i] = ap[i];
