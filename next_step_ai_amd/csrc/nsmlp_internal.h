@@ -478,6 +478,16 @@ __device__ __forceinline__ void ld_lds4(rsrc_t r, const void* lds, uint32_t voff
   asm volatile("s_mov_b32 m0, %1\n\tbuffer_load_dword %0, %2, 0 offen lds" ::"v"(voff), "s"(lds_addr(lds)), "s"(r)
                : "memory", "m0");
 }
+__device__ __forceinline__ void ld_lds4s(rsrc_t r, const void* lds, uint32_t voff, uint32_t soff) {
+  asm volatile("s_mov_b32 m0, %1\n\tbuffer_load_dword %0, %2, %3 offen lds" ::"v"(voff), "s"(lds_addr(lds)), "s"(r),
+               "s"(soff)
+               : "memory", "m0");
+}
+__device__ __forceinline__ void ld_lds1s(rsrc_t r, const void* lds, uint32_t voff, uint32_t soff) {
+  asm volatile("s_mov_b32 m0, %1\n\tbuffer_load_ubyte %0, %2, %3 offen lds" ::"v"(voff), "s"(lds_addr(lds)), "s"(r),
+               "s"(soff)
+               : "memory", "m0");
+}
 __device__ __forceinline__ void ld_lds1(rsrc_t r, const void* lds, uint32_t voff) {
   asm volatile("s_mov_b32 m0, %1\n\tbuffer_load_ubyte %0, %2, 0 offen lds" ::"v"(voff), "s"(lds_addr(lds)), "s"(r)
                : "memory", "m0");

@@ -30,6 +30,7 @@
 // use the same permutation, which leaves the dot products unchanged.
 #include <cstring>
 #include <mutex>
+#include <type_traits>
 
 #include "nsmlp_internal.h"
 
@@ -262,51 +263,58 @@ __global__ void __launch_bounds__(kPfThreads, 4) k_pf_gu(PrefillArgs p) {  // 4 
   // this wave's MFMA step and projection; lane (j, g)
   const int s = wave & 3, proj = wave >> 2;
   const int j = lane & 15, g = lane >> 4;
+  // per-lane load offsets, the same for every chunk (the chunk's column
+  // offset goes in the scalar offset): weight dwords, absmax entries
+  const rsrc_t rW = wup ? ru : rg;
+  const rsrc_t rQ = DQ ? (wup ? ruq : rgq) : (wup ? rua : rga);
+  const rsrc_t rA2 = wup ? ru2 : rg2;
+  const rsrc_t rnone = make_rsrc(p.x, 0);
+  const uint32_t wv0 = wrow_b[0] * rs + wdw[0] * 4u, wv1 = wrow_b[1] * rs + wdw[1] * 4u;
+  const uint32_t ape = (16u * (uint32_t)apart) >> d.qbs_shift;  // the entry's group past the chunk's first
+  const uint32_t qv = DQ ? ((arow >> 1) * A + ape) * 2u + (arow & 1u) : (arow * A + ape) * 4u;
+  const uint32_t fb = (32u * (uint32_t)b + arow) * A + ape;  // absmax index of the entry in chunk 0
   __syncthreads();
 
   for (int t0 = 0; t0 < cnt; t0 += kGuTok) {
     const int T = min(kGuTok, cnt - t0);
     const int ntiles = (T + 15) >> 4;
-    int xtok[2];
+    // token rows of this pass (rows past T load zeros)
+    uint32_t xv[2];
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
       const int tr = 8 * wave + 4 * h + (lane >> 4);
-      xtok[h] = tr < T ? buf_ldic(rtok, (uint32_t)(t0 + tr) * 4u, 0) : -1;
+      const uint32_t pc = (uint32_t)(xslot ^ (tr & 15));
+      const int tok = tr < T ? buf_ldic(rtok, (uint32_t)(t0 + tr) * 4u, 0) : -1;
+      xv[h] = tok >= 0 ? ((uint32_t)tok * (uint32_t)H + pc * 8u) * 2u : kOffNone;
     }
-    // chunk c into stage c % kGuNS (a chunk past the end loads zeros)
-    auto issue = [&](int c) {
+    // chunk c into stage c % kGuNS (a chunk past the end: descriptors of
+    // extent zero, so its loads write zeros without reading memory)
+    auto issue = [&](int c, auto stc) {
+      constexpr int st = decltype(stc)::value;
       const bool live = c < nchunks;
-      const int st = c % kGuNS;
       const uint32_t col0 = (uint32_t)(cfirst + (live ? c : 0)) * kGuChunk;
-#pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        const int i = 2 * wave + h;
-        const int tr = 4 * i + (lane >> 4);
-        const uint32_t pc = (uint32_t)(xslot ^ (tr & 15));
-        const uint32_t xo = (live && xtok[h] >= 0) ? ((uint32_t)xtok[h] * (uint32_t)H + col0 + pc * 8u) * 2u : kOffNone;
-        ld_lds16(rx, &L.x[st][i * 1024], xo);
-      }
-#pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        const int i = 2 * wave + h;
-        const uint32_t wo = live ? wrow_b[h] * rs + (col0 >> 1) + wdw[h] * 4u : kOffNone;
-        ld_lds4(wup ? ru : rg, &L.w[st][i * 256], wo);
-      }
-      const uint32_t ce = (col0 + 16u * (uint32_t)apart) >> d.qbs_shift;
+      const uint32_t cq = col0 >> d.qbs_shift;
+      const rsrc_t rxc = live ? rx : rnone, rWc = live ? rW : rnone, rQc = live ? rQ : rnone;
+      ld_lds16s(rxc, &L.x[st][(2 * wave) * 1024], xv[0], col0 * 2u);
+      ld_lds16s(rxc, &L.x[st][(2 * wave + 1) * 1024], xv[1], col0 * 2u);
+      ld_lds4s(rWc, &L.w[st][(2 * wave) * 256], wv0, col0 >> 1);
+      ld_lds4s(rWc, &L.w[st][(2 * wave + 1) * 256], wv1, col0 >> 1);
       if constexpr (DQ) {
-        ld_lds1(wup ? ruq : rgq, &L.qa[st][wave * 64], live ? ((arow >> 1) * A + ce) * 2u + (arow & 1u) : kOffNone);
-        const uint32_t f = (32u * (uint32_t)b + arow) * A + ce;
-        ld_lds4(wup ? ru2 : rg2, &L.a2[st][wave * 64], live ? (f >> d.dq_shift) * 4u : kOffNone);
+        ld_lds1s(rQc, &L.qa[st][wave * 64], qv, cq * 2u);
+        ld_lds4(live ? rA2 : rnone, &L.a2[st][wave * 64], ((fb + cq) >> d.dq_shift) * 4u);
       } else {
-        ld_lds4(wup ? rua : rga, &L.qa[st][wave * 64], live ? (arow * A + ce) * 4u : kOffNone);
+        ld_lds4s(rQc, &L.qa[st][wave * 64], qv, cq * 4u);
       }
     };
     float4_t acc[kGuTiles][2];
 #pragma unroll
     for (int tt = 0; tt < kGuTiles; ++tt) acc[tt][0] = acc[tt][1] = float4_t{0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-    for (int c = 0; c < kGuNS - 1; ++c) issue(c);
-    for (int c = 0; c < nchunks; ++c) {
+    issue(0, std::integral_constant<int, 0>());
+    issue(1, std::integral_constant<int, 1>());
+    // chunk c from stage ST = c % kGuNS (a compile-time constant: the loop
+    // below is unrolled by kGuNS, so the stage offsets are immediates)
+    auto chunk = [&](int c, auto stc) {
+      constexpr int st = decltype(stc)::value;
       // this thread's loads of chunk c have landed (those of the next
       // kGuNS - 2 chunks may not), then every thread's
       if constexpr (DQ)
@@ -314,8 +322,7 @@ __global__ void __launch_bounds__(kPfThreads, 4) k_pf_gu(PrefillArgs p) {  // 4 
       else
         asm volatile("s_waitcnt vmcnt(5)" ::: "memory");  // (kGuNS - 2) chunks x 5 loads
       lds_barrier();  // also: every wave is done with chunk c - 1, whose stage the next issue refills
-      issue(c + kGuNS - 1);
-      const int st = c % kGuNS;
+      issue(c + kGuNS - 1, std::integral_constant<int, (st + kGuNS - 1) % kGuNS>());
       half8_t bf[2];
       {
         const int r0 = proj * 32 + j, r1 = r0 + 16;
@@ -346,7 +353,16 @@ __global__ void __launch_bounds__(kPfThreads, 4) k_pf_gu(PrefillArgs p) {  // 4 
           acc[tt][1] = mfma16(af, bf[1], acc[tt][1]);
         }
       }
+    };
+    static_assert(kGuNS == 3, "the chunk loop is unrolled by 3");
+    int c = 0;
+    for (; c + 3 <= nchunks; c += 3) {
+      chunk(c, std::integral_constant<int, 0>());
+      chunk(c + 1, std::integral_constant<int, 1>());
+      chunk(c + 2, std::integral_constant<int, 2>());
     }
+    if (c < nchunks) chunk(c, std::integral_constant<int, 0>());
+    if (c + 1 < nchunks) chunk(c + 1, std::integral_constant<int, 1>());
     // the stages are free once every load (the zeros past the end too) has
     // landed; step partials summed in step order into [kGuTok tok][64 rows]
     // fp32 (rows: gate 0-31, up 32-63), reusing the token stages
