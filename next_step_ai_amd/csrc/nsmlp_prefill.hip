@@ -50,23 +50,18 @@ __device__ __forceinline__ void cpair_fill(uint32_t* cpair, const float* code, i
     cpair[e] = (uint32_t)f2h(code[e >> 4]) | ((uint32_t)f2h(code[e & 15]) << 16);
 }
 
-// fp32 code pairs per packed byte: entry e = (code[e >> 4], code[e & 15]),
-// the (even, odd) elements of byte e.
-__device__ __forceinline__ void fpair_fill(float2* cp, const float* code, int tid, int nthr) {
-  for (int e = tid; e < 256; e += nthr) cp[e] = make_float2(code[e >> 4], code[e & 15]);
-}
-
 // 16 consecutive NF4 elements of two rows (words w0, w1: 4 bytes each, even
 // element in the high nibble) as fp16(code * absmax), the reference
 // fallback's rounding of the weights.  All eight pair lookups go out before
 // any is used.
+template <int kCopies>
 __device__ __forceinline__ void deq8x2(uint32_t w0, float am0, uint32_t w1, float am1, const float2* cp,
                                        half8_t& h0, half8_t& h1) {
   float2 p[8];
 #pragma unroll
   for (int m = 0; m < 4; ++m) {
-    p[m] = cp[(w0 >> (8 * m)) & 0xFFu];
-    p[4 + m] = cp[(w1 >> (8 * m)) & 0xFFu];
+    p[m] = cp[((w0 >> (8 * m)) & 0xFFu) * kCopies];
+    p[4 + m] = cp[((w1 >> (8 * m)) & 0xFFu) * kCopies];
   }
 #pragma unroll
   for (int m = 0; m < 4; ++m) {
@@ -195,18 +190,19 @@ constexpr int kGuTiles = kGuTok / 16;      // MFMA token tiles per pass
 constexpr int kGuNS = 3;                   // LDS stages (chunks): 76 KB, two workgroups per CU
 constexpr int kGuXBytes = kGuTok * kGuChunk * 2;   // token rows of a stage: [64][16 pieces of 16 B]
 constexpr int kGuWBytes = 64 * kGuChunk / 2;       // NF4 rows of a stage: [64][16 dwords]
-constexpr int kGuAux = 64 * 8;                     // absmax entries of a stage: [64 rows][8 pieces of 16 columns]
+constexpr int kGuAux = 64 * 4;                     // absmax entries of a stage: [64 rows][4 pieces of 32 columns]
+constexpr int kGuCopies = 4;                       // code-pair table copies (lane % 4)
 struct GuLds {
   uint8_t x[kGuNS][kGuXBytes];
   uint8_t w[kGuNS][kGuWBytes];
   uint32_t qa[kGuNS][kGuAux];  // double-quantised: u8 code (low byte); fp32: the absmax bits
-  float a2[kGuNS][kGuAux];     // double-quantised: the entry's absmax2
-  float2 cpair[256];
+  float a2[kGuNS][kGuAux];     // double-quantised: the entry's absmax2 (fp32: a second copy of qa)
+  float2 cpair[256 * kGuCopies];  // entry e, copy c at e * kGuCopies + c
   float c2[2][256];
 };
 static_assert(kGuTok * 64 * 4 <= kGuNS * kGuXBytes, "gate/up sums must fit the token stages");
-static_assert(kGuTok * 16 == 2 * kPfThreads && 64 * 16 == 2 * kPfThreads && kGuAux == kPfThreads,
-              "loads per chunk: two token pieces, two weight dwords, one absmax entry per thread");
+static_assert(kGuTok * 16 == 2 * kPfThreads && 64 * 16 == 2 * kPfThreads && 2 * kGuAux == kPfThreads,
+              "loads per chunk: two token pieces, two weight dwords, one absmax load per thread");
 
 template <bool DQ>
 __global__ void __launch_bounds__(kPfThreads, 4) k_pf_gu(PrefillArgs p) {  // 4 waves per SIMD: two workgroups per CU
@@ -222,7 +218,10 @@ __global__ void __launch_bounds__(kPfThreads, 4) k_pf_gu(PrefillArgs p) {  // 4 
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int beg = p.offsets[b], cnt = p.offsets[b + 1] - beg;
   if (cnt == 0) return;
-  fpair_fill(L.cpair, d.code, tid, kPfThreads);
+  for (int i = tid; i < 256 * kGuCopies; i += kPfThreads) {
+    const int e = i / kGuCopies;
+    L.cpair[i] = make_float2(d.code[e >> 4], d.code[e & 15]);
+  }
   if constexpr (DQ) L.c2[tid >> 8][tid & 255] = (tid < 256 ? d.gate.code2 : d.up.code2)[tid & 255];
   const BlockRef br = resolve_id(d, b);
   if (!br.ok && tid == 0) atomicOr(d.status, 1);
@@ -252,25 +251,28 @@ __global__ void __launch_bounds__(kPfThreads, 4) k_pf_gu(PrefillArgs p) {  // 4 
   // chunk, lane l): token row 4 i + l / 16, LDS slot l % 16 <- global piece
   // (l % 16) ^ (row % 16); weight row 4 i + l / 16 (gate rows 0-31 from waves
   // 0-3), LDS dword l % 16 <- global dword (l % 16) ^ 4 ((row / 4) % 4);
-  // absmax entry tid = (row tid / 8, 16-column piece tid % 8)
+  // absmax entry e = tid % 256 = (row e / 4, 32-column piece e % 4): its u8
+  // code from waves 0-3 and its absmax2 from waves 4-7 (fp32 absmax: the
+  // value from both, into qa and a2)
   const int xslot = lane & 15;
   const bool wup = wave >= 4;
   const uint32_t wdw[2] = {(uint32_t)((lane & 15) ^ (((((8 * wave + 4 * 0 + (lane >> 4)) & 31) >> 2) & 3) << 2)),
                            (uint32_t)((lane & 15) ^ (((((8 * wave + 4 * 1 + (lane >> 4)) & 31) >> 2) & 3) << 2))};
   const uint32_t wrow_b[2] = {(uint32_t)((8 * wave + (lane >> 4)) & 31), (uint32_t)((8 * wave + 4 + (lane >> 4)) & 31)};
-  const int ar = tid >> 3, apart = tid & 7;
+  const int ae = tid & (kGuAux - 1), ar = ae >> 2, apart = ae & 3;
   const uint32_t arow = (uint32_t)(ar & 31);
+  const bool aup = (wave & 3) >= 2;  // ar >= 32, from the (uniform) wave index
   // this wave's MFMA step and projection; lane (j, g)
   const int s = wave & 3, proj = wave >> 2;
   const int j = lane & 15, g = lane >> 4;
   // per-lane load offsets, the same for every chunk (the chunk's column
   // offset goes in the scalar offset): weight dwords, absmax entries
   const rsrc_t rW = wup ? ru : rg;
-  const rsrc_t rQ = DQ ? (wup ? ruq : rgq) : (wup ? rua : rga);
-  const rsrc_t rA2 = wup ? ru2 : rg2;
+  const rsrc_t rQ = DQ ? (aup ? ruq : rgq) : (aup ? rua : rga);
+  const rsrc_t rA2 = aup ? ru2 : rg2;
   const rsrc_t rnone = make_rsrc(p.x, 0);
   const uint32_t wv0 = wrow_b[0] * rs + wdw[0] * 4u, wv1 = wrow_b[1] * rs + wdw[1] * 4u;
-  const uint32_t ape = (16u * (uint32_t)apart) >> d.qbs_shift;  // the entry's group past the chunk's first
+  const uint32_t ape = (32u * (uint32_t)apart) >> d.qbs_shift;  // the entry's group past the chunk's first
   const uint32_t qv = DQ ? ((arow >> 1) * A + ape) * 2u + (arow & 1u) : (arow * A + ape) * 4u;
   const uint32_t fb = (32u * (uint32_t)b + arow) * A + ape;  // absmax index of the entry in chunk 0
   __syncthreads();
@@ -300,10 +302,12 @@ __global__ void __launch_bounds__(kPfThreads, 4) k_pf_gu(PrefillArgs p) {  // 4 
       ld_lds4s(rWc, &L.w[st][(2 * wave) * 256], wv0, col0 >> 1);
       ld_lds4s(rWc, &L.w[st][(2 * wave + 1) * 256], wv1, col0 >> 1);
       if constexpr (DQ) {
-        ld_lds1s(rQc, &L.qa[st][wave * 64], qv, cq * 2u);
-        ld_lds4(live ? rA2 : rnone, &L.a2[st][wave * 64], ((fb + cq) >> d.dq_shift) * 4u);
+        if (!wup)
+          ld_lds1s(rQc, &L.qa[st][wave * 64], qv, cq * 2u);
+        else
+          ld_lds4(live ? rA2 : rnone, &L.a2[st][(wave - 4) * 64], ((fb + cq) >> d.dq_shift) * 4u);
       } else {
-        ld_lds4s(rQc, &L.qa[st][wave * 64], qv, cq * 4u);
+        ld_lds4s(rQc, wup ? (const void*)&L.a2[st][(wave - 4) * 64] : (const void*)&L.qa[st][wave * 64], qv, cq * 4u);
       }
     };
     float4_t acc[kGuTiles][2];
@@ -317,16 +321,13 @@ __global__ void __launch_bounds__(kPfThreads, 4) k_pf_gu(PrefillArgs p) {  // 4 
       constexpr int st = decltype(stc)::value;
       // this thread's loads of chunk c have landed (those of the next
       // kGuNS - 2 chunks may not), then every thread's
-      if constexpr (DQ)
-        asm volatile("s_waitcnt vmcnt(6)" ::: "memory");  // (kGuNS - 2) chunks x 6 loads
-      else
-        asm volatile("s_waitcnt vmcnt(5)" ::: "memory");  // (kGuNS - 2) chunks x 5 loads
+      asm volatile("s_waitcnt vmcnt(5)" ::: "memory");  // (kGuNS - 2) chunks x 5 loads
       lds_barrier();  // also: every wave is done with chunk c - 1, whose stage the next issue refills
       issue(c + kGuNS - 1, std::integral_constant<int, (st + kGuNS - 1) % kGuNS>());
       half8_t bf[2];
       {
         const int r0 = proj * 32 + j, r1 = r0 + 16;
-        const int a0 = r0 * 8 + 2 * s + (g >> 1), a1 = r1 * 8 + 2 * s + (g >> 1);
+        const int a0 = r0 * 4 + s, a1 = r1 * 4 + s;  // piece s: the step's 32 columns
         const uint32_t w0 = *reinterpret_cast<const uint32_t*>(
             &L.w[st][r0 * 64 + ((uint32_t)(4 * s + g) ^ ((((uint32_t)(r0 & 31) >> 2) & 3u) << 2)) * 4]);
         const uint32_t w1 = *reinterpret_cast<const uint32_t*>(
@@ -341,7 +342,7 @@ __global__ void __launch_bounds__(kPfThreads, 4) k_pf_gu(PrefillArgs p) {  // 4 
           am0 = __uint_as_float(L.qa[st][a0]);
           am1 = __uint_as_float(L.qa[st][a1]);
         }
-        deq8x2(w0, am0, w1, am1, L.cpair, bf[0], bf[1]);
+        deq8x2<kGuCopies>(w0, am0, w1, am1, L.cpair + (lane & (kGuCopies - 1)), bf[0], bf[1]);
       }
 #pragma unroll
       for (int tt = 0; tt < kGuTiles; ++tt) {
