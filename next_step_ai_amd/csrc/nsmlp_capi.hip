@@ -633,18 +633,6 @@ static bool prefill_dense_down(int H, int NB, int M, int k) {
          (long long)M * H * 2 < (1LL << 31);
 }
 
-// Column slices of the prefill gate/up: two halves of every block's rows on
-// two workgroups (twice the workgroups for the same bytes, each XCD's L2
-// holding one half of the token rows), their sums added by k_pf_act.
-// NSMLP_PF_KS=1/2/4/8 overrides it (measurement switch).
-static int prefill_slices(int H) {
-  static const int forced = env_int("NSMLP_PF_KS", 0);
-  int ks = 2;
-  if (forced == 1 || forced == 2 || forced == 4 || forced == 8) ks = forced;
-  while (ks > 1 && H % (128 * ks) != 0) ks >>= 1;
-  return ks;
-}
-
 size_t nsmlp_prefill_workspace_bytes(int H, int NB, int M, int k) {
   if (H <= 0 || NB <= 0 || M <= 0 || k <= 0) return 0;
   const size_t words = (size_t)(M + 31) / 32, TG = (size_t)(M + 127) / 128, nk = (size_t)M * (size_t)k;
@@ -659,8 +647,6 @@ size_t nsmlp_prefill_workspace_bytes(int H, int NB, int M, int k) {
   } else {
     off += align_up(nk * 32 * 2);                  // act per (block, token) entry
   }
-  const int ks = prefill_slices(H);
-  if (ks > 1) off += align_up((size_t)ks * nk * 64 * 4);  // gate/up sums per column slice
   return off;
 }
 
@@ -711,8 +697,6 @@ int nsmlp_prefill_slots_f16(const nsmlp_slot_table* table, const void* x, int M,
   } else {
     p.act = (uint16_t*)(base + off);
   }
-  p.KS = prefill_slices(p.d.H);
-  if (p.KS > 1) p.gpart = (float*)(base + need - align_up((size_t)p.KS * nk * 64 * 4));  // the last region
   launch_prefill(p, (hipStream_t)stream);
   return check_launch("prefill");
 }

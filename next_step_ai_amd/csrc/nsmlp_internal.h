@@ -776,12 +776,6 @@ struct PrefillArgs {
   uint16_t* act_dense;    // or nullptr
   float* part;            // [S][M][H] fp32 partial sums
   int S;
-  // gate/up split over KS column slices (KS > 1): one workgroup per (block,
-  // slice), slice = XCD % KS, so each XCD's L2 holds one slice of the token
-  // rows; fp32 sums [KS][M k][64] (gate rows 0-31, up 32-63), added in slice
-  // order by k_pf_act
-  float* gpart;
-  int KS;
 };
 void launch_prefill(const PrefillArgs& p, hipStream_t s);
 

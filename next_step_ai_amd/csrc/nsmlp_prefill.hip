@@ -6,14 +6,11 @@
 //
 //   k_pf_mark / k_pf_scan / k_pf_list  token lists per block (CSR, ascending
 //               token ids), from a [NB][M/32] membership bitmap and counts;
-//   k_pf_gu     one workgroup per block and column slice (KS slices of
-//               H / KS columns; slice = XCD % KS): gate and up of the
-//               block's tokens as a staged GEMM, the token rows gathered as the MFMA A
+//   k_pf_gu     one workgroup per block: gate and up of the block's tokens
+//               as a staged GEMM, the token rows gathered as the MFMA A
 //               operand and the NF4 rows decoded to fp16(code * absmax) as the
 //               B operand (the reference fallback's rounding of the weights,
-//               RT:5439-5447); act = fp16(silu(gate) * up) per (block, token)
-//               (KS = 1), else fp32 sums per slice;
-//   k_pf_act    KS > 1: the slices' sums added in slice order, then act;
+//               RT:5439-5447); act = fp16(silu(gate) * up) per (block, token);
 //   k_pf_down   one workgroup per 64 output rows and 128-token group: for
 //               every block, act [tokens x 32] times the block's down columns
 //               [32 x 64 rows] as fp16 codes, the absmax applied to the MFMA
@@ -209,11 +206,7 @@ __global__ void __launch_bounds__(kPfThreads, 4) k_pf_gu(PrefillArgs p) {  // 4 
   extern __shared__ __attribute__((aligned(16))) uint8_t pf_lds[];
   GuLds& L = *reinterpret_cast<GuLds*>(pf_lds);
   const DecodeArgs& d = p.d;
-  // workgroup i runs on XCD i % 8: slice (i % 8) % KS of block
-  // (i / 8) (8 / KS) + (i % 8) / KS
-  const int xcd = blockIdx.x & 7, ks = xcd & (p.KS - 1);
-  const int b = (int)(blockIdx.x >> 3) * (8 / p.KS) + xcd / p.KS;
-  if (b >= d.NB) return;
+  const int b = blockIdx.x;
   const int tid = threadIdx.x, lane = tid & (kWave - 1);
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int beg = p.offsets[b], cnt = p.offsets[b + 1] - beg;
@@ -246,7 +239,7 @@ __global__ void __launch_bounds__(kPfThreads, 4) k_pf_gu(PrefillArgs p) {  // 4 
   }
   const rsrc_t rx = make_rsrc(p.x, (int)((long long)p.M * H * 2));
   const rsrc_t rtok = make_rsrc(p.tokens + beg, cnt * 4);
-  const int nchunks = H / kGuChunk / p.KS, cfirst = ks * nchunks;
+  const int nchunks = H / kGuChunk;
   // loads of this thread per chunk (instruction i = 2 wave + h of 16 per
   // chunk, lane l): token row 4 i + l / 16, LDS slot l % 16 <- global piece
   // (l % 16) ^ (row % 16); weight row 4 i + l / 16 (gate rows 0-31 from waves
@@ -294,7 +287,7 @@ __global__ void __launch_bounds__(kPfThreads, 4) k_pf_gu(PrefillArgs p) {  // 4 
     auto issue = [&](int c, auto stc) {
       constexpr int st = decltype(stc)::value;
       const bool live = c < nchunks;
-      const uint32_t col0 = (uint32_t)(cfirst + (live ? c : 0)) * kGuChunk;
+      const uint32_t col0 = (uint32_t)(live ? c : 0) * kGuChunk;
       const uint32_t cq = col0 >> d.qbs_shift;
       const rsrc_t rxc = live ? rx : rnone, rWc = live ? rW : rnone, rQc = live ? rQ : rnone;
       ld_lds16s(rxc, &L.x[st][(2 * wave) * 1024], xv[0], col0 * 2u);
@@ -388,13 +381,6 @@ __global__ void __launch_bounds__(kPfThreads, 4) k_pf_gu(PrefillArgs p) {  // 4 
       }
       __syncthreads();
     }
-    if (p.KS > 1) {  // this slice's sums, entry beg + t0 + ti
-      float4* dst = reinterpret_cast<float4*>(p.gpart + ((long long)ks * p.M * p.k + beg + t0) * 64);
-      const float4* src = reinterpret_cast<const float4*>(cs);
-      for (int o = tid; o < T * 16; o += kPfThreads) dst[o] = src[o];
-      __syncthreads();
-      continue;
-    }
     for (int o = tid; o < T * 32; o += kPfThreads) {
       const int ti = o >> 5, row = o & 31;
       const float gs = cs[ti * 64 + row], us = cs[ti * 64 + 32 + row];
@@ -405,31 +391,6 @@ __global__ void __launch_bounds__(kPfThreads, 4) k_pf_gu(PrefillArgs p) {  // 4 
         p.act[(long long)(beg + t0 + ti) * 32 + row] = a;
     }
     __syncthreads();
-  }
-}
-
-// act of every (block, token) entry from the KS slices' gate/up sums, added
-// in slice order: one workgroup per block.
-__global__ void __launch_bounds__(256) k_pf_act(PrefillArgs p) {
-  const DecodeArgs& d = p.d;
-  const int b = blockIdx.x;
-  const int beg = p.offsets[b], cnt = p.offsets[b + 1] - beg;
-  if (cnt == 0) return;
-  const bool ok = resolve_id(d, b).ok;
-  const long long sl = (long long)p.M * p.k * 64;
-  for (int o = threadIdx.x; o < cnt * 32; o += 256) {
-    const int ti = o >> 5, row = o & 31;
-    const float* src = p.gpart + (long long)(beg + ti) * 64 + row;
-    float gs = src[0], us = src[32];
-    for (int s = 1; s < p.KS; ++s) {
-      gs += src[s * sl];
-      us += src[s * sl + 32];
-    }
-    const uint16_t a = ok ? f2h(silu_mul(gs, us)) : (uint16_t)0;
-    if (p.act_dense != nullptr)
-      p.act_dense[(long long)p.tokens[beg + ti] * (d.NB * 32) + 32 * b + row] = a;
-    else
-      p.act[(long long)(beg + ti) * 32 + row] = a;
   }
 }
 
@@ -645,12 +606,10 @@ void launch_prefill(const PrefillArgs& p, hipStream_t s) {
     for (const void* f : {reinterpret_cast<const void*>(k_pf_gu<true>), reinterpret_cast<const void*>(k_pf_gu<false>)})
       (void)hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, (int)sizeof(GuLds));
   });
-  const dim3 gg((unsigned)((p.d.NB * p.KS + 7) / 8 * 8));
   if (p.d.dq)
-    k_pf_gu<true><<<gg, dim3(kPfThreads), sizeof(GuLds), s>>>(p);
+    k_pf_gu<true><<<dim3(p.d.NB), dim3(kPfThreads), sizeof(GuLds), s>>>(p);
   else
-    k_pf_gu<false><<<gg, dim3(kPfThreads), sizeof(GuLds), s>>>(p);
-  if (p.KS > 1) k_pf_act<<<dim3(p.d.NB), dim3(256), 0, s>>>(p);
+    k_pf_gu<false><<<dim3(p.d.NB), dim3(kPfThreads), sizeof(GuLds), s>>>(p);
   if (p.act_dense != nullptr) {
     // every token's act is zero outside its own blocks, so the dense down GEMM
     // over the scattered act is the per-token sum over the selected blocks
