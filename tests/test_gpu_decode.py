@@ -75,6 +75,24 @@ def test_decode_layer_matches_oracle(gpu, orc, H, I, R, k, seed):
     assert torch.equal(out2, out) and torch.equal(sel2, sel)
 
 
+@pytest.mark.parametrize("qbs", [32, 128])
+def test_decode_layer_quant_block_sizes(gpu, orc, qbs):
+    """Absmax blocks of 32 and 128 columns on the streaming layer path, u8
+    and fp32 absmax: against the oracle, the two absmax forms bit-identical."""
+    from next_step_ai_amd.synth import make_synthetic_layer
+
+    H, I, R, k = 4096, 14336, 64, 64
+    print(f"decode layer qbs={qbs}", flush=True)
+    L = make_synthetic_layer(H=H, I=I, R=R, seed=77 + qbs, device=gpu, qbs=qbs, double_quant=True)
+    out, sel = L.layer(k, absmax="dq").forward(L.x)
+    out_f, sel_f = L.layer(k, absmax="f32").forward(L.x)
+    torch.cuda.synchronize()
+    assert torch.equal(sel, sel_f) and torch.equal(out, out_f)
+    sel_g = _np(sel).astype(np.int64)
+    ye, yf, _ = _oracle_for_layer(orc, L, sel_g)
+    _check_tolerance(orc, _np(out).astype(np.float64), ye, yf, f"layer qbs={qbs}")
+
+
 @pytest.mark.parametrize("H,I,k,n_pos", [
     (2048, 2048, 64, 10),      # k = NB: every block
     (2048, 8192, 200, 37),     # ties at the clamped score 0 decide most of the selection

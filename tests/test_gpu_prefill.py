@@ -23,13 +23,13 @@ def _np(t):
 
 def _oracle_rows(orc, L, x, sel_rows):
     """Oracle (exact, fallback) for token rows x [n, H] with block sets sel_rows [n, k]."""
-    H, I = L.H, L.I
+    H, I, qbs = L.H, L.I, L.qbs
     union = np.unique(sel_rows)
     local = np.searchsorted(union, sel_rows).astype(np.int32)
-    gp, ga = orc.gather_rows_blocks(_np(L.gate_packed), _np(L.gate_absmax), union, H, 64)
-    upk, ua = orc.gather_rows_blocks(_np(L.up_packed), _np(L.up_absmax), union, H, 64)
-    dp, da = orc.gather_down_columns(_np(L.down_packed), _np(L.down_absmax), union, H, I, 64)
-    ye, yf = orc.sparse_mlp(_u16(x), local, gp, ga, upk, ua, dp, da, qbs=64)
+    gp, ga = orc.gather_rows_blocks(_np(L.gate_packed), _np(L.gate_absmax), union, H, qbs)
+    upk, ua = orc.gather_rows_blocks(_np(L.up_packed), _np(L.up_absmax), union, H, qbs)
+    dp, da = orc.gather_down_columns(_np(L.down_packed), _np(L.down_absmax), union, H, I, qbs)
+    ye, yf = orc.sparse_mlp(_u16(x), local, gp, ga, upk, ua, dp, da, qbs=qbs)
     return ye, yf
 
 
@@ -132,3 +132,25 @@ def test_prefill_405b_shape_rows_match_oracle(gpu, orc):
     sel_np = _np(sel).astype(np.int64)
     ye, yf = _oracle_rows(orc, L, x[rows], sel_np[rows])
     _check_rows(orc, _np(out)[rows], ye, yf, range(len(rows)), "prefill 405B")
+
+
+@pytest.mark.parametrize("qbs", [32, 128])
+def test_prefill_quant_block_sizes(gpu, orc, qbs):
+    """Absmax blocks of 32 and 128 columns (the gate/up kernel stages one
+    absmax entry per 32 columns): rows against the oracle and the u8
+    absmax path bit-identical to the fp32 path of the resolved absmax."""
+    from next_step_ai_amd.synth import make_synthetic_layer, synth_normal_f16
+
+    H, I, M, k = 2048, 8192, 96, 24
+    print(f"prefill qbs={qbs}", flush=True)
+    L = make_synthetic_layer(H=H, I=I, R=16, seed=31 + qbs, device=gpu, qbs=qbs, double_quant=True)
+    x = synth_normal_f16(qbs, (M, H), 1.0, gpu)
+    out_dq, sel = L.layer(k, absmax="dq").prefill(x)
+    out_f, sel_f = L.layer(k, absmax="f32").prefill(x)
+    torch.cuda.synchronize()
+    assert torch.equal(sel, sel_f)
+    assert torch.equal(out_dq, out_f)
+    rows = [0, 7, 50, 95]
+    sel_np = _np(sel).astype(np.int64)
+    ye, yf = _oracle_rows(orc, L, x[rows], sel_np[rows])
+    _check_rows(orc, _np(out_dq)[rows], ye, yf, range(len(rows)), f"prefill qbs={qbs}")
