@@ -59,30 +59,6 @@ __device__ __forceinline__ void exact_add(Exact3& e, double d) {
   e.a0 += c0;
 }
 
-// Two-part variant for sums whose terms' magnitudes add up to less than 2^40
-// (checked by the caller): a1 takes d rounded to a multiple of 2^-11 (exact
-// for |d| < 2^40), a0 the exact remainder (|a0 term| <= 2^-12, a multiple of
-// 2^-48 for products of fp16 values); a1 stays exact while |a1| < 2^42.
-struct Exact2 {
-  double a0, a1;
-};
-
-__device__ __forceinline__ void exact2_add(Exact2& e, double d) {
-  const double C1 = 3298534883328.0;  // 1.5 * 2^41
-  const double t1 = d + C1;
-  const double c1 = t1 - C1;
-  e.a1 += c1;
-  e.a0 += d - c1;
-}
-
-// The Exact3 form of an Exact2 sum (a1 split at 2^12), as exact_to_f16 takes it.
-__device__ __forceinline__ Exact3 exact2_to_3(const Exact2& e) {
-  const double C2 = 27670116110564327424.0;  // 1.5 * 2^64
-  const double t2 = e.a1 + C2;
-  const double c2 = t2 - C2;
-  return Exact3{e.a0, e.a1 - c2, c2};
-}
-
 __device__ __forceinline__ void exact_merge(Exact3& e, const Exact3& o) {
   e.a0 += o.a0;
   e.a1 += o.a1;

@@ -83,10 +83,11 @@ __global__ void __launch_bounds__(kLatThreads) k_latent(RouteArgs a) {
 // l / 8 and token l % 8 of the tile and reads 8 columns of both per step
 // (16-byte loads; the 8 lanes of one row or token read the same bytes), so
 // each x and enc_w byte is read once per tile instead of once per output.
-// Exact3 sums do not depend on how the terms are split, so the fp16 latent
-// equals k_latent's.  A tile whose terms' magnitudes add up to less than 2^39
-// per output (the common case) keeps two-part sums (Exact2: 5 instead of 9
-// fp64 operations per term); otherwise it sums again in three parts.
+// The first pass sums in plain fp64 (one add per term) with a bound on the
+// rounding error; an output whose bounded interval rounds to one fp16 value
+// has that value as the exact sum's rounding (the common case).  Any other
+// output of the tile is summed again in three parts (Exact3, exact for any
+// fp16 inputs) by the whole workgroup, so the fp16 latent equals k_latent's.
 constexpr int kLtRows = 8, kLtTok = 8, kLtThreads = 1024;
 
 __global__ void __launch_bounds__(kLtThreads) k_latent_tiled(RouteArgs a) {
@@ -98,13 +99,19 @@ __global__ void __launch_bounds__(kLtThreads) k_latent_tiled(RouteArgs a) {
   const uint16_t* __restrict__ w = a.enc_w + (long long)rc * a.H;
   const int span = (a.H + 8 * kLtThreads / kWave - 1) / (8 * kLtThreads / kWave) * 8;  // columns per wave
   const int c_lo = wave * span, c_hi = min(a.H, c_lo + span);
-  __shared__ double red[kLtThreads / kWave][kWave][3];
+  __shared__ double red[kLtThreads / kWave][kWave];
   __shared__ float bred[kLtThreads / kWave][kWave];
-  __shared__ int use3;
-  // First pass: the two-part sums and the sum of |term| (fp32: relative error
-  // below 2^-13 over this lane's terms, against a 4x margin below).
-  Exact2 acc2{0.0, 0.0};
-  float bound = 0.0f;
+  __shared__ double xred[kLtThreads / kWave][3];
+  __shared__ unsigned long long undecided;
+  // First pass: plain fp64 sums and the sum of |term| (fp32, relative error
+  // below 2^-13 here).  Each product of two fp16 values is exact in fp32 and
+  // fp64, so a sum of n of them in any order is within (n - 1) 2^-53 sum|t|
+  // of the exact sum; where that interval (with the bias and a margin)
+  // rounds to one fp16 value, that value is the exact sum's.  4 fp64 and 4
+  // fp32 accumulators: independent add chains (the bound holds for any
+  // order of the adds).
+  double acc[4] = {0.0, 0.0, 0.0, 0.0};
+  float bnd[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll 4
   for (int c = c_lo; c < c_hi; c += 8) {
     const uint4 xv = *reinterpret_cast<const uint4*>(x + c);
@@ -115,61 +122,65 @@ __global__ void __launch_bounds__(kLtThreads) k_latent_tiled(RouteArgs a) {
     for (int q = 0; q < 4; ++q) {
       const float p0 = h2f((uint16_t)(xs[q] & 0xFFFFu)) * h2f((uint16_t)(ws[q] & 0xFFFFu));
       const float p1 = h2f((uint16_t)(xs[q] >> 16)) * h2f((uint16_t)(ws[q] >> 16));
-      bound += fabsf(p0) + fabsf(p1);
-      exact2_add(acc2, (double)p0);
-      exact2_add(acc2, (double)p1);
+      bnd[q] += fabsf(p0) + fabsf(p1);
+      acc[q] += (double)p0 + (double)p1;
     }
   }
-  red[wave][lane][0] = acc2.a0;
-  red[wave][lane][1] = acc2.a1;
-  bred[wave][lane] = bound;
+  red[wave][lane] = (acc[0] + acc[1]) + (acc[2] + acc[3]);
+  bred[wave][lane] = (bnd[0] + bnd[1]) + (bnd[2] + bnd[3]);
   __syncthreads();
-  Exact3 sum = exact_zero();
+  const bool real = r < a.R && t < a.rows;
   if (wave == 0) {
-    Exact2 s2{0.0, 0.0};
+    double sum1 = 0.0;
     float b = 0.0f;
 #pragma unroll
     for (int v = 0; v < kLtThreads / kWave; ++v) {
-      s2.a0 += red[v][lane][0];
-      s2.a1 += red[v][lane][1];
+      sum1 += red[v][lane];
       b += bred[v][lane];
     }
-    sum = exact2_to_3(s2);
-    // exact while the magnitudes stay below 2^40 (|a1| < 2^42 needed)
-    const bool big = !(b < 549755813888.0f);  // 2^39; also catches inf and nan
-    // every lane of wave 0 votes (one lane per output of the tile)
-    const bool any_big = __ballot(big) != 0ull;
-    if (lane == 0) use3 = any_big;
+    const double bias = a.enc_b != nullptr ? (double)h2f(a.enc_b[rc]) : 0.0;
+    const double sb = sum1 + bias;
+    // (H + 64) 2^-53 (2 b): the sums' rounding (2 b > sum|t|); 2^-49 (|sb| +
+    // |bias|): the bias add and the two interval ends' own rounding
+    const double B = (double)(a.H + 64) * 1.1102230246251565e-16 * (2.0 * (double)b) +
+                     1.7763568394002505e-15 * (fabs(sb) + fabs(bias));
+    const uint16_t lo = exact_to_f16(Exact3{sb - B, 0.0, 0.0});
+    const uint16_t hi = exact_to_f16(Exact3{sb + B, 0.0, 0.0});
+    const bool ok = b < 3.0e38f && fabs(sb) < 1.0e300 && lo == hi;  // false for inf and nan
+    if (ok && real) a.lat16[(long long)t * a.R + r] = lo;
+    const unsigned long long m = __ballot(!ok);
+    if (lane == 0) undecided = m;
   }
   __syncthreads();
-  if (use3) {
-    // Large terms: the three-part sums (exact for any fp16 inputs)
-    Exact3 acc = exact_zero();
-#pragma unroll 4
-    for (int c = c_lo; c < c_hi; c += 8) {
-      const uint4 xv = *reinterpret_cast<const uint4*>(x + c);
-      const uint4 wv = *reinterpret_cast<const uint4*>(w + c);
-      const uint32_t xs[4] = {xv.x, xv.y, xv.z, xv.w};
-      const uint32_t ws[4] = {wv.x, wv.y, wv.z, wv.w};
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        exact_add(acc, (double)(h2f((uint16_t)(xs[q] & 0xFFFFu)) * h2f((uint16_t)(ws[q] & 0xFFFFu))));
-        exact_add(acc, (double)(h2f((uint16_t)(xs[q] >> 16)) * h2f((uint16_t)(ws[q] >> 16))));
-      }
+  // The outputs the fp64 sums leave undecided (an exact sum within the
+  // bound of an fp16 rounding boundary, large cancelling terms, inf or nan),
+  // one at a time over the whole workgroup: the three-part sums (exact for
+  // any fp16 inputs, in any split of the terms) and one rounding.
+  unsigned long long m = undecided;
+  while (m != 0ull) {
+    const int l = __builtin_ctzll(m);
+    m &= m - 1ull;
+    const int ur = (int)blockIdx.x * kLtRows + (l >> 3), ut = (int)blockIdx.y * kLtTok + (l & 7);
+    const uint16_t* __restrict__ ux = a.x + (long long)min(ut, a.rows - 1) * a.H;
+    const uint16_t* __restrict__ uw = a.enc_w + (long long)min(ur, a.R - 1) * a.H;
+    Exact3 e = exact_zero();
+    for (int c = tid; c < a.H; c += kLtThreads) exact_add(e, (double)(h2f(ux[c]) * h2f(uw[c])));
+    e = wave_sum_exact(e);
+    if (lane == 0) {
+      xred[wave][0] = e.a0;
+      xred[wave][1] = e.a1;
+      xred[wave][2] = e.a2;
     }
-    __syncthreads();  // the first pass's partials have been read
-    red[wave][lane][0] = acc.a0;
-    red[wave][lane][1] = acc.a1;
-    red[wave][lane][2] = acc.a2;
     __syncthreads();
-    if (wave != 0) return;
-    sum = exact_zero();
+    if (tid == 0 && ur < a.R && ut < a.rows) {
+      Exact3 sum = exact_zero();
 #pragma unroll
-    for (int v = 0; v < kLtThreads / kWave; ++v) exact_merge(sum, Exact3{red[v][lane][0], red[v][lane][1], red[v][lane][2]});
+      for (int v = 0; v < kLtThreads / kWave; ++v) exact_merge(sum, Exact3{xred[v][0], xred[v][1], xred[v][2]});
+      if (a.enc_b != nullptr) exact_add(sum, (double)h2f(a.enc_b[ur]));
+      a.lat16[(long long)ut * a.R + ur] = exact_to_f16(sum);
+    }
+    __syncthreads();
   }
-  if (wave != 0) return;
-  if (a.enc_b != nullptr) exact_add(sum, (double)h2f(a.enc_b[rc]));
-  if (r < a.R && t < a.rows) a.lat16[(long long)t * a.R + r] = exact_to_f16(sum);
 }
 
 // Fewer than kLatSplitRows rows: one workgroup per (latent row, column range,

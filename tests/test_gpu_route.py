@@ -219,3 +219,34 @@ def test_route_tiled_latent_one_large_output_exact(gpu, orc):
         lat_o, sc_o, sel_o = orc.route(x16[t], w16, enc_b, swt, sb, k)
         assert np.array_equal(lat[t], lat_o), f"latent of row {t}"
         assert np.array_equal(sc[t], sc_o) and np.array_equal(sel[t], sel_o)
+
+
+def test_route_tiled_latent_fp16_ties_exact(gpu, orc):
+    """Outputs whose exact sum is an fp16 tie (1 + 2^-11, halfway between 1
+    and 1 + 2^-10; -3 - 2^-10, halfway between -3 and -3 - 2^-9): the tiled
+    latent's fast fp64 pass must leave them to the exact sums, which round
+    ties to even (1 and -3).  Every other output is random."""
+    H, R, N, NB, k = 2048, 16, 16, 40, 5
+    rng = np.random.default_rng(37)
+    x = (rng.standard_normal((N, H)) * 0.5).astype(np.float16)
+    w = (rng.standard_normal((R, H)) * 0.02).astype(np.float16)
+    # token 2 x latent row 5: 1 * 1 + 1 * 2^-11 (other terms zero)
+    x[2, :] = 0
+    w[5, :] = 0
+    x[2, 0] = x[2, 1] = np.float16(1.0)
+    w[5, 0], w[5, 1] = np.float16(1.0), np.float16(2.0 ** -11)
+    # token 11 x latent row 9: -1 * 3 - 1 * 2^-10
+    x[11, :] = 0
+    w[9, :] = 0
+    x[11, 0] = x[11, 1] = np.float16(-1.0)
+    w[9, 0], w[9, 1] = np.float16(3.0), np.float16(2.0 ** -10)
+    x16, w16 = x.view(np.uint16), w.view(np.uint16)
+    enc_b = np.zeros(R, dtype=np.uint16)
+    swt, sb = _rand16(rng, (NB, R), 0.02), _rand16(rng, NB, 0.02)
+    sel, lat, sc = _route_gpu(gpu, x16, w16, enc_b, swt, sb, k)
+    assert lat.view(np.float16)[2, 5] == np.float16(1.0)
+    assert lat.view(np.float16)[11, 9] == np.float16(-3.0)
+    for t in range(N):
+        lat_o, sc_o, sel_o = orc.route(x16[t], w16, enc_b, swt, sb, k)
+        assert np.array_equal(lat[t], lat_o), f"latent of row {t}"
+        assert np.array_equal(sc[t], sc_o) and np.array_equal(sel[t], sel_o)
