@@ -82,8 +82,22 @@ int nsmlp_workspace_init(void* ws, size_t ws_bytes, void* stream);
  * nsmlp_host_device_pointer; the caller zeroes it once) and clears the word,
  * in stream order, in one kernel (no memset: it may be captured in a graph).
  * The caller reads *dst once the stream has passed that point (an event), so
- * the launches in between are not stalled. */
+ * the launches in between are not stalled.  dst == NULL (version >= 104):
+ * the word is only cleared (e.g. before a call whose status is checked). */
 int nsmlp_workspace_take_status(void* ws, int32_t* dst, void* stream);
+
+/* Block-source counts (version >= 104).  The decode kernels count the
+ * selected blocks of every call that they read from HBM slots and from host
+ * copies into two counters of the workspace's counter region, kept until
+ * taken like the status word.  This takes them: dst[0] += blocks read from
+ * HBM slots, dst[1] += blocks read from host copies (int64, device memory or
+ * pinned host memory through its device pointer, 8-byte aligned), and the
+ * counters are cleared, in stream order, in one kernel.  Replaces the
+ * runtime status counters of RT:1694-1779 (incremented at RT:3926, 3934,
+ * 5263, 5279, 5328; the reference counts its decode_mlp_* entries once per
+ * gate and once per up projection, its decode_down_* entries once per
+ * block).  Decode calls only (the reference counts in the decode phase). */
+int nsmlp_workspace_take_block_counts(void* ws, int64_t* dst, void* stream);
 
 /* ------------------------------------------------------------------ router
  * Replaces RT:4311-4352 (_route_sparse_mlp) together with RT:4209-4238
@@ -165,6 +179,13 @@ typedef struct nsmlp_slot_table {
 size_t nsmlp_decode_workspace_bytes(int H, int k);
 int nsmlp_decode_slots_f16(const nsmlp_slot_table* table, const void* x, const int32_t* sel, int k, void* out,
                            void* ws, size_t ws_bytes, void* stream);
+/* The same with the decode loop's residual add fused into the output
+ * (version >= 104; RT:7774): out[o] = fp16(residual[o] + fp16(mlp(x)[o])),
+ * as nsmlp_decode_layer_add_f16 does it, for callers that route first (e.g.
+ * to promote the selected blocks into HBM slots before the decode reads
+ * them, so a missed block crosses the host link once: RT:4094-4131). */
+int nsmlp_decode_slots_add_f16(const nsmlp_slot_table* table, const void* x, const void* residual,
+                               const int32_t* sel, int k, void* out, void* ws, size_t ws_bytes, void* stream);
 
 /* Router + fused decode for one decode token (the decode branch of
  * RT:5833-5923 _mlp_forward_dispatch: route, then sparse MLP), entirely on
@@ -204,9 +225,11 @@ int nsmlp_decode_layer_add_f16(const nsmlp_router* router, const nsmlp_slot_tabl
  * nsmlp_decode_layer_add_f16), for the streaming shapes: hidden size a
  * multiple of 2048 up to 16384, num_blocks <= 4096, k <= 2048, and a scratch
  * need of at most 256 KiB (k up to about 1800); other shapes fail with
- * NSMLP_EINVAL and a message.  status_out (nullable, device or pinned host
- * memory, zeroed once by the caller): the call's status word is ORed into it
- * (see nsmlp_workspace_take_status) and the scratch's word cleared.  Every
+ * NSMLP_EINVAL and a message.  The scratch's status word and block counts
+ * are cleared at the start of every call (by its first kernel), so they hold
+ * that call's alone.  status_out (nullable, device or pinned host memory,
+ * zeroed once by the caller): the call's status word is ORed into it (see
+ * nsmlp_workspace_take_status).  Every
  * call on a device shares that device's scratch, which keeps the last call's
  * contents: calls that overlap on one GPU (other streams, other threads)
  * race. */
@@ -233,7 +256,11 @@ int nsmlp_decode_layer_noalloc_f16(const nsmlp_router* router, const nsmlp_slot_
  * RT:5439-5447; down weights as fp16 codes with the absmax applied to each
  * block's product in fp32), fp32 accumulation, act rounded to fp16 (RT:5459),
  * the down sums accumulated in fixed point (independent of scheduling).
- * M <= 65536 and M*H*2, M*k*64 < 2^31. */
+ * M <= 65536 and M*H*2, M*k*64 < 2^31.  The workspace grows with M: when
+ * the tokens' blocks cover most of the layer (M k >= 2 NB) the down runs as
+ * the dense GEMM over an act matrix [M][I] fp16 with S fp32 partials [M][H]
+ * (at the 405B shape about 0.36 MB per token, 2.9 GB at 8192 tokens): run
+ * long prompts in chunks (the reference's prefill is chunked too). */
 size_t nsmlp_prefill_workspace_bytes(int H, int NB, int M, int k);
 int nsmlp_prefill_slots_f16(const nsmlp_slot_table* table, const void* x, int M, const int32_t* sel, int k, void* out,
                             void* ws, size_t ws_bytes, void* stream);
@@ -245,7 +272,10 @@ int nsmlp_prefill_slots_f16(const nsmlp_slot_table* table, const void* x, int M,
  * out = fp16(act Wd^T + down_bias) (+ residual: fp16(residual + out)).
  * x [M][H] fp16 (16-byte aligned), residual [M][H] fp16 or NULL, out [M][H]
  * fp16.  H % 256 == 0, I % 128 == 0; blocks read from their HBM slots or
- * host copies.  Deterministic. */
+ * host copies.  Deterministic.  The tokens run in chunks of at most 1024
+ * (version >= 104; each token's result is that of one call over all tokens),
+ * so the workspace is bounded by the 1024-token size (at the 405B shape
+ * about 0.37 GB). */
 size_t nsmlp_dense_mlp_workspace_bytes(int H, int I, int M);
 int nsmlp_dense_mlp_slots_f16(const nsmlp_slot_table* table, const void* x, int M, const void* residual, void* out,
                               void* ws, size_t ws_bytes, void* stream);

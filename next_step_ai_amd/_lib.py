@@ -86,10 +86,12 @@ SIGNATURES: dict[str, tuple] = {
     "nsmlp_device_supported": (I32, [I32]),
     "nsmlp_workspace_init": (I32, [P, SZ, P]),
     "nsmlp_workspace_take_status": (I32, [P, P, P]),
+    "nsmlp_workspace_take_block_counts": (I32, [P, P, P]),
     "nsmlp_route_workspace_bytes": (SZ, [I32, I32, I32, I32, I32]),
     "nsmlp_route_f16": (I32, [P, I32, I32, P, P, I32, I32, P, P, P, I32, I32, I32, P, P, P, P, SZ, P]),
     "nsmlp_decode_workspace_bytes": (SZ, [I32, I32]),
     "nsmlp_decode_slots_f16": (I32, [ctypes.POINTER(SlotTable), P, P, I32, P, P, SZ, P]),
+    "nsmlp_decode_slots_add_f16": (I32, [ctypes.POINTER(SlotTable), P, P, P, I32, P, P, SZ, P]),
     "nsmlp_layer_workspace_bytes": (SZ, [I32, I32, I32, I32]),
     "nsmlp_decode_layer_f16": (I32, [ctypes.POINTER(Router), ctypes.POINTER(SlotTable), P, I32, P, P, P, SZ, P]),
     "nsmlp_decode_layer_add_f16": (I32, [ctypes.POINTER(Router), ctypes.POINTER(SlotTable), P, P, I32, P, P, P, SZ,

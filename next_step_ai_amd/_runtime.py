@@ -96,6 +96,12 @@ class StatusWord:
         self._dptr = int(out.value)
         self._event: torch.cuda.Event | None = None
 
+    def clear(self, ws: torch.Tensor) -> None:
+        """Clear the workspace's status word (in stream order) so that the
+        next take reports the calls enqueued after this point only, not bits
+        an earlier unchecked call on the same workspace left."""
+        _lib.call("nsmlp_workspace_take_status", ptr(ws), None, stream_handle(self.device))
+
     def take(self, ws: torch.Tensor) -> None:
         if torch.cuda.is_current_stream_capturing():
             raise RuntimeError(f"{self.what}: the status check cannot run inside a graph capture")
@@ -119,6 +125,33 @@ class StatusWord:
         if self._event is not None:
             self._event.synchronize()
             self._read()
+
+
+class BlockCounts:
+    """Running counts of the selected blocks a layer's decode calls read from
+    HBM slots and from host copies (the reference's runtime status counters,
+    RT:1694-1779).  ``take(ws)`` enqueues ``nsmlp_workspace_take_block_counts``
+    into a device int64 [2] (no stall; it may be captured in a graph);
+    ``hbm``/``host`` read the totals (they wait for the stream)."""
+
+    def __init__(self, device: torch.device):
+        self.device = device
+        self.counts = torch.zeros(2, dtype=torch.int64, device=device)
+
+    def clear(self, ws: torch.Tensor) -> None:
+        """Drop what earlier calls left in the workspace's counters."""
+        junk = torch.zeros(2, dtype=torch.int64, device=self.device)
+        _lib.call("nsmlp_workspace_take_block_counts", ptr(ws), ptr(junk), stream_handle(self.device))
+
+    def take(self, ws: torch.Tensor) -> None:
+        _lib.call("nsmlp_workspace_take_block_counts", ptr(ws), ptr(self.counts), stream_handle(self.device))
+
+    def totals(self) -> tuple[int, int]:
+        c = self.counts.to("cpu")
+        return int(c[0]), int(c[1])
+
+    def reset(self) -> None:
+        self.counts.zero_()
 
 
 def nf4_code(device: torch.device) -> torch.Tensor:

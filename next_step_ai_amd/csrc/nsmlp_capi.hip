@@ -20,6 +20,7 @@ constexpr size_t kAlign = 256;
 // Fixed counter region at the start of every workspace (zeroed once by
 // nsmlp_workspace_init, restored to zero by the kernels that use it).
 constexpr size_t kStatusOff = 0;
+constexpr size_t kServedOff = 16;  // [2] u32 block counts: HBM slots, host copies
 constexpr size_t kBlkCountOff = 256;
 constexpr int kMaxK = 32768;
 constexpr size_t kRowCountOff = kBlkCountOff + (size_t)kMaxK * sizeof(int);
@@ -163,6 +164,7 @@ int fill_decode_ws(DecodeArgs& a, void* ws, size_t ws_bytes) {
   if (((uintptr_t)ws & (kAlign - 1)) != 0) return set_error(NSMLP_EINVAL, "workspace must be 256-byte aligned");
   char* base = (char*)ws;
   a.status = (int*)(base + kStatusOff);
+  a.served = (uint32_t*)(base + kServedOff);
   a.blk_count = (int*)(base + kBlkCountOff);
   a.row_count = (int*)(base + kRowCountOff);
   a.part = (float*)(base + L.part);
@@ -238,6 +240,7 @@ int fill_route(RouteArgs& r, const void* x, int rows, int H, const void* enc_w, 
   r.scores = (uint16_t*)(base + L.scores);
   r.status = (int*)(base + kStatusOff);
   r.lat_part = rows < kLatSplitRows ? (double*)(base + L.lat_part) : nullptr;
+  r.clear_words = nullptr;
   return NSMLP_OK;
 }
 
@@ -408,7 +411,7 @@ extern "C" {
 
 const char* nsmlp_last_error(void) { return g_err; }
 
-int nsmlp_version(void) { return 103; }
+int nsmlp_version(void) { return 104; }
 
 int nsmlp_device_supported(int device) {
   hipDeviceProp_t prop;
@@ -424,10 +427,18 @@ int nsmlp_workspace_init(void* ws, size_t ws_bytes, void* stream) {
 }
 
 int nsmlp_workspace_take_status(void* ws, int32_t* dst, void* stream) {
-  if (ws == nullptr || dst == nullptr) return set_error(NSMLP_EINVAL, "ws and dst must be non-NULL");
+  if (ws == nullptr) return set_error(NSMLP_EINVAL, "ws must be non-NULL");
   if (((uintptr_t)ws & (kAlign - 1)) != 0) return set_error(NSMLP_EINVAL, "workspace must be 256-byte aligned");
   launch_take_status((int*)((char*)ws + kStatusOff), (int*)dst, (hipStream_t)stream);
   return check_launch("take status");
+}
+
+int nsmlp_workspace_take_block_counts(void* ws, int64_t* dst, void* stream) {
+  if (ws == nullptr || dst == nullptr) return set_error(NSMLP_EINVAL, "ws and dst must be non-NULL");
+  if (((uintptr_t)ws & (kAlign - 1)) != 0) return set_error(NSMLP_EINVAL, "workspace must be 256-byte aligned");
+  if (((uintptr_t)dst & 7) != 0) return set_error(NSMLP_EINVAL, "dst must be 8-byte aligned");
+  launch_take_counts((uint32_t*)((char*)ws + kServedOff), (long long*)dst, (hipStream_t)stream);
+  return check_launch("take block counts");
 }
 
 size_t nsmlp_route_workspace_bytes(int rows, int H, int R, int NB, int k) {
@@ -453,8 +464,8 @@ int nsmlp_route_f16(const void* x, int rows, int H, const void* enc_w, const voi
 
 size_t nsmlp_decode_workspace_bytes(int H, int k) { return decode_ws_layout(H, k).total; }
 
-int nsmlp_decode_slots_f16(const nsmlp_slot_table* table, const void* x, const int32_t* sel, int k, void* out,
-                           void* ws, size_t ws_bytes, void* stream) {
+static int decode_slots(const nsmlp_slot_table* table, const void* x, const void* residual, const int32_t* sel,
+                        int k, void* out, void* ws, size_t ws_bytes, void* stream) {
   DecodeArgs a;
   int rc = table_to_args(table, a);
   if (rc) return rc;
@@ -467,10 +478,22 @@ int nsmlp_decode_slots_f16(const nsmlp_slot_table* table, const void* x, const i
   a.k = k;
   a.sel = sel;
   a.out = (uint16_t*)out;
+  a.residual = (const uint16_t*)residual;
   rc = fill_decode_ws(a, ws, ws_bytes);
   if (rc) return rc;
   fill_decode_tiling(a);
   return run_decode(a, (hipStream_t)stream);
+}
+
+int nsmlp_decode_slots_f16(const nsmlp_slot_table* table, const void* x, const int32_t* sel, int k, void* out,
+                           void* ws, size_t ws_bytes, void* stream) {
+  return decode_slots(table, x, nullptr, sel, k, out, ws, ws_bytes, stream);
+}
+
+int nsmlp_decode_slots_add_f16(const nsmlp_slot_table* table, const void* x, const void* residual,
+                               const int32_t* sel, int k, void* out, void* ws, size_t ws_bytes, void* stream) {
+  if (residual == nullptr) return set_error(NSMLP_EINVAL, "residual must be non-NULL");
+  return decode_slots(table, x, residual, sel, k, out, ws, ws_bytes, stream);
 }
 
 size_t nsmlp_layer_workspace_bytes(int H, int R, int NB, int k) {
@@ -590,6 +613,7 @@ int nsmlp_decode_layer_noalloc_f16(const nsmlp_router* router, const nsmlp_slot_
   rc = device_scratch(s, &base);
   if (rc) return rc;
   a.status = (int*)base;
+  a.served = (uint32_t*)(base + kServedOff);
   a.st_act = (float*)(base + o_act);
   a.st_enc = (uint32_t*)(base + o_enc);
   a.st_bid = (int32_t*)(base + o_bid);
@@ -598,6 +622,9 @@ int nsmlp_decode_layer_noalloc_f16(const nsmlp_router* router, const nsmlp_slot_
   fill_route(r, x, 1, a.H, router->enc_w, router->enc_b, router->R, router->basis_top_k, router->score_w,
              router->score_b, router->down_block_norm, router->NB, router->flags & NSMLP_ROUTE_LEGACY_ABS, k, nullptr,
              nullptr, nullptr, base, o_route);
+  // the call's status word and block counts start at zero: the first router
+  // kernel clears them before anything of the call is written
+  r.clear_words = (int*)base;
   launch_route_scores(r, s);
   rc = check_launch("route");
   if (rc) return rc;
@@ -690,6 +717,8 @@ int nsmlp_prefill_slots_f16(const nsmlp_slot_table* table, const void* x, int M,
   off += align_up(nk * 4);
   // the grouped down fits in the dense path's workspace (M k <= M NB)
   if (prefill_dense_down(p.d.H, p.d.NB, M, k) && dense_down_fits(p.d, dense_guard_splits(p.d.H, p.d.NB, M))) {
+    rc = dense_down_check();
+    if (rc) return rc;
     p.act_dense = (uint16_t*)(base + off);
     off += align_up((size_t)M * p.d.NB * 64);
     p.part = (float*)(base + off);
@@ -701,10 +730,19 @@ int nsmlp_prefill_slots_f16(const nsmlp_slot_table* table, const void* x, int M,
   return check_launch("prefill");
 }
 
+// The dense MLP runs the tokens in chunks of at most kDenseChunk (a multiple
+// of the 256-token tile, so each token's tile and sums are those of one
+// call over all tokens): the workspace, act [chunk][I] fp16 and S partials
+// [chunk][H] fp32, stays bounded however long the prompt (at the 405B shape
+// about 0.37 GB instead of 2.9 GB at 8192 tokens).  Each chunk reads the
+// weights once more, a few percent of its MFMA time.
+constexpr int kDenseChunk = 1024;
+
 size_t nsmlp_dense_mlp_workspace_bytes(int H, int I, int M) {
   if (H <= 0 || I <= 0 || M <= 0) return 0;
   const size_t S = (size_t)dense_guard_splits(H, I / 32, M);
-  return align_up(kCounterBytes) + align_up((size_t)M * I * 2) + align_up(S * M * H * 4);
+  const size_t Mc = (size_t)(M < kDenseChunk ? M : kDenseChunk);
+  return align_up(kCounterBytes) + align_up(Mc * I * 2) + align_up(S * Mc * H * 4);
 }
 
 int nsmlp_dense_mlp_slots_f16(const nsmlp_slot_table* table, const void* x, int M, const void* residual, void* out,
@@ -719,8 +757,8 @@ int nsmlp_dense_mlp_slots_f16(const nsmlp_slot_table* table, const void* x, int 
   if (g.d.qbs < 32 || (g.d.qbs & (g.d.qbs - 1)) != 0 || H % g.d.qbs != 0)
     return set_error(NSMLP_EINVAL, "quant block size %d must be a power of two >= 32 dividing %d", g.d.qbs, H);
   if (M <= 0) return set_error(NSMLP_EINVAL, "M=%d must be positive", M);
-  if ((long long)M * I * 2 >= (1LL << 31) || (long long)M * H * 2 >= (1LL << 31))
-    return set_error(NSMLP_EINVAL, "M=%d too large for one dense MLP call at H=%d, I=%d (split the tokens)", M, H, I);
+  if ((long long)kDenseChunk * I * 2 >= (1LL << 31) || (long long)kDenseChunk * H * 2 >= (1LL << 31))
+    return set_error(NSMLP_EINVAL, "dense MLP shape H=%d, I=%d too large", H, I);
   if (!x || !out) return set_error(NSMLP_EINVAL, "x and out must be non-NULL");
   if (!aligned16(x)) return set_error(NSMLP_EINVAL, "x must be 16-byte aligned");
   const size_t need = nsmlp_dense_mlp_workspace_bytes(H, I, M);
@@ -735,14 +773,24 @@ int nsmlp_dense_mlp_slots_f16(const nsmlp_slot_table* table, const void* x, int 
   g.S = dense_guard_splits(H, g.d.NB, M);
   if (!dense_down_fits(g.d, g.S))
     return set_error(NSMLP_EINVAL, "dense MLP: the down weights of %d slots at H=%d exceed 31-bit offsets", g.d.n_slots, H);
+  rc = dense_down_check();
+  if (rc) return rc;
+  const int Mc = M < kDenseChunk ? M : kDenseChunk;
   size_t off = align_up(kCounterBytes);
   g.act = (uint16_t*)(base + off);
-  off += align_up((size_t)M * I * 2);
+  off += align_up((size_t)Mc * I * 2);
   g.part = (float*)(base + off);
-  g.out = (uint16_t*)out;
-  g.residual = (const uint16_t*)residual;
-  launch_dense_guard(g, (hipStream_t)stream);
-  return check_launch("dense MLP");
+  for (int t0 = 0; t0 < M; t0 += kDenseChunk) {
+    DenseGuardArgs c = g;
+    c.M = M - t0 < kDenseChunk ? M - t0 : kDenseChunk;
+    c.x = (const uint16_t*)x + (size_t)t0 * H;
+    c.out = (uint16_t*)out + (size_t)t0 * H;
+    c.residual = residual ? (const uint16_t*)residual + (size_t)t0 * H : nullptr;
+    launch_dense_guard(c, (hipStream_t)stream);
+    rc = check_launch("dense MLP");
+    if (rc) return rc;
+  }
+  return NSMLP_OK;
 }
 
 size_t nsmlp_single_kernel_workspace_bytes(int H, int top_k) { return decode_ws_layout(H, top_k).total; }

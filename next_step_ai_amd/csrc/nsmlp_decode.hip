@@ -74,6 +74,7 @@ __device__ __forceinline__ void gate_up_task(const DecodeArgs& a, DecodeSmem& sm
 
   const BlockRef br = resolve_block(a, j);
   if (!br.ok && !br.silent && tid == 0 && s == 0) atomicOr(a.status, 1);
+  if (br.ok && tid == 0 && s == 0 && a.served != nullptr) atomicAdd(a.served + (br.dev ? 0 : 1), 1u);
   const uint8_t* gbase = (br.dev ? a.gate.packed : a.host_gate.packed) + br.q * a.gate.blk_stride;
   const uint8_t* ubase = (br.dev ? a.up.packed : a.host_up.packed) + br.q * a.up.blk_stride;
   const float* gabs = (br.dev ? a.gate.absmax : a.host_gate.absmax) + br.q * a.gate.abs_blk_stride;

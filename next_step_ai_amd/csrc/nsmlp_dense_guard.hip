@@ -718,6 +718,36 @@ void dg_set_lds() {
 
 }  // namespace
 
+// k_dg_down reads its code-pair table and token stages at fixed LDS
+// addresses (immediate offsets from 0): that holds only while the kernel has
+// no static LDS, so that its dynamic LDS starts at address 0.  Checked once
+// per process on the compiled kernels, before the first launch.
+int dense_down_check() {
+  static std::once_flag once;
+  static size_t static_lds = 0;
+  static int rc_attr = 0;
+  std::call_once(once, [] {
+    for (int q = 0; q < 2; ++q)
+      for (int h = 0; h < 2; ++h)
+        for (int m = 0; m < 4; ++m) {
+          hipFuncAttributes attr;
+          if (hipFuncGetAttributes(&attr, reinterpret_cast<const void*>(kDgDown[q][h][m])) != hipSuccess) {
+            rc_attr = 1;
+            continue;
+          }
+          if (attr.sharedSizeBytes > static_lds) static_lds = attr.sharedSizeBytes;
+        }
+  });
+  if (rc_attr) {
+    (void)hipGetLastError();
+    return set_error(NSMLP_EHIP, "dense down GEMM: kernel attributes unavailable");
+  }
+  if (static_lds != 0)
+    return set_error(NSMLP_EHIP, "dense down GEMM has %zu bytes of static LDS; its LDS reads assume its dynamic LDS "
+                                 "starts at address 0", static_lds);
+  return NSMLP_OK;
+}
+
 int dense_down_refs(int NB, int S) { return 2 * ((NB / 2 + S - 1) / S); }
 
 bool dense_down_fits(const DecodeArgs& d, int S) {

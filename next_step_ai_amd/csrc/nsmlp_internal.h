@@ -689,6 +689,9 @@ struct DecodeArgs {
   int32_t* st_bid;       // [k] block ids of the selected positions (streaming)
   int st_gu_a2bytes;     // extent of gate/up absmax2 (bytes)
   int st_dn_a2n;         // down absmax2 entries staged per 64-row chunk
+  // [2] selected blocks read from HBM slots, from host copies (added per
+  // call, kept until taken); nullptr: not counted
+  uint32_t* served;
 };
 
 // Output row o of a decode: the MLP sum y (+ bias) rounded once to fp16;
@@ -779,6 +782,9 @@ void launch_dense_down(const DenseGuardArgs& g, hipStream_t s);
 // host copy addressable by 31-bit offsets, the range's block references in LDS.
 bool dense_down_fits(const DecodeArgs& d, int S);
 int dense_down_refs(int NB, int S);
+// NSMLP_OK when the down GEMM's compiled kernels have no static LDS (its LDS
+// addressing assumes so); otherwise an error status with the message set.
+int dense_down_check();
 
 // Dense NF4 rows (the LM head): y[t][o] = sum_i W[o][i] x[t][i] over a
 // row-major [out][in] NF4 matrix, in % 32 == 0, in <= 16384.
@@ -866,7 +872,12 @@ struct RouteArgs {
   // column ranges [rows][R][kLatParts] x (a0, a1, a2), merged and rounded by
   // the scores kernel; nullptr otherwise
   double* lat_part;
+  // [kClearWords] words zeroed by the first latent kernel before anything of
+  // the call is written (the per-call status and block counts of a shared
+  // scratch); nullptr: none
+  int* clear_words;
 };
+constexpr int kClearWords = 8;
 constexpr int kLatSplitRows = 8;
 constexpr int kLatParts = 4;
 
@@ -895,6 +906,7 @@ void launch_output_linear(const LinearArgs& a, hipStream_t s);
 void launch_input_linear(const LinearArgs& a, hipStream_t s);
 void launch_zero_u32(uint32_t* p, long long n, hipStream_t s);
 void launch_take_status(int* status, int* dst, hipStream_t s);
+void launch_take_counts(uint32_t* counts, long long* dst, hipStream_t s);
 void launch_silu_mul(const uint16_t* g, const uint16_t* u, uint16_t* out, long long n, hipStream_t s);
 template <typename AbsT>  // float or uint8_t (double-quantised codes)
 void launch_gather_rows(const uint8_t* src, const AbsT* src_abs, const int32_t* blocks, int src_blocks, int n,

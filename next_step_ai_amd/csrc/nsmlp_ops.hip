@@ -143,9 +143,22 @@ __global__ void k_take_status(int* status, int* dst) {
   if (threadIdx.x == 0) {
     const int v = *status;
     *status = 0;
-    if (v != 0) {
+    if (v != 0 && dst != nullptr) {
       const int old = __hip_atomic_load(dst, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
       __hip_atomic_store(dst, old | v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+    }
+  }
+}
+
+// Block counts [2] of a workspace added to dst [2] (int64) and cleared.
+__global__ void k_take_counts(uint32_t* counts, long long* dst) {
+  if (threadIdx.x < 2) {
+    const uint32_t v = counts[threadIdx.x];
+    counts[threadIdx.x] = 0;
+    if (v != 0) {
+      long long* d = dst + threadIdx.x;
+      const long long old = __hip_atomic_load(d, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+      __hip_atomic_store(d, old + (long long)v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
     }
   }
 }
@@ -340,6 +353,10 @@ void launch_zero_u32(uint32_t* p, long long n, hipStream_t s) {
 
 void launch_take_status(int* status, int* dst, hipStream_t s) {
   hipLaunchKernelGGL(k_take_status, dim3(1), dim3(64), 0, s, status, dst);
+}
+
+void launch_take_counts(uint32_t* counts, long long* dst, hipStream_t s) {
+  hipLaunchKernelGGL(k_take_counts, dim3(1), dim3(64), 0, s, counts, dst);
 }
 
 void launch_silu_mul(const uint16_t* g, const uint16_t* u, uint16_t* out, long long n, hipStream_t s) {

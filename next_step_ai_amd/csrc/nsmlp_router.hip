@@ -196,6 +196,7 @@ __global__ void __launch_bounds__(kLpThreads) k_latent_part(RouteArgs a) {
   kernarg_warm<sizeof(RouteArgs)>();
   const int r = blockIdx.x, p = blockIdx.y, row = blockIdx.z;
   const int tid = threadIdx.x, wave = tid / kWave, lane = tid % kWave;
+  if (a.clear_words != nullptr && (r | p | row) == 0 && tid < kClearWords) a.clear_words[tid] = 0;
   const uint16_t* __restrict__ x = a.x + (long long)row * a.H;
   const uint16_t* __restrict__ w = a.enc_w + (long long)r * a.H;
   const int span = (a.H + kLatParts * 8 - 1) / (kLatParts * 8) * 8;  // columns per range, a multiple of 8

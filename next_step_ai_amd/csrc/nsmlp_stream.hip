@@ -268,6 +268,9 @@ __device__ __forceinline__ void pin_gu_rest(DecodeArgs& a) {
   }
   a.gate.absmax2 = (const float*)g2;
   a.up.absmax2 = (const float*)u2;
+  auto served = gptr(a.served);
+  asm volatile("" : "+s"(served));
+  a.served = (uint32_t*)served;
 }
 
 // SKPT > 0: the workgroup first selects the top k of a.sel_scores itself (SKPT
@@ -388,6 +391,18 @@ __global__ void __launch_bounds__(kThreads8, 2) k_gu_rep(DecodeArgs args) {
 #pragma unroll
   for (int i = 0; i < kGuStages; ++i)
     gu_issue<DQ>(a, i < R ? lane_value(enc_v, i) : kBad, ((i * nwg + wg) * NS + q) & 15, cb, ca, st[i]);
+  sched_fence();
+  // block-source counts (behind the stages: nothing waits for them early),
+  // one per selected block: its row pair 0 at split 0
+  if (a.served != nullptr && s == 0) {
+    const bool first = own && (id0 & 15) == 0 && !(enc_v & kBad);
+    const unsigned long long mh = __ballot(first && !(enc_v & kHostBit));
+    const unsigned long long mc = __ballot(first && (enc_v & kHostBit));
+    if (lane == 0) {
+      if (mh) atomicAdd(a.served, (uint32_t)__popcll(mh));
+      if (mc) atomicAdd(a.served + 1, (uint32_t)__popcll(mc));
+    }
+  }
   sched_fence();
   lut_store(lds, codes, tid);
   if constexpr (DQ) lds[kGuCode2Word + tid] = __float_as_uint(c2v);

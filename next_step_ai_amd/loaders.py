@@ -180,19 +180,25 @@ def write_nf4_safetensors(path: str | os.PathLike, params: dict[str, Nf4Param]) 
     from safetensors.torch import save_file
 
     out: dict[str, torch.Tensor] = {}
+
+    def own(t: torch.Tensor) -> torch.Tensor:
+        # a tensor the caller passes for several parameters (one code book for
+        # gate, up and down) is written once per key, as separate storage
+        return t.clone() if any(t.data_ptr() == o.data_ptr() for o in out.values()) else t
+
     for name, p in params.items():
         meta = {"quant_type": "nf4", "blocksize": int(p.blocksize), "dtype": p.dtype, "shape": list(p.shape)}
-        out[name] = p.packed.reshape(-1, 1).to("cpu", torch.uint8).contiguous()
-        out[f"{name}.quant_map"] = p.code.to("cpu", torch.float32).contiguous()
+        out[name] = own(p.packed.reshape(-1, 1).to("cpu", torch.uint8).contiguous())
+        out[f"{name}.quant_map"] = own(p.code.to("cpu", torch.float32).contiguous())
         if p.nested:
             a = p.absmax
-            out[f"{name}.absmax"] = a.q.reshape(-1).to("cpu", torch.uint8).contiguous()
-            out[f"{name}.nested_absmax"] = a.absmax2.to("cpu", torch.float32).contiguous()
-            out[f"{name}.nested_quant_map"] = a.code2.to("cpu", torch.float32).contiguous()
+            out[f"{name}.absmax"] = own(a.q.reshape(-1).to("cpu", torch.uint8).contiguous())
+            out[f"{name}.nested_absmax"] = own(a.absmax2.to("cpu", torch.float32).contiguous())
+            out[f"{name}.nested_quant_map"] = own(a.code2.to("cpu", torch.float32).contiguous())
             meta.update({"nested_blocksize": int(a.blocksize), "nested_dtype": "float32",
                          "nested_offset": float(a.offset)})
         else:
-            out[f"{name}.absmax"] = p.absmax.reshape(-1).to("cpu", torch.float32).contiguous()
+            out[f"{name}.absmax"] = own(p.absmax.reshape(-1).to("cpu", torch.float32).contiguous())
         out[f"{name}.{_QS_PREFIX}nf4"] = torch.tensor(list(json.dumps(meta).encode("utf-8")), dtype=torch.uint8)
     save_file(out, os.fspath(path))
 

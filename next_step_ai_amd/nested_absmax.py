@@ -51,6 +51,12 @@ def dynamic_map_device(device: torch.device) -> torch.Tensor:
     return t
 
 
+def default_offset(absmax: torch.Tensor) -> float:
+    """bitsandbytes' compress_statistics offset: the mean of the absmax,
+    summed in fp64 and rounded once to fp32."""
+    return float(np.float32(absmax.to(torch.float64).mean().item()))
+
+
 @dataclass
 class NestedAbsmax:
     """u8 absmax codes ``q`` (the fp32 absmax's shape), second-level scales
@@ -83,7 +89,7 @@ class NestedAbsmax:
         device = require_device(absmax, "absmax")
         a = absmax.to(dtype=torch.float32).contiguous().reshape(-1)
         c2 = dynamic_map_device(device) if code2 is None else code2.to(device=device, dtype=torch.float32).contiguous()
-        off = float(np.float32(a.double().mean().item())) if offset is None else float(np.float32(offset))
+        off = default_offset(a) if offset is None else float(np.float32(offset))
         n = int(a.numel())
         q = torch.empty(n, dtype=torch.uint8, device=device)
         a2 = torch.empty((n + blocksize - 1) // blocksize, dtype=torch.float32, device=device)

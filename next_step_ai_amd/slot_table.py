@@ -29,7 +29,7 @@ import ctypes
 import torch
 
 from . import _lib
-from ._runtime import StatusWord, nf4_code, ptr, require_device, stream_handle, workspace
+from ._runtime import BlockCounts, StatusWord, nf4_code, ptr, require_device, stream_handle, workspace
 from .layout import (MlpBlockBankLayout, build_intermediate_mlp_block_bank_layout,
                      validate_intermediate_mlp_block_bank_params)
 from .nested_absmax import NestedAbsmax
@@ -273,12 +273,23 @@ class SparseMlpSlotTable:
         self._struct = st
         return st
 
-    def _checked(self, ws: torch.Tensor, what: str) -> None:
+    def _status_for(self, ws: torch.Tensor, what: str, check: bool) -> StatusWord | None:
+        """With ``check``: a status word for the call about to be enqueued on
+        ``ws``, whose earlier bits (from unchecked calls sharing the
+        workspace) are cleared first, so the check reports this call alone."""
+        if not check:
+            return None
+        sw = StatusWord(self.device, what)
+        sw.clear(ws)
+        return sw
+
+    @staticmethod
+    def _checked(sw: StatusWord | None, ws: torch.Tensor) -> None:
         """Raise RuntimeError if the call just enqueued on ``ws`` reported a
         block it could not serve (waits for it)."""
-        sw = StatusWord(self.device, what)
-        sw.take(ws)
-        sw.check()
+        if sw is not None:
+            sw.take(ws)
+            sw.check()
 
     def decode(self, x: torch.Tensor, sel: torch.Tensor, out: torch.Tensor | None = None, *,
                check: bool = False) -> torch.Tensor:
@@ -294,10 +305,10 @@ class SparseMlpSlotTable:
         nbytes = int(_lib.lib().nsmlp_decode_workspace_bytes(self.H, k))
         ws = workspace(nbytes, self.device)
         st = self._struct if self._struct is not None else self.as_struct()
+        sw = self._status_for(ws, "sparse MLP decode", check)
         _lib.call("nsmlp_decode_slots_f16", ctypes.byref(st), ptr(x16), ptr(s), k, ptr(out), ptr(ws), ws.numel(),
                   stream_handle(self.device))
-        if check:
-            self._checked(ws, "sparse MLP decode")
+        self._checked(sw, ws)
         return out
 
 
@@ -319,10 +330,10 @@ class SparseMlpSlotTable:
         nbytes = int(_lib.lib().nsmlp_dense_mlp_workspace_bytes(self.H, self.I, M))
         ws = workspace(nbytes, self.device)
         st = self._struct if self._struct is not None else self.as_struct()
+        sw = self._status_for(ws, "dense-guard MLP", check)
         _lib.call("nsmlp_dense_mlp_slots_f16", ctypes.byref(st), ptr(x16), M, ptr(r16), ptr(out), ptr(ws), ws.numel(),
                   stream_handle(self.device))
-        if check:
-            self._checked(ws, "dense-guard MLP")
+        self._checked(sw, ws)
         return out
 
     def prefill(self, x: torch.Tensor, sel: torch.Tensor, out: torch.Tensor | None = None, *,
@@ -342,10 +353,10 @@ class SparseMlpSlotTable:
         nbytes = int(_lib.lib().nsmlp_prefill_workspace_bytes(self.H, self.NB, M, k))
         ws = workspace(nbytes, self.device)
         st = self._struct if self._struct is not None else self.as_struct()
+        sw = self._status_for(ws, "sparse MLP prefill", check)
         _lib.call("nsmlp_prefill_slots_f16", ctypes.byref(st), ptr(x16), M, ptr(s), k, ptr(out), ptr(ws), ws.numel(),
                   stream_handle(self.device))
-        if check:
-            self._checked(ws, "sparse MLP prefill")
+        self._checked(sw, ws)
         return out
 
 
@@ -473,13 +484,27 @@ class SparseMlpLayer:
     round trip (the decode branch of RT:5833-5923)."""
 
     def __init__(self, router: SparseMlpRouter, table: SparseMlpSlotTable, top_k: int,
-                 cache: HotBlockCache | None = None, *, check_blocks: bool = False):
+                 cache: HotBlockCache | None = None, *, check_blocks: bool = False, count_blocks: bool = False):
         """``check_blocks``: after every ``forward`` the kernels' status word
         is handed to a pinned host word (one small kernel, no stall); the
         next ``forward`` raises RuntimeError if a finished call selected a
         block that is neither resident nor host-copied, and
         ``check_status()`` waits and raises on demand (the reference's gather
-        raises for such a block, RT:4530-4578).  Not for graph capture."""
+        raises for such a block, RT:4530-4578).  Not for graph capture.
+
+        ``count_blocks``: every ``forward`` adds the selected blocks it read
+        from HBM slots and from host copies to running device counters (two
+        small kernels per call, no stall); ``served_blocks`` and
+        ``runtime_status()`` read them (the reference's runtime status,
+        RT:1694-1779).
+
+        With a hot-block ``cache`` a ``forward`` routes first, promotes the
+        selected blocks that are not resident into slots (copied once from the
+        host copies, the fixed-capacity plan of RT:2576-2617), then decodes
+        every selected block from HBM: a missed block crosses the host link
+        once, as in the reference, which promotes from the copy it already
+        moved to the GPU (RT:4094-4131).  A selected block that the plan
+        evicts is read from its host copy."""
         if router.NB != table.NB:
             raise RuntimeError(f"router num_blocks {router.NB} != table num_blocks {table.NB}")
         if cache is not None and cache.table is not table:
@@ -493,6 +518,23 @@ class SparseMlpLayer:
         self.device = table.device
         self._lookahead_done: torch.cuda.Event | None = None
         self._status = StatusWord(self.device, "sparse MLP decode layer") if check_blocks else None
+        self._counts = BlockCounts(self.device) if count_blocks else None
+
+    @property
+    def served_blocks(self) -> tuple[int, int]:
+        """(blocks read from HBM slots, blocks read from host copies), summed
+        over the ``forward`` calls so far (waits for the stream)."""
+        if self._counts is None:
+            raise RuntimeError("build the layer with count_blocks=True to count the served blocks")
+        return self._counts.totals()
+
+    def runtime_status(self) -> dict[str, int]:
+        """The reference's decode counters (RT:1694-1779) for this layer: its
+        gate and up projections each count a block (decode_mlp_*), its down
+        projection counts it once (decode_down_*)."""
+        hbm, host = self.served_blocks
+        return {"decode_mlp_hot_blocks_hit": 2 * hbm, "decode_mlp_cold_blocks_streamed": 2 * host,
+                "decode_down_hot_blocks_hit": hbm, "decode_down_cold_blocks_streamed": host}
 
     def check_status(self) -> None:
         """Wait for the last checked ``forward`` and raise RuntimeError if a
@@ -542,25 +584,45 @@ class SparseMlpLayer:
             sel_out = torch.empty(self.top_k, dtype=torch.int32, device=self.device)
         if ws is None:
             ws = workspace(self.workspace_bytes(), self.device)
-        if self._status is not None:
-            self._status.poll()  # a finished earlier call's report; no wait
-        if self._lookahead_done is not None:  # the promotion of a lookahead reads and writes the table
-            torch.cuda.current_stream(self.device).wait_event(self._lookahead_done)
-            self._lookahead_done = None
-        if residual is None:
-            _lib.call("nsmlp_decode_layer_f16", ctypes.byref(self._r), ctypes.byref(self._t), ptr(x16), self.top_k,
-                      ptr(sel_out), ptr(out), ptr(ws), ws.numel(), stream_handle(self.device))
-        else:
+        r16 = None
+        if residual is not None:
             r16 = residual.reshape(-1)
             if r16.dtype != torch.float16 or r16.device != self.device or not r16.is_contiguous() \
                     or int(r16.numel()) != self.table.H:
                 raise RuntimeError(f"residual must be a contiguous fp16 [{self.table.H}] tensor on {self.device}")
+        if self._status is not None:
+            self._status.poll()  # a finished earlier call's report; no wait
+            self._status.clear(ws)  # bits other calls left in the shared workspace are not this layer's
+        if self._counts is not None:
+            self._counts.clear(ws)
+        if self._lookahead_done is not None:  # the promotion of a lookahead reads and writes the table
+            torch.cuda.current_stream(self.device).wait_event(self._lookahead_done)
+            self._lookahead_done = None
+        h = stream_handle(self.device)
+        if self.cache is not None:
+            # route, promote the missed blocks into slots, then decode from HBM
+            r = self.router
+            flags = _lib.NSMLP_ROUTE_LEGACY_ABS if r.legacy_abs else 0
+            _lib.call("nsmlp_route_f16", ptr(x16), 1, self.table.H, ptr(r.enc_w), ptr(r.enc_b), r.R, r.basis_top_k,
+                      ptr(r.score_w), ptr(r.score_b), ptr(r.dbn), r.NB, flags, self.top_k, ptr(sel_out), None, None,
+                      ptr(ws), ws.numel(), h)
+            self.cache.promote(sel_out)
+            if r16 is None:
+                _lib.call("nsmlp_decode_slots_f16", ctypes.byref(self._t), ptr(x16), ptr(sel_out), self.top_k,
+                          ptr(out), ptr(ws), ws.numel(), h)
+            else:
+                _lib.call("nsmlp_decode_slots_add_f16", ctypes.byref(self._t), ptr(x16), ptr(r16), ptr(sel_out),
+                          self.top_k, ptr(out), ptr(ws), ws.numel(), h)
+        elif r16 is None:
+            _lib.call("nsmlp_decode_layer_f16", ctypes.byref(self._r), ctypes.byref(self._t), ptr(x16), self.top_k,
+                      ptr(sel_out), ptr(out), ptr(ws), ws.numel(), h)
+        else:
             _lib.call("nsmlp_decode_layer_add_f16", ctypes.byref(self._r), ctypes.byref(self._t), ptr(x16), ptr(r16),
-                      self.top_k, ptr(sel_out), ptr(out), ptr(ws), ws.numel(), stream_handle(self.device))
+                      self.top_k, ptr(sel_out), ptr(out), ptr(ws), ws.numel(), h)
         if self._status is not None:
             self._status.take(ws)
-        if self.cache is not None:  # the blocks that missed take slots for the next tokens
-            self.cache.promote(sel_out)
+        if self._counts is not None:
+            self._counts.take(ws)
         return out, sel_out
 
     def prefill(self, x: torch.Tensor, out: torch.Tensor | None = None):

@@ -55,11 +55,16 @@ def test_partial_residency_405b(gpu, orc):
     table = L.slot_table(resident_blocks=torch.from_numpy(resident), host_copy=True)
     lookup = table.lookup_cpu()
     assert int((lookup[torch.from_numpy(sel_np)] < 0).sum()) == MISSES
-    part = SparseMlpLayer(L.router(), table, K, check_blocks=True)
+    part = SparseMlpLayer(L.router(), table, K, check_blocks=True, count_blocks=True)
     y_part, sel_p = part.forward(L.x)
     part.check_status()
     assert torch.equal(sel_p, sel) and torch.equal(y_part, y_full)
-    print("[config 3] decode with 62 host misses bit-identical", flush=True)
+    # the block-source counts (the reference's runtime status counters)
+    assert part.served_blocks == (K - MISSES, MISSES)
+    st = part.runtime_status()
+    assert st["decode_down_hot_blocks_hit"] == K - MISSES and st["decode_down_cold_blocks_streamed"] == MISSES
+    assert st["decode_mlp_hot_blocks_hit"] == 2 * (K - MISSES) and st["decode_mlp_cold_blocks_streamed"] == 2 * MISSES
+    print("[config 3] decode with 62 host misses bit-identical; 146 HBM + 62 host blocks counted", flush=True)
 
     # prefill and dense guard through the same table (grouped down at 4
     # tokens, the dense down over the scattered act at 16) and the all-resident one
@@ -83,14 +88,22 @@ def test_partial_residency_405b(gpu, orc):
     scores = torch.zeros(RESIDENT)
     scores[: hit.size] = 1.0
     cache = HotBlockCache(table, scores=scores)
-    slots = cache.promote(sel, return_slots=True)
-    torch.cuda.synchronize()
-    assert int((slots >= 0).sum()) == MISSES
-    assert int((table.lookup_cpu()[torch.from_numpy(sel_np)] < 0).sum()) == 0
-    y_prom, sel_q = SparseMlpLayer(L.router(), table, K).forward(L.x)
+    # a layer with the cache routes, promotes the 62 misses into slots (one
+    # crossing of the host link), then decodes every block from HBM
+    cached = SparseMlpLayer(L.router(), table, K, cache=cache, count_blocks=True)
+    y_prom, sel_q = cached.forward(L.x)
     torch.cuda.synchronize()
     assert torch.equal(sel_q, sel) and torch.equal(y_prom, y_full)
-    del L, full, full_table, table, part, cache
+    assert int((table.lookup_cpu()[torch.from_numpy(sel_np)] < 0).sum()) == 0
+    assert cached.served_blocks == (K, 0), cached.served_blocks
+    y_again, _ = cached.forward(L.x)  # nothing left to promote
+    torch.cuda.synchronize()
+    assert torch.equal(y_again, y_full) and cached.served_blocks == (2 * K, 0)
+    slots = cache.promote(sel, return_slots=True)
+    torch.cuda.synchronize()
+    assert int((slots >= 0).sum()) == 0
+    print("[config 3] promote-first decode bit-identical, every block served from HBM", flush=True)
+    del L, full, full_table, table, part, cache, cached
     _free()
 
 

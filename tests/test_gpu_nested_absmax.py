@@ -33,6 +33,15 @@ def test_quantize_and_resolve_match_oracle(gpu, orc, dq_block):
     assert np.array_equal(_np(nest.q), q_o)
     back_o = orc.double_dequant(q_o, a2_o, off, dq_block=dq_block)
     assert np.array_equal(_np(res).view(np.uint32), back_o.view(np.uint32))
+    if dq_block == 256:
+        # the default offset (the mean, bitsandbytes' compress_statistics) and
+        # the codes it leads to equal the oracle's defaults
+        nest0 = NestedAbsmax.quantize(torch.from_numpy(absmax).to(gpu))
+        torch.cuda.synchronize()
+        q_d, a2_d, off_d = orc.double_quant(absmax)
+        assert nest0.offset == off_d and off_d != 0.0
+        assert np.array_equal(_np(nest0.q), q_d)
+        assert np.array_equal(_np(nest0.absmax2).view(np.uint32), a2_d.view(np.uint32))
 
 
 def test_q8_gathers_match_reference_slicing(gpu, orc):

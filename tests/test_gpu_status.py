@@ -83,3 +83,31 @@ def test_prefill_fixed_point_range_is_reported(gpu):
     t.down_absmax[b].fill_(1.0e7)  # block-major slots, identity lookup: slot b
     with pytest.raises(RuntimeError, match="fixed-point range"):
         t.prefill(x, sel, check=True)
+
+
+def test_checked_call_reports_its_own_status_only(gpu):
+    """An unchecked call that reads an unavailable block leaves its bit in the
+    shared workspace's status word; a checked call after it (a good one) does
+    not raise: the check clears the word before its call.  The same for a
+    checked layer after an unchecked layer on the same stream."""
+    from next_step_ai_amd.slot_table import SparseMlpLayer
+    from next_step_ai_amd.synth import make_synthetic_layer
+
+    H, I, R, k = 2048, 8192, 16, 40
+    L = make_synthetic_layer(H=H, I=I, R=R, seed=97, device=gpu)
+    full = L.slot_table()
+    _, sel = L.layer(k).forward(L.x)
+    missing = int(sel[2])
+    bad = L.slot_table(resident_blocks=torch.from_numpy(np.setdiff1d(np.arange(L.NB), [missing])))
+    bad.decode(L.x, sel)  # unchecked: leaves the bit
+    full.decode(L.x, sel, check=True)  # must not raise
+    bad.prefill(L.x.reshape(1, H).repeat(2, 1), sel.reshape(1, k).repeat(2, 1))
+    full.prefill(L.x.reshape(1, H).repeat(2, 1), sel.reshape(1, k).repeat(2, 1), check=True)
+    bad_layer = SparseMlpLayer(L.router(), bad, k)
+    good_layer = SparseMlpLayer(L.router(), full, k, check_blocks=True)
+    bad_layer.forward(L.x)
+    good_layer.forward(L.x)
+    good_layer.check_status()
+    # and the bad call, checked, still raises
+    with pytest.raises(RuntimeError, match="neither in an HBM slot"):
+        bad.decode(L.x, sel, check=True)

@@ -172,3 +172,22 @@ def test_routing_artifact_needing_code_is_refused(tmp_path):
     torch.save(pay, tmp_path / "u.pt")
     with pytest.raises(RuntimeError, match="cannot be loaded safely"):
         load_routing_artifact(tmp_path / "u.pt", hidden_size=64, intermediate_size=2048)
+
+
+def test_writer_takes_one_code_book_for_every_projection(tmp_path, orc):
+    """One code-book tensor passed for gate, up and down (and one dynamic map
+    for their nested states) is written under each key."""
+    from next_step_ai_amd.loaders import Nf4Param, SafetensorShards, load_nf4_param, write_nf4_safetensors
+
+    ps = {f"model.layers.0.mlp.{n}_proj.weight": _nf4(orc, 32, 64, 10 + i, True) for i, n in
+          enumerate(("gate", "up", "down"))}
+    code, code2 = ps["model.layers.0.mlp.gate_proj.weight"].code, None
+    for p in ps.values():
+        p.code = code
+        code2 = p.absmax.code2 if code2 is None else code2
+        p.absmax.code2 = code2
+    write_nf4_safetensors(tmp_path / "m.safetensors", ps)
+    s = SafetensorShards(tmp_path)
+    for name in ps:
+        r = load_nf4_param(s, name)
+        assert torch.equal(r.code, code) and torch.equal(r.absmax.code2, code2)

@@ -8,6 +8,7 @@ last bit (bitsandbytes takes a torch fp32 mean on the weight's device) stay
 unpinned (bitsandbytes==0.49.1 is absent); the decode only consumes
 (q, absmax2, code2, offset) as data."""
 import numpy as np
+import torch
 
 
 def _nearest_brute(m, v):
@@ -110,3 +111,36 @@ def test_double_dequant_exact_for_representable_values(orc):
     assert np.array_equal(q, np.arange(256, dtype=np.uint8))
     back = orc.double_dequant(q, got_a2, 0.0, m, dq_block=256)
     assert np.array_equal(back.view(np.uint32), vals.view(np.uint32))
+
+
+def test_double_quant_default_offset_is_the_mean(orc):
+    """bitsandbytes' compress_statistics subtracts the mean of the absmax
+    (an fp32 value) before the second-level quantisation; the oracle's
+    default offset is that mean: exactly (n + 1) / 2 for 1..n, the fp32
+    rounding of the mean for random values, the value itself for a constant
+    vector (whose centred entries are then all zero: the map's 0 code)."""
+    m = orc.dynamic_map_signed()
+    _, _, off = orc.double_quant(np.arange(1, 513, dtype=np.float32))
+    assert off == 256.5
+    rng = np.random.default_rng(5)
+    a = (np.abs(rng.standard_normal(4096)) * 0.03 + 0.002).astype(np.float32)
+    _, _, off = orc.double_quant(a)
+    assert np.float32(off) == np.float32(np.mean(a, dtype=np.float64)) and off != 0.0
+    c = np.full(512, 0.37, dtype=np.float32)
+    q, a2, off = orc.double_quant(c)
+    assert np.float32(off) == np.float32(0.37) and np.all(a2 == 0.0) and np.all(m[q] == 0.0)
+
+
+def test_package_default_offset_is_the_mean():
+    """The package's NestedAbsmax.quantize default offset, computed on the
+    host the same way from its argument (checked here without a device: the
+    offset is formed before any kernel runs)."""
+    import inspect
+
+    from next_step_ai_amd.nested_absmax import NestedAbsmax, default_offset
+
+    assert "offset" in inspect.signature(NestedAbsmax.quantize).parameters
+    assert default_offset(torch.arange(1, 513, dtype=torch.float32)) == 256.5
+    rng = np.random.default_rng(6)
+    a = (np.abs(rng.standard_normal(4096)) * 0.03 + 0.002).astype(np.float32)
+    assert default_offset(torch.from_numpy(a)) == float(np.float32(np.mean(a, dtype=np.float64)))

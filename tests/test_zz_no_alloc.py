@@ -79,6 +79,12 @@ def test_noalloc_reports_unavailable_blocks_and_rejects_large_shapes(gpu):
     _noalloc(full, L.x, status=status)  # the scratch's word was cleared by the hand-over
     torch.cuda.synchronize()
     assert int(status.item()) == 0
+    # a bad call without status_out leaves its bit in the scratch; the next
+    # call clears the word at its start, so it reports its own status only
+    _noalloc(layer, L.x)
+    _noalloc(full, L.x, status=status)
+    torch.cuda.synchronize()
+    assert int(status.item()) == 0
     big = make_synthetic_layer(H=2048, I=131072, R=16, seed=2104, device=gpu)  # 4096 blocks
     with pytest.raises(RuntimeError, match="per-device scratch holds 262144"):
         _noalloc(big.layer(2048), big.x)  # k = 2048 needs more than the scratch
