@@ -65,6 +65,20 @@ int nsmlp_version(void);
 /* 1 if device `device` is a gfx950 GPU usable by this library, else 0. */
 int nsmlp_device_supported(int device);
 
+/* Fault injection for tests of a caller's failure handling: the reference
+ * runtime's failure counter for its single-kernel decode (off after three
+ * failures, RT:5626-5637), its fallback on any v1 exception (RT:5681-5685)
+ * and its out-of-memory test by message (runtime/_helpers.py:301-308).
+ * spec = "name=kind[:count],..." arms the named compute entry points (name
+ * without the nsmlp_ prefix, or * for all of them) to fail before they touch
+ * the device: kind oom (NSMLP_EHIP, the message says "out of memory"), hip
+ * (NSMLP_EHIP), inval, nospc or nodev (NSMLP_EINVAL / _ENOSPC / _ENODEV);
+ * count = how many calls fail (default every call).  NULL or "" disarms.
+ * The environment variable NSMLP_FAULT_INJECT sets the same at load time.
+ * Process-wide; returns NSMLP_EINVAL for a bad spec (the rules stay as they
+ * were). */
+int nsmlp_fault_inject(const char* spec);
+
 /* Zero the counter region of a workspace; call once after allocating it.
  * The first int32 of a workspace is a status word, set by the kernels and
  * kept until the caller clears it:

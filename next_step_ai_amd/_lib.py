@@ -84,6 +84,7 @@ SIGNATURES: dict[str, tuple] = {
     "nsmlp_last_error": (ctypes.c_char_p, []),
     "nsmlp_version": (I32, []),
     "nsmlp_device_supported": (I32, [I32]),
+    "nsmlp_fault_inject": (I32, [ctypes.c_char_p]),
     "nsmlp_workspace_init": (I32, [P, SZ, P]),
     "nsmlp_workspace_take_status": (I32, [P, P, P]),
     "nsmlp_workspace_take_block_counts": (I32, [P, P, P]),
@@ -164,3 +165,28 @@ def call(name: str, *args) -> None:
     """Call a status-returning entry point; raise RuntimeError on failure."""
     rc = getattr(lib(), name)(*args)
     check(int(rc), name)
+
+
+def fault_inject(spec: str | None) -> None:
+    """Arm (or, with None or "", disarm) the library's fault injection: the
+    compute entry points named in ``spec`` ("name=kind[:count],...", names
+    without the nsmlp_ prefix or ``*``; kind oom, hip, inval, nospc or nodev)
+    fail before they touch the device, so the drop-ins raise RuntimeError as
+    on a real failure.  Process-wide; see nsmlp_fault_inject in nsmlp.h."""
+    check(int(lib().nsmlp_fault_inject(None if not spec else spec.encode())), "nsmlp_fault_inject")
+
+
+class injected_faults:
+    """Context manager: ``with injected_faults("single_kernel_decode_f16=hip:3"):``
+    arms the spec and disarms it on exit."""
+
+    def __init__(self, spec: str):
+        self.spec = spec
+
+    def __enter__(self):
+        fault_inject(self.spec)
+        return self
+
+    def __exit__(self, *exc):
+        fault_inject(None)
+        return False

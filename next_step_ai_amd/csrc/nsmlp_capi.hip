@@ -6,6 +6,7 @@
 #include <stdlib.h>
 #include <string.h>
 
+#include <atomic>
 #include <mutex>
 
 #include "nsmlp_internal.h"
@@ -39,6 +40,132 @@ int env_int(const char* name, int dflt) {
   if (v == nullptr || *v == 0) return dflt;
   return atoi(v);
 }
+
+// Fault injection, for tests of a caller's failure handling: the reference
+// runtime counts failures of its single-kernel decode and turns it off after
+// three (RT:5626-5637), drops to the dequant fallback on any exception of the
+// v1 path (RT:5681-5685) and tells an out-of-memory error by its message
+// (runtime/_helpers.py:301-308).  A spec "name=kind[:count],..." makes the
+// named compute entry points (name without the nsmlp_ prefix, or * for all)
+// fail before they touch the device.  kind: oom (NSMLP_EHIP, the message says
+// "out of memory"), hip (NSMLP_EHIP), inval (NSMLP_EINVAL), nospc
+// (NSMLP_ENOSPC), nodev (NSMLP_ENODEV); count: the number of calls that fail
+// (default: every call).  The first matching rule with calls left applies.
+struct FaultRule {
+  char name[64];
+  int code;
+  bool oom;
+  int left;  // < 0: every call
+};
+constexpr int kMaxFaultRules = 16;
+std::mutex g_fault_mu;
+std::atomic<int> g_fault_armed{0};
+FaultRule g_fault_rules[kMaxFaultRules];
+int g_fault_n = 0;
+
+// Parses spec into rules; returns the rule count, or -1 for a bad spec.
+int fault_parse(const char* spec, FaultRule (&rules)[kMaxFaultRules]) {
+  int n = 0;
+  const char* p = spec;
+  while (*p) {
+    const char* end = strchr(p, ',');
+    const size_t len = end ? (size_t)(end - p) : strlen(p);
+    if (len > 0) {
+      if (n == kMaxFaultRules || len >= 128) return -1;
+      char item[128];
+      memcpy(item, p, len);
+      item[len] = 0;
+      char* eq = strchr(item, '=');
+      if (eq == nullptr || eq == item || (size_t)(eq - item) >= sizeof(rules[n].name)) return -1;
+      *eq = 0;
+      char* kind = eq + 1;
+      char* colon = strchr(kind, ':');
+      int count = -1;
+      if (colon != nullptr) {
+        *colon = 0;
+        char* tail = nullptr;
+        const long c = strtol(colon + 1, &tail, 10);
+        if (tail == colon + 1 || *tail != 0 || c < 1 || c > (1L << 30)) return -1;
+        count = (int)c;
+      }
+      FaultRule& r = rules[n];
+      snprintf(r.name, sizeof(r.name), "%s", item);
+      r.oom = false;
+      r.left = count;
+      if (strcmp(kind, "oom") == 0) {
+        r.code = NSMLP_EHIP;
+        r.oom = true;
+      } else if (strcmp(kind, "hip") == 0) {
+        r.code = NSMLP_EHIP;
+      } else if (strcmp(kind, "inval") == 0) {
+        r.code = NSMLP_EINVAL;
+      } else if (strcmp(kind, "nospc") == 0) {
+        r.code = NSMLP_ENOSPC;
+      } else if (strcmp(kind, "nodev") == 0) {
+        r.code = NSMLP_ENODEV;
+      } else {
+        return -1;
+      }
+      ++n;
+    }
+    if (end == nullptr) break;
+    p = end + 1;
+  }
+  return n;
+}
+
+int fault_set(const char* spec) {
+  FaultRule rules[kMaxFaultRules];
+  const int n = spec ? fault_parse(spec, rules) : 0;
+  if (n < 0) return set_error(NSMLP_EINVAL, "bad fault-injection spec \"%s\" (name=kind[:count],...)", spec);
+  std::lock_guard<std::mutex> lk(g_fault_mu);
+  for (int i = 0; i < n; ++i) g_fault_rules[i] = rules[i];
+  g_fault_n = n;
+  g_fault_armed.store(n > 0 ? 1 : 0, std::memory_order_release);
+  return NSMLP_OK;
+}
+
+// NSMLP_FAULT_INJECT is read when the library loads; a bad spec there makes
+// every compute entry point fail with NSMLP_EINVAL.
+bool g_fault_env_bad = false;
+const int g_fault_env_init = [] {
+  const char* s = getenv("NSMLP_FAULT_INJECT");
+  if (s != nullptr && *s != 0 && fault_set(s) != NSMLP_OK) {
+    g_fault_env_bad = true;
+    g_fault_armed.store(1, std::memory_order_release);
+  }
+  return 0;
+}();
+
+const char* fault_kind_name(int code) {
+  switch (code) {
+    case NSMLP_EINVAL: return "NSMLP_EINVAL";
+    case NSMLP_ENOSPC: return "NSMLP_ENOSPC";
+    case NSMLP_ENODEV: return "NSMLP_ENODEV";
+    default: return "NSMLP_EHIP";
+  }
+}
+
+// Called first by every compute entry point: NSMLP_OK unless a rule fires.
+int fault_point(const char* name) {
+  if (g_fault_armed.load(std::memory_order_acquire) == 0) return NSMLP_OK;
+  std::lock_guard<std::mutex> lk(g_fault_mu);
+  if (g_fault_env_bad) return set_error(NSMLP_EINVAL, "nsmlp_%s: NSMLP_FAULT_INJECT is not a valid spec", name);
+  for (int i = 0; i < g_fault_n; ++i) {
+    FaultRule& r = g_fault_rules[i];
+    if (r.left == 0 || (strcmp(r.name, "*") != 0 && strcmp(r.name, name) != 0)) continue;
+    if (r.left > 0) --r.left;
+    if (r.oom) return set_error(r.code, "nsmlp_%s: HIP error out of memory (injected fault)", name);
+    return set_error(r.code, "nsmlp_%s: injected fault (%s)", name, fault_kind_name(r.code));
+  }
+  return NSMLP_OK;
+}
+
+#define NSMLP_FAULT_POINT(name)             \
+  do {                                      \
+    const int fault_rc_ = fault_point(name); \
+    if (fault_rc_) return fault_rc_;        \
+  } while (0)
 
 // NF4 code values (QLoRA normal-float 4-bit table).
 const float kNF4[16] = {
@@ -411,7 +538,9 @@ extern "C" {
 
 const char* nsmlp_last_error(void) { return g_err; }
 
-int nsmlp_version(void) { return 104; }
+int nsmlp_version(void) { return 105; }
+
+int nsmlp_fault_inject(const char* spec) { return fault_set(spec); }
 
 int nsmlp_device_supported(int device) {
   hipDeviceProp_t prop;
@@ -449,6 +578,7 @@ size_t nsmlp_route_workspace_bytes(int rows, int H, int R, int NB, int k) {
 int nsmlp_route_f16(const void* x, int rows, int H, const void* enc_w, const void* enc_b, int R, int basis_top_k,
                     const void* score_w, const void* score_b, const void* down_block_norm, int NB, int flags, int k,
                     int32_t* sel, void* latent_out, void* scores_out, void* ws, size_t ws_bytes, void* stream) {
+  NSMLP_FAULT_POINT("route_f16");
   int rc = validate_route(rows, H, R, NB, k, flags);
   if (rc) return rc;
   if (!x || !enc_w || !score_w || !sel) return set_error(NSMLP_EINVAL, "x, enc_w, score_w and sel must be non-NULL");
@@ -487,11 +617,13 @@ static int decode_slots(const nsmlp_slot_table* table, const void* x, const void
 
 int nsmlp_decode_slots_f16(const nsmlp_slot_table* table, const void* x, const int32_t* sel, int k, void* out,
                            void* ws, size_t ws_bytes, void* stream) {
+  NSMLP_FAULT_POINT("decode_slots_f16");
   return decode_slots(table, x, nullptr, sel, k, out, ws, ws_bytes, stream);
 }
 
 int nsmlp_decode_slots_add_f16(const nsmlp_slot_table* table, const void* x, const void* residual,
                                const int32_t* sel, int k, void* out, void* ws, size_t ws_bytes, void* stream) {
+  NSMLP_FAULT_POINT("decode_slots_add_f16");
   if (residual == nullptr) return set_error(NSMLP_EINVAL, "residual must be non-NULL");
   return decode_slots(table, x, residual, sel, k, out, ws, ws_bytes, stream);
 }
@@ -555,12 +687,14 @@ static int decode_layer(const nsmlp_router* router, const nsmlp_slot_table* tabl
 
 int nsmlp_decode_layer_f16(const nsmlp_router* router, const nsmlp_slot_table* table, const void* x, int k,
                            int32_t* sel_out, void* out, void* ws, size_t ws_bytes, void* stream) {
+  NSMLP_FAULT_POINT("decode_layer_f16");
   return decode_layer(router, table, x, nullptr, k, sel_out, out, ws, ws_bytes, stream);
 }
 
 int nsmlp_decode_layer_add_f16(const nsmlp_router* router, const nsmlp_slot_table* table, const void* x,
                                const void* residual, int k, int32_t* sel_out, void* out, void* ws, size_t ws_bytes,
                                void* stream) {
+  NSMLP_FAULT_POINT("decode_layer_add_f16");
   if (residual == nullptr) return set_error(NSMLP_EINVAL, "residual must be non-NULL");
   return decode_layer(router, table, x, residual, k, sel_out, out, ws, ws_bytes, stream);
 }
@@ -568,6 +702,7 @@ int nsmlp_decode_layer_add_f16(const nsmlp_router* router, const nsmlp_slot_tabl
 int nsmlp_decode_layer_noalloc_f16(const nsmlp_router* router, const nsmlp_slot_table* table, const void* x,
                                    const void* residual, int k, int32_t* sel_out, void* out, int32_t* status_out,
                                    void* stream) {
+  NSMLP_FAULT_POINT("decode_layer_noalloc_f16");
   if (router == nullptr) return set_error(NSMLP_EINVAL, "router is NULL");
   DecodeArgs a;
   int rc = table_to_args(table, a);
@@ -679,6 +814,7 @@ size_t nsmlp_prefill_workspace_bytes(int H, int NB, int M, int k) {
 
 int nsmlp_prefill_slots_f16(const nsmlp_slot_table* table, const void* x, int M, const int32_t* sel, int k, void* out,
                             void* ws, size_t ws_bytes, void* stream) {
+  NSMLP_FAULT_POINT("prefill_slots_f16");
   PrefillArgs p;
   memset(&p, 0, sizeof(p));
   int rc = table_to_args(table, p.d);
@@ -747,6 +883,7 @@ size_t nsmlp_dense_mlp_workspace_bytes(int H, int I, int M) {
 
 int nsmlp_dense_mlp_slots_f16(const nsmlp_slot_table* table, const void* x, int M, const void* residual, void* out,
                               void* ws, size_t ws_bytes, void* stream) {
+  NSMLP_FAULT_POINT("dense_mlp_slots_f16");
   DenseGuardArgs g;
   memset(&g, 0, sizeof(g));
   int rc = table_to_args(table, g.d);
@@ -800,6 +937,7 @@ int nsmlp_single_kernel_decode_f16(const void* x, const uint8_t* gate_packed, co
                                    const float* up_code, const uint8_t* down_packed, const float* down_absmax,
                                    const float* down_code, void* out, float* out_accum, int H, int block_size,
                                    int qbs, int top_k, void* ws, size_t ws_bytes, void* stream) {
+  NSMLP_FAULT_POINT("single_kernel_decode_f16");
   if (block_size != 32) return set_error(NSMLP_EINVAL, "block_size must be 32 (got %d)", block_size);
   int rc = validate_decode_shape(H, qbs, top_k);
   if (rc) return rc;
@@ -844,6 +982,7 @@ int nsmlp_fused_decode_gathered_f16(const void* x, int H, const int32_t* active_
                                     const uint8_t* down_packed, const float* down_absmax, const float* down_code,
                                     const void* down_bias, int qbs, void* out, void* ws, size_t ws_bytes,
                                     void* stream) {
+  NSMLP_FAULT_POINT("fused_decode_gathered_f16");
   int rc = validate_decode_shape(H, qbs, kk);
   if (rc) return rc;
   if (A <= 0 || A > kMaxSelect) return set_error(NSMLP_EINVAL, "A=%d out of range", A);
@@ -893,6 +1032,7 @@ int nsmlp_output_linear_nf4_f16(const void* x, int rows, int in_dim, const int32
                                 const void* flat_mask, const uint8_t* packed, const float* absmax, const float* code,
                                 int qbs, const void* bias, int block_size, void* out, void* ws, size_t ws_bytes,
                                 void* stream) {
+  NSMLP_FAULT_POINT("output_linear_nf4_f16");
   if (block_size != 32) return set_error(NSMLP_EINVAL, "block_size must be 32 (got %d)", block_size);
   if (rows <= 0 || kk <= 0 || A <= 0) return set_error(NSMLP_EINVAL, "rows, kk and A must be positive");
   if (in_dim <= 0 || in_dim % 256 != 0) return set_error(NSMLP_EINVAL, "input_dim %d must be a multiple of 256", in_dim);
@@ -928,6 +1068,7 @@ int nsmlp_output_linear_nf4_f16(const void* x, int rows, int in_dim, const int32
 int nsmlp_input_linear_nf4_f16(const void* x, int rows, int in_features, const int32_t* active_idx, int kk,
                                const uint8_t* packed, const float* absmax, const float* code, int qbs,
                                int out_features, const void* bias, int block_size, void* out, void* stream) {
+  NSMLP_FAULT_POINT("input_linear_nf4_f16");
   if (block_size <= 0 || block_size % 32 != 0)
     return set_error(NSMLP_EINVAL, "block_size must be a multiple of 32 (got %d)", block_size);
   if (rows <= 0 || kk <= 0 || out_features <= 0) return set_error(NSMLP_EINVAL, "rows, kk, out_features must be > 0");
@@ -959,6 +1100,7 @@ int nsmlp_input_linear_nf4_f16(const void* x, int rows, int in_features, const i
 
 int nsmlp_dense_linear_nf4_f16(const nsmlp_nf4_matrix* w, const void* x, int rows, void* out, float* out_f32,
                                void* stream) {
+  NSMLP_FAULT_POINT("dense_linear_nf4_f16");
   if (!w) return set_error(NSMLP_EINVAL, "NULL matrix");
   const int in = w->in_features, O = w->out_features, qbs = w->qbs;
   if (rows < 0 || O <= 0) return set_error(NSMLP_EINVAL, "rows must be >= 0 and out_features > 0");
@@ -1015,6 +1157,7 @@ int nsmlp_dense_linear_nf4_f16(const nsmlp_nf4_matrix* w, const void* x, int row
 }
 
 int nsmlp_silu_mul_f16(const void* gate, const void* up, void* out, long long n, void* stream) {
+  NSMLP_FAULT_POINT("silu_mul_f16");
   if (n < 0 || (n > 0 && (!gate || !up || !out))) return set_error(NSMLP_EINVAL, "bad silu_mul arguments");
   if (n == 0) return NSMLP_OK;
   launch_silu_mul((const uint16_t*)gate, (const uint16_t*)up, (uint16_t*)out, n, (hipStream_t)stream);
@@ -1131,6 +1274,7 @@ size_t nsmlp_cache_workspace_bytes(int n) {
 
 int nsmlp_cache_promote(const nsmlp_slot_table* table, const nsmlp_cache_state* cache, const int32_t* blocks, int n,
                         int flags, int32_t* slot_out, void* ws, size_t ws_bytes, void* stream) {
+  NSMLP_FAULT_POINT("cache_promote");
   if (table == nullptr || cache == nullptr) return set_error(NSMLP_EINVAL, "table and cache must be non-NULL");
   DecodeArgs a;
   int rc = table_to_args(table, a);
@@ -1199,6 +1343,7 @@ int nsmlp_cache_promote(const nsmlp_slot_table* table, const nsmlp_cache_state* 
 
 int nsmlp_cache_record_f32(float* counts, int NB, const int32_t* blocks, int rows, int k, const float* row_weights,
                            void* stream) {
+  NSMLP_FAULT_POINT("cache_record_f32");
   if (counts == nullptr || NB <= 0) return set_error(NSMLP_EINVAL, "counts must be non-NULL and NB >= 1");
   if (rows < 0 || k < 0 || (long long)rows * k >= (1LL << 31))
     return set_error(NSMLP_EINVAL, "rows %d x k %d out of range", rows, k);
