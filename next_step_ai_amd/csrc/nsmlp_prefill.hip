@@ -316,35 +316,49 @@ __global__ void __launch_bounds__(kPfThreads, 4) k_pf_gu(PrefillArgs p) {  // 4 
       // kGuNS - 2 chunks may not), then every thread's
       asm volatile("s_waitcnt vmcnt(5)" ::: "memory");  // (kGuNS - 2) chunks x 5 loads
       lds_barrier();  // also: every wave is done with chunk c - 1, whose stage the next issue refills
+      // every LDS read of the chunk that depends on no other goes out first
+      // (the token tiles' A fragments, the two weight words, the absmax
+      // entries), the next chunk's loads behind them; then the code-book
+      // reads that need them.  Two LDS round trips per chunk before the
+      // MFMAs (the A fragments read tile by tile after the decode made six).
+      const int r0 = proj * 32 + j, r1 = r0 + 16;
+      const int a0 = r0 * 4 + s, a1 = r1 * 4 + s;  // piece s: the step's 32 columns
+      half8_t af[kGuTiles];
+#pragma unroll
+      for (int tt = 0; tt < kGuTiles; ++tt) {
+        if (tt < ntiles) {
+          const int row = tt * 16 + j;
+          af[tt] = as_h8(*reinterpret_cast<const uint4*>(
+              &L.x[st][row * 256 + ((uint32_t)(4 * s + g) ^ (uint32_t)(row & 15)) * 16]));
+        }
+      }
+      const uint32_t w0 = *reinterpret_cast<const uint32_t*>(
+          &L.w[st][r0 * 64 + ((uint32_t)(4 * s + g) ^ ((((uint32_t)(r0 & 31) >> 2) & 3u) << 2)) * 4]);
+      const uint32_t w1 = *reinterpret_cast<const uint32_t*>(
+          &L.w[st][r1 * 64 + ((uint32_t)(4 * s + g) ^ ((((uint32_t)(r1 & 31) >> 2) & 3u) << 2)) * 4]);
+      const uint32_t q0 = L.qa[st][a0], q1 = L.qa[st][a1];
+      const float x0 = DQ ? L.a2[st][a0] : 0.0f, x1 = DQ ? L.a2[st][a1] : 0.0f;
+      __builtin_amdgcn_sched_barrier(0);
       issue(c + kGuNS - 1, std::integral_constant<int, (st + kGuNS - 1) % kGuNS>());
       half8_t bf[2];
       {
-        const int r0 = proj * 32 + j, r1 = r0 + 16;
-        const int a0 = r0 * 4 + s, a1 = r1 * 4 + s;  // piece s: the step's 32 columns
-        const uint32_t w0 = *reinterpret_cast<const uint32_t*>(
-            &L.w[st][r0 * 64 + ((uint32_t)(4 * s + g) ^ ((((uint32_t)(r0 & 31) >> 2) & 3u) << 2)) * 4]);
-        const uint32_t w1 = *reinterpret_cast<const uint32_t*>(
-            &L.w[st][r1 * 64 + ((uint32_t)(4 * s + g) ^ ((((uint32_t)(r1 & 31) >> 2) & 3u) << 2)) * 4]);
         float am0, am1;
         if constexpr (DQ) {
           const float* c2 = L.c2[proj];
           const float off = proj ? d.up.offset : d.gate.offset;
-          am0 = dq_absmax(c2[L.qa[st][a0] & 0xFFu], L.a2[st][a0], off);
-          am1 = dq_absmax(c2[L.qa[st][a1] & 0xFFu], L.a2[st][a1], off);
+          am0 = dq_absmax(c2[q0 & 0xFFu], x0, off);
+          am1 = dq_absmax(c2[q1 & 0xFFu], x1, off);
         } else {
-          am0 = __uint_as_float(L.qa[st][a0]);
-          am1 = __uint_as_float(L.qa[st][a1]);
+          am0 = __uint_as_float(q0);
+          am1 = __uint_as_float(q1);
         }
         deq8x2<kGuCopies>(w0, am0, w1, am1, L.cpair + (lane & (kGuCopies - 1)), bf[0], bf[1]);
       }
 #pragma unroll
       for (int tt = 0; tt < kGuTiles; ++tt) {
         if (tt < ntiles) {
-          const int row = tt * 16 + j;
-          const half8_t af = as_h8(*reinterpret_cast<const uint4*>(
-              &L.x[st][row * 256 + ((uint32_t)(4 * s + g) ^ (uint32_t)(row & 15)) * 16]));
-          acc[tt][0] = mfma16(af, bf[0], acc[tt][0]);
-          acc[tt][1] = mfma16(af, bf[1], acc[tt][1]);
+          acc[tt][0] = mfma16(af[tt], bf[0], acc[tt][0]);
+          acc[tt][1] = mfma16(af[tt], bf[1], acc[tt][1]);
         }
       }
     };
