@@ -9,21 +9,21 @@
 //   u  = fp16(x W_up^T),    act = fp16(s * u)  (act = gate * up)
 //   y  = fp16(act W_down^T + bias)             (F.linear(act, Wd, bias))
 //
-//   k_dg_gu    one workgroup per 128 intermediate rows and 256 tokens: the
-//              tokens' rows and the 128 gate + 128 up weight rows go through
-//              double-buffered LDS in 64-column chunks (the weights decoded
-//              to fp16(code * absmax) as they are staged); wave w computes
-//              64 tokens (w % 4) x 64 rows (w / 4) of both projections, so
-//              the act epilogue pairs g and u in registers;
+//   k_dg_gu2   one workgroup of 4 waves per 4 blocks and 256 tokens: wave w
+//              owns block 4 bq + w, its 32 gate and 32 up rows x all the
+//              tile's tokens in 256 fp32 accumulators; the weights are
+//              decoded to fp16(code * absmax) in registers (each fed to 16
+//              MFMAs), the token rows staged in LDS for the 4 waves; g and u
+//              of a (token, row) meet in one lane, so act is formed there;
 //   k_dg_down  one workgroup per 256 output rows, 256 tokens and one of S
-//              ranges of the intermediate blocks: the same staged GEMM over
-//              act and the down columns (two blocks per chunk); fp32
-//              partial sums per range;
+//              ranges of the intermediate blocks: the same register-decode
+//              GEMM over act and the down columns (two blocks per step);
+//              fp32 partial sums per range;
 //   k_dg_fin   y = fp16(sum of the S partials in range order + bias).
 //
 // The tokens past the last whole 256-token tile (all of a prompt of fewer than
 // 256) go in a second launch with the smallest tile of 64, 128 or 192 tokens
-// that holds them (wave w then computes 16, 32 or 48 tokens x 64 rows; the
+// that holds them (a wave then computes 64, 128 or 192 tokens; the
 // per-element K order is the same, so every token's result equals the
 // 256-token tiles' bit for bit).
 //
@@ -37,278 +37,8 @@ namespace nsmlp {
 
 namespace {
 
-constexpr int kDgThreads = 512;
-constexpr int kDgTok = 256;                 // tokens per tile (64, 128 or 192 for shorter prompts)
-constexpr int kDgK = 64;                    // columns per chunk
-constexpr int kDgRow = 72;                  // halfs per staged row (64 + 8: conflict-free fragment reads)
-constexpr int kDgStage = 256 * kDgRow;      // halfs per staged operand (256 rows)
-constexpr int kDgPairCopies = 4;  // code-pair table copies (the gate/up kernel keeps 2 of each of its 2 tables)
-constexpr size_t kDgLds =
-    (size_t)4 * kDgStage * 2 + kDgPairCopies * 256 * sizeof(float2) + 2 * 256 * sizeof(float);
-
-// fp32 code pairs per packed byte: (code[e >> 4], code[e & 15]) = (even, odd
-// element), `copies` interleaved copies of each entry (entry e, copy c at
-// e * copies + c): lanes reading their own copy spread random lookups over
-// more banks.
-__device__ __forceinline__ void dg_pairs(float2* cp, const float* code, int i, int copies) {
-  const int e = i / copies;
-  cp[i] = make_float2(code[e >> 4], code[e & 15]);
-}
-
 typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
 typedef float float2_t __attribute__((ext_vector_type(2)));
-
-// 32 NF4 codes (16 bytes, even element in the high nibble) -> 32 fp16(code * am)
-// (fp32 products rounded to nearest, two per v_cvt_pk_f16_f32) written as 64
-// bytes to dst (16-byte aligned).
-template <int COPIES>
-__device__ __forceinline__ void dg_decode32(_Float16* dst, uint4 w, float am, const float2* cp) {
-  const uint32_t words[4] = {w.x, w.y, w.z, w.w};
-#pragma unroll
-  for (int q = 0; q < 4; ++q) {
-    uint32_t o[4];
-#pragma unroll
-    for (int b = 0; b < 4; ++b) {
-      const float2 pr = cp[((words[q] >> (8 * b)) & 0xFFu) * COPIES];
-      const float2_t v = {pr.x * am, pr.y * am};
-      o[b] = __builtin_bit_cast(uint32_t, __builtin_convertvector(v, half2_t));
-    }
-    *reinterpret_cast<uint4*>(dst + 8 * q) = make_uint4(o[0], o[1], o[2], o[3]);
-  }
-}
-
-// One staged weight unit: 32 NF4 codes of one row and its absmax.
-struct DgW {
-  uint4 w;
-  float am;     // fp32 absmax, or the absmax2 (double-quantised)
-  uint32_t qa;  // u8 absmax code (double-quantised)
-};
-
-// The wave's 16 MT x 128 tile for one staged chunk (MT = 4: 256-token tiles,
-// MT = 1: 64-token tiles): A rows (tokens) 16 MT mq + 16 mi + lane % 16, B
-// rows brow(ni) + lane % 16, K halves 32 ks + 8 (lane / 16).
-template <int MT, typename BRow>
-__device__ __forceinline__ void dg_mma(float4_t (&acc)[MT][8], const _Float16* As, const _Float16* Bs, int mq,
-                                       int lane, BRow brow) {
-  const int j = lane & 15, g = lane >> 4;
-#pragma unroll
-  for (int ks = 0; ks < 2; ++ks) {
-    half8_t a[MT];
-#pragma unroll
-    for (int mi = 0; mi < MT; ++mi)
-      a[mi] = as_h8(*reinterpret_cast<const uint4*>(As + (16 * MT * mq + 16 * mi + j) * kDgRow + 32 * ks + 8 * g));
-#pragma unroll
-    for (int ni = 0; ni < 8; ++ni) {
-      const half8_t b = as_h8(*reinterpret_cast<const uint4*>(Bs + (brow(ni) + j) * kDgRow + 32 * ks + 8 * g));
-#pragma unroll
-      for (int mi = 0; mi < MT; ++mi) acc[mi][ni] = mfma16(a[mi], b, acc[mi][ni]);
-    }
-    // keep the next step's fragment reads after this step's MFMAs (register pressure)
-    __builtin_amdgcn_sched_barrier(0);
-  }
-}
-
-// Token rows of one chunk (64 MT tokens): piece p = tid + 512 h (h < MT) is
-// token p / 8, columns 8 (p % 8) .. + 7 of the chunk.
-template <int MT>
-__device__ __forceinline__ void dg_load_rows(uint4 (&x)[MT], rsrc_t r, int tid, int t0, int M, uint32_t row_len,
-                                             uint32_t k0, bool live) {
-#pragma unroll
-  for (int h = 0; h < MT; ++h) {
-    const int p = tid + h * kDgThreads, t = t0 + (p >> 3);
-    x[h] = buf_ld16c(r, (live && t < M) ? ((uint32_t)t * row_len + k0 + (uint32_t)(p & 7) * 8u) * 2u : kOffNone, 0);
-  }
-}
-
-template <int MT>
-__device__ __forceinline__ void dg_store_rows(_Float16* As, const uint4 (&x)[MT], int tid) {
-#pragma unroll
-  for (int h = 0; h < MT; ++h) {
-    const int p = tid + h * kDgThreads;
-    *reinterpret_cast<uint4*>(As + (p >> 3) * kDgRow + (p & 7) * 8) = x[h];
-  }
-}
-
-// Staging schedule shared by both GEMMs (chunks c_lo .. c_hi - 1, buffer c & 1):
-// chunk c computes from LDS while chunk c + 1 is written to the other buffer
-// from registers and chunk c + 2 is loaded into registers, so each global
-// load has a whole chunk of MFMAs to arrive; unrolled by two so the register
-// stages are named.
-template <int MT, typename LoadX, typename LoadW, typename StoreX, typename StoreW, typename Mma>
-__device__ __forceinline__ void dg_pipeline(int c_lo, int c_hi, LoadX load_x, LoadW load_w, StoreX store_x,
-                                            StoreW store_w, Mma mma) {
-  uint4 X0[MT], X1[MT];
-  DgW W0, W1;
-  load_x(X0, c_lo);
-  load_w(W0, c_lo);
-  load_x(X1, c_lo + 1);
-  load_w(W1, c_lo + 1);
-  __syncthreads();  // code tables
-  store_x(0, X0);
-  store_w(0, W0);
-  load_x(X0, c_lo + 2);
-  load_w(W0, c_lo + 2);
-  __syncthreads();
-  for (int c = c_lo; c < c_hi; c += 2) {
-    mma(0);
-    store_x(1, X1);
-    store_w(1, W1);
-    load_x(X1, c + 3);
-    load_w(W1, c + 3);
-    __syncthreads();
-    if (c + 1 < c_hi) mma(1);  // uniform
-    store_x(0, X0);
-    store_w(0, W0);
-    load_x(X0, c + 4);
-    load_w(W0, c + 4);
-    __syncthreads();
-  }
-}
-
-// Weight staging of the gate/up kernel in pairs of chunks: a row's 128
-// columns of a pair are 64 contiguous bytes of packed NF4, read by 4
-// consecutive lanes (a load that reads 32 bytes of each row per chunk runs at
-// a lower rate).  Load j of lane l takes staged row 16 w + 128 j + l / 4 and
-// 16-byte segment (l % 4) ^ 2 j of that row's 64 bytes, i.e. chunk
-// ((l % 4) / 2) ^ j of the pair, columns 32 (l % 2) .. + 31: every lane
-// decodes one piece per chunk.
-struct DgPair {
-  uint4 w[2];
-  float am[2];     // fp32 absmax, or the absmax2 (double-quantised)
-  uint32_t qa[2];  // u8 absmax codes (double-quantised)
-};
-
-template <bool DQ, int MT>
-__global__ void __launch_bounds__(kDgThreads, 2) k_dg_gu(DenseGuardArgs g) {
-  extern __shared__ __attribute__((aligned(16))) uint8_t dg_lds[];
-  _Float16* As = reinterpret_cast<_Float16*>(dg_lds);  // [2][256][72] token rows
-  _Float16* Bs = As + 2 * kDgStage;                      // [2][256][72] gate rows 0-127, up rows 128-255
-  float2* cp = reinterpret_cast<float2*>(Bs + 2 * kDgStage);  // [2][256 x 2] gate, up code pairs
-  float* c2s = reinterpret_cast<float*>(cp + 1024);           // [2][256] second-level code books
-  const DecodeArgs& d = g.d;
-  const int tid = threadIdx.x, lane = tid & (kWave - 1);
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int nt = blockIdx.x, t0 = g.t_base + (int)blockIdx.y * 64 * MT;
-  const int H = d.H, I = d.NB * 32, M = g.M;
-  dg_pairs(cp, d.code, tid, 2);
-  dg_pairs(cp + 512, d.code_up, tid, 2);
-  if constexpr (DQ) c2s[tid] = (tid < 256 ? d.gate.code2 : d.up.code2)[tid & 255];
-  // load j of this wave: staged rows 16 wave + 128 j .. + 15, all in block
-  // 4 nt + wave / 2 of the gate (j = 0) or up (j = 1) projection, so each
-  // load's block and buffer descriptors are uniform over the wave
-  const uint32_t rs = (uint32_t)d.gate.row_stride, A = (uint32_t)d.gate.abs_row_stride;
-  const uint32_t wrow = (uint32_t)((16 * wave + (lane >> 2)) & 31);  // row inside the block
-  const int u = (lane & 3) >> 1, half = lane & 1;
-  const int blk = 4 * nt + (wave >> 1);
-  const BlockRef br = resolve_id(d, blk);
-  if (!br.ok && lane == 0) atomicOr(d.status, 1);
-  rsrc_t rw[2], ra[2], r2[2];
-#pragma unroll
-  for (int jj = 0; jj < 2; ++jj) {
-    const ProjView& pv = jj ? d.up : d.gate;
-    const ProjView& hv = jj ? d.host_up : d.host_gate;
-    rw[jj] = make_rsrc((br.dev ? pv.packed : hv.packed) + br.q * pv.blk_stride, br.ok ? (int)(32 * rs) : 0);
-    if constexpr (DQ) {
-      ra[jj] = make_rsrc((br.dev ? pv.qabsmax : hv.qabsmax) + br.q * pv.abs_blk_stride, br.ok ? (int)(32 * A) : 0);
-      r2[jj] = make_rsrc(pv.absmax2,
-                         br.ok ? (int)((((long long)I * A + (1 << d.dq_shift) - 1) >> d.dq_shift) * 4) : 0);
-    } else {
-      ra[jj] = make_rsrc((br.dev ? pv.absmax : hv.absmax) + br.q * pv.abs_blk_stride, br.ok ? (int)(32 * A * 4) : 0);
-      r2[jj] = ra[jj];
-    }
-  }
-  const rsrc_t rx = make_rsrc(g.x, (int)((long long)M * H * 2));
-  const int nch = H / kDgK, np = (nch + 1) / 2;
-  auto load_x = [&](uint4 (&X)[MT], int c) {
-    const bool live = c < nch;
-    dg_load_rows(X, rx, tid, t0, M, (uint32_t)H, (uint32_t)(live ? c : 0) * kDgK, live);
-  };
-  auto load_p = [&](DgPair& P, int pr) {
-    const bool live = pr < np;
-#pragma unroll
-    for (int jj = 0; jj < 2; ++jj) {
-      const uint32_t seg = (uint32_t)((lane & 3) ^ (2 * jj));  // chunk seg / 2, half seg % 2
-      const uint32_t col = (uint32_t)pr * 128u + seg * 32u;
-      const bool ok = live && (int)col < H;
-      const uint32_t ce = col >> d.qbs_shift;
-      P.w[jj] = buf_ld16(rw[jj], ok ? wrow * rs + (col >> 1) : kOffNone, 0);
-      if constexpr (DQ) {
-        P.qa[jj] = buf_ldu8(ra[jj], ok ? ((wrow >> 1) * A + ce) * 2u + (wrow & 1u) : kOffNone, 0);
-        const uint32_t f = (32u * (uint32_t)blk + wrow) * A + ce;
-        P.am[jj] = buf_ldfc(r2[jj], ok ? (f >> d.dq_shift) * 4u : kOffNone, 0);
-      } else {
-        P.qa[jj] = 0;
-        P.am[jj] = buf_ldf(ra[jj], ok ? (wrow * A + ce) * 4u : kOffNone, 0);
-      }
-    }
-  };
-  // chunk k of a pair into buffer bi: this lane's piece jj = k ^ u (gate for
-  // jj = 0, up for jj = 1)
-  auto decode = [&](int bi, const DgPair& P, int k) {
-    const bool up = (k ^ u) != 0;
-    const uint4 w = up ? P.w[1] : P.w[0];
-    float am = up ? P.am[1] : P.am[0];
-    if constexpr (DQ) am = dq_absmax(c2s[(up ? 256 : 0) + (up ? P.qa[1] : P.qa[0])], am, up ? d.up.offset : d.gate.offset);
-    const int row = 16 * wave + (up ? 128 : 0) + (lane >> 2);
-    dg_decode32<2>(Bs + bi * kDgStage + row * kDgRow + 32 * half, w, am, cp + (up ? 512 : 0) + (lane & 1));
-  };
-  auto store_x = [&](int bi, const uint4 (&X)[MT]) { dg_store_rows<MT>(As + bi * kDgStage, X, tid); };
-  const int mq = wave & 3, nh = wave >> 2;
-  auto brow = [nh](int ni) { return (ni < 4 ? 0 : 128) + 64 * nh + 16 * (ni & 3); };
-  float4_t acc[MT][8];
-#pragma unroll
-  for (int mi = 0; mi < MT; ++mi)
-#pragma unroll
-    for (int ni = 0; ni < 8; ++ni) acc[mi][ni] = float4_t{0.0f, 0.0f, 0.0f, 0.0f};
-  uint4 X[2][MT];
-  DgPair P[2];
-  load_p(P[0], 0);
-  load_p(P[1], 1);
-  load_x(X[0], 0);
-  load_x(X[1], 1);
-  __syncthreads();  // code tables
-  store_x(0, X[0]);
-  decode(0, P[0], 0);
-  load_x(X[0], 2);
-  __syncthreads();
-  // chunk c computes from buffer c & 1 while chunk c + 1 is staged into the
-  // other buffer (token rows from registers, weights decoded from the pair
-  // registers) and chunk c + 3's token rows are loaded; a pair's registers
-  // are reloaded with the pair after next once its second chunk is decoded.
-  // Unrolled by 4 chunks so every register index is static.
-  for (int c = 0; c < nch; c += 4) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int cc = c + i;
-      if (cc < nch) dg_mma(acc, As + (i & 1) * kDgStage, Bs + (i & 1) * kDgStage, mq, lane, brow);  // uniform
-      const int nb = (i + 1) & 1;
-      store_x(nb, X[nb]);
-      decode(nb, P[((i + 1) >> 1) & 1], (i + 1) & 1);
-      load_x(X[nb], cc + 3);
-      if (((i + 1) & 1) == 1) load_p(P[((i + 1) >> 1) & 1], ((cc + 1) >> 1) + 2);
-      __syncthreads();
-    }
-  }
-  mfma_drain();
-  // act = fp16(fp16(silu(fp16(g))) * fp16(u)) for (token, row)
-  const int j = lane & 15, gq = lane >> 4;
-#pragma unroll
-  for (int mi = 0; mi < MT; ++mi) {
-#pragma unroll
-    for (int rr = 0; rr < 4; ++rr) {
-      const int t = t0 + 16 * MT * mq + 16 * mi + 4 * gq + rr;
-      if (t < M) {
-#pragma unroll
-        for (int ni = 0; ni < 4; ++ni) {
-          const float g16 = h2f(f2h(acc[mi][ni][rr]));
-          const float s16 = h2f(f2h(g16 / (1.0f + expf(-g16))));
-          const float u16 = h2f(f2h(acc[mi][4 + ni][rr]));
-          g.act[(long long)t * I + 128 * nt + 64 * nh + 16 * ni + j] = f2h(s16 * u16);
-        }
-      }
-    }
-  }
-}
 
 // ------------------------------------------------------------- down GEMM --
 // part[s][t][o] = sum over the blocks of range s of act[t][i] * Wd[o][i],
@@ -662,6 +392,253 @@ __global__ void __launch_bounds__(kDnThreads, 1) k_dg_down(DenseGuardArgs g) {
   }
 }
 
+// ---------------------------------------------------------- gate/up GEMM --
+// g[t][i], u[t][i] = sum over k of x[t][k] * W[i][k] for the gate and up rows,
+// W = fp16(code * absmax), then act[t][i] = fp16(fp16(silu(fp16(g))) *
+// fp16(u)).  The down kernel's scheme with the roles of the operands kept: a
+// workgroup of 4 waves takes 4 consecutive blocks and 16 MT tokens, wave w
+// owns block 4 bq + w, i.e. its 32 gate rows (groups rg = 0, 1: rows
+// 16 rg + n) and its 32 up rows (rg = 2, 3) x all the tile's tokens in
+// 16 MT fp32 accumulators per group (AGPRs); each decoded weight feeds MT
+// MFMAs and every weight is read from HBM once.  The 4 waves share the
+// tile's token rows.  A step covers 64 columns:
+//   - lane (n = l % 16, q = l / 16) loads, for each row group, 8 packed
+//     bytes of its row: bytes 8 q .. + 7 of the step's 32.  Dword j is its B
+//     fragment for MFMA step j, so K slots 8 q .. 8 q + 7 of step j are
+//     columns 16 q + 8 j .. + 7 of the step (the A fragments use the same
+//     order); the absmax of those 16 columns is the entry (64 c + 16 q) / qbs;
+//   - the tokens' rows of the 64 columns (128 bytes each) go into an LDS
+//     stage by loads straight into LDS (row r's 16-byte piece p in slot
+//     p ^ ((r / 2) % 8)); the A fragment of token group mi and MFMA step j is
+//     piece 2 q + j of token row 16 mi + n.
+// Gate and up accumulators of the same (token, row) sit in the same lane, so
+// act is formed in registers.  The code-pair table, the step schedule (4
+// units of 2 MT MFMAs) and the register pinning are the down kernel's.
+constexpr uint32_t kGuC2 = kDnTab + 2u * kDnStage;  // second-level code books [2][256]
+constexpr uint32_t kGuLds = kGuC2 + 2u * 256u * 4u;
+
+template <bool DQ, int MT>
+__global__ void __launch_bounds__(kDnThreads, 1) k_dg_gu2(DenseGuardArgs g) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t gu_lds[];  // no static LDS: gu_lds is LDS address 0
+  const DecodeArgs& d = g.d;
+  const int tid = threadIdx.x, lane = tid & (kWave - 1);
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int H = d.H, I = d.NB * 32, M = g.M;
+  const int t0 = g.t_base + (int)blockIdx.y * 16 * MT;
+  const int blk = 4 * (int)blockIdx.x + wave;
+  const int nst = H / 64;
+  // the K loop starts at a step that depends on the workgroup (16 starting
+  // points), so that the many rows that share a cache set are not read at
+  // the same columns at the same time
+  const int rot = (int)(((long long)((blockIdx.x >> 3) & 15) * nst) >> 4);
+  float* c2s = reinterpret_cast<float*>(gu_lds + kGuC2);
+
+  // code-pair table: thread e writes the 32 copies of entry e (code[e >> 4],
+  // code[e & 15]), 256 contiguous bytes
+  {
+    const float hi = d.code[tid >> 4], lo = d.code[tid & 15];
+    uint4* dst = reinterpret_cast<uint4*>(gu_lds + tid * 256);
+    const uint4 v = make_uint4(__float_as_uint(hi), __float_as_uint(lo), __float_as_uint(hi), __float_as_uint(lo));
+#pragma unroll
+    for (int i = 0; i < 16; ++i) dst[i] = v;
+  }
+  if constexpr (DQ) {
+    c2s[tid] = d.gate.code2[tid];
+    c2s[256 + tid] = d.up.code2[tid];
+  }
+  const BlockRef br = resolve_id(d, blk);
+  if (!br.ok && lane == 0) atomicOr(d.status, 1);
+  __syncthreads();
+
+  const int n = lane & 15, q = lane >> 4;
+  const uint32_t rs = (uint32_t)d.gate.row_stride, A = (uint32_t)d.gate.abs_row_stride;
+  rsrc_t rw[2], ra[2], r2[2];
+#pragma unroll
+  for (int jj = 0; jj < 2; ++jj) {
+    const ProjView& pv = jj ? d.up : d.gate;
+    const ProjView& hv = jj ? d.host_up : d.host_gate;
+    rw[jj] = make_rsrc((br.dev ? pv.packed : hv.packed) + br.q * pv.blk_stride, br.ok ? (int)(32 * rs) : 0);
+    if constexpr (DQ) {
+      ra[jj] = make_rsrc((br.dev ? pv.qabsmax : hv.qabsmax) + br.q * pv.abs_blk_stride, br.ok ? (int)(32 * A) : 0);
+      r2[jj] = make_rsrc(pv.absmax2, br.ok ? (int)((((long long)I * A + (1 << d.dq_shift) - 1) >> d.dq_shift) * 4) : 0);
+    } else {
+      ra[jj] = make_rsrc((br.dev ? pv.absmax : hv.absmax) + br.q * pv.abs_blk_stride, br.ok ? (int)(32 * A * 4) : 0);
+      r2[jj] = ra[jj];
+    }
+  }
+  const rsrc_t rx = make_rsrc(g.x, (int)((long long)M * H * 2));
+  // per-lane parts of the weight and absmax offsets (row 16 (rg % 2) + n);
+  // the row group's part is uniform and goes into the scalar offset
+  const uint32_t wv = (uint32_t)n * rs + 8u * (uint32_t)q;
+  const uint32_t qv = DQ ? ((uint32_t)(n >> 1) * A) * 2u + (uint32_t)(n & 1) : (uint32_t)n * A * 4u;
+  const uint32_t fv = (32u * (uint32_t)blk + (uint32_t)n) * A;  // absmax index of row n, entry 0
+  auto issue_w = [&](DnW& W, int c) {
+    const bool live = c < nst;
+    c = c + rot < nst ? c + rot : c + rot - nst;
+    const uint32_t ce = ((uint32_t)(64 * c) + 16u * (uint32_t)q) >> d.qbs_shift;  // the lane's absmax entry
+    const uint32_t wo = live ? wv : kOffNone, qo = live ? qv + (DQ ? 2u : 4u) * ce : kOffNone;
+    W.ok = br.ok;
+#pragma unroll
+    for (int rg = 0; rg < 4; ++rg) {
+      const int jj = rg >> 1;
+      const uint32_t half = (uint32_t)(rg & 1);
+      // temporal loads: a row's 128-byte line serves 4 steps (an
+      // nontemporal load fetched it again for each)
+      W.w[rg] = buf_ld8c(rw[jj], wo, 16u * half * rs + 32u * (uint32_t)c);
+      if constexpr (DQ) {
+        W.qa[rg] = buf_ldu8c(ra[jj], qo, 16u * half * A);
+        const uint32_t fo = ((fv + 16u * half * A + ce) >> d.dq_shift) * 4u;
+        W.a[rg] = buf_ldfc(r2[jj], live ? fo : kOffNone, 0);
+      } else {
+        W.a[rg] = buf_ldfc(ra[jj], qo, 16u * half * A * 4u);
+      }
+    }
+  };
+  // token rows of step c into stage c & 1: load i of wave w fills rows
+  // 32 i + 8 w .. + 7 (lane l: row + l / 8, slot l % 8); row i's offset is
+  // load 0's plus 32 i rows (a scalar offset)
+  const int arow = 8 * wave + (lane >> 3);
+  const uint32_t apiece = (uint32_t)((lane & 7) ^ ((arow >> 1) & 7));
+  const uint32_t xrow = ((uint32_t)(t0 + arow) * (uint32_t)H + 8u * apiece) * 2u;
+  auto issue_x = [&](int c) {
+    const int tlim = c < nst ? M - t0 - arow : 0;  // rows 32 i with 32 i < tlim are tokens of this call
+    const int cp = c + rot < nst ? c + rot : c + rot - nst;
+    const uint32_t xo = xrow + 128u * (uint32_t)cp;
+    const uint32_t sb = kDnTab + (uint32_t)(c & 1) * kDnStage;
+#pragma unroll
+    for (int i = 0; i < MT / 2; ++i) {
+      const uint32_t xi = 32 * i < tlim ? xo : kOffNone;
+      ld_lds16s(rx, gu_lds + sb + (32 * i + 8 * wave) * 128, xi, 64u * (uint32_t)i * (uint32_t)H);
+    }
+  };
+
+  float4_t acc[MT][4];
+#pragma unroll
+  for (int mi = 0; mi < MT; ++mi)
+#pragma unroll
+    for (int rg = 0; rg < 4; ++rg) {
+      acc[mi][rg] = float4_t{0.0f, 0.0f, 0.0f, 0.0f};
+      asm volatile("" : "+a"(acc[mi][rg]));
+    }
+  uint32_t ad[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) ad[i] = (uint32_t)(lane & (kDnCopies - 1)) * 8u;
+  // A fragment (token group mi, MFMA step j) of step c: token row 16 mi + n,
+  // piece 2 q + j, in slot piece ^ ((row / 2) % 8)
+  auto read_a = [&](half8_t (&a)[MT / 2], int c, int j, int h) {
+    const uint32_t piece = (uint32_t)(2 * q + j);
+    const uint32_t base = kDnTab + (uint32_t)(c & 1) * kDnStage + (uint32_t)n * 128u +
+                          ((piece ^ (uint32_t)((n >> 1) & 7)) << 4) + (uint32_t)h * 1024u * MT;
+#pragma unroll
+    for (int mi = 0; mi < MT / 2; ++mi) a[mi] = lds_ld_h8(base + (uint32_t)mi * 2048u);
+  };
+  auto am_of = [&](const DnW& W, float (&am)[4]) {
+#pragma unroll
+    for (int rg = 0; rg < 4; ++rg) {
+      float v = W.a[rg];
+      if constexpr (DQ) v = dq_absmax(c2s[(rg >> 1) * 256 + W.qa[rg]], W.a[rg], rg >> 1 ? d.up.offset : d.gate.offset);
+      am[rg] = W.ok ? v : 0.0f;
+    }
+  };
+  auto lookup4 = [&](DnPairs (&pr)[4], const DnW& W, int j) {
+#pragma unroll
+    for (int rg = 0; rg < 4; ++rg) pr[rg] = dn_lookup4(j == 0 ? W.w[rg].x : W.w[rg].y, ad);
+  };
+  auto finish4 = [&](half8_t (&b)[4], const DnPairs (&pr)[4], const float (&am)[4]) {
+#pragma unroll
+    for (int rg = 0; rg < 4; ++rg) b[rg] = dn_finish8(pr[rg], am[rg]);
+  };
+  auto mfma_unit = [&](const half8_t (&a)[MT / 2], const half8_t (&b)[4], int h) {
+#pragma unroll
+    for (int rg = 0; rg < 4; ++rg)
+#pragma unroll
+      for (int mi = 0; mi < MT / 2; ++mi) acc[MT / 2 * h + mi][rg] = mfma16(a[mi], b[rg], acc[MT / 2 * h + mi][rg]);
+#pragma unroll
+    for (int i = 0; i < 2 * MT; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  auto step_sync = [] {
+    __builtin_amdgcn_s_waitcnt(0);  // vmcnt(0) expcnt(0) lgkmcnt(0)
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+  };
+
+  // the down kernel's step schedule: 4 units (MFMA step j, token half h) of
+  // 2 MT MFMAs, three weight register sets (decoded, arrived, in flight)
+  // moved down one set at the end of a step, step c + 2's weights issued in
+  // unit (0, 1) and its token rows after the barrier of the last unit
+  DnW W0, W1, W2;
+  half8_t ax[MT / 2], ay[MT / 2], b0[4], b1[4];
+  DnPairs pr[4];
+  float am_c[4], am_n[4];
+  issue_w(W0, 0);
+  issue_x(0);
+  issue_w(W1, 1);
+  issue_x(1);
+  __builtin_amdgcn_s_waitcnt(0);
+  __builtin_amdgcn_s_barrier();  // step 0's token rows are in LDS (and step 1's)
+  asm volatile("" ::: "memory");
+  am_of(W0, am_c);
+  read_a(ax, 0, 0, 0);
+  lookup4(pr, W0, 0);
+  finish4(b0, pr, am_c);
+  __builtin_amdgcn_sched_barrier(0);
+
+  auto step = [&](int c, const DnW& Wc, const DnW& Wn, DnW& Wf) {
+    read_a(ay, c, 0, 1);
+    lookup4(pr, Wc, 1);
+    mfma_unit(ax, b0, 0);
+    issue_w(Wf, c + 2);
+    read_a(ax, c, 1, 0);
+    finish4(b1, pr, am_c);
+    mfma_unit(ay, b0, 1);
+    read_a(ay, c, 1, 1);
+    am_of(Wn, am_n);
+    lookup4(pr, Wn, 0);
+    mfma_unit(ax, b1, 0);
+    step_sync();
+    issue_x(c + 2);
+    read_a(ax, c + 1, 0, 0);
+    finish4(b0, pr, am_n);
+    mfma_unit(ay, b1, 1);
+#pragma unroll
+    for (int rg = 0; rg < 4; ++rg) am_c[rg] = am_n[rg];
+#pragma unroll
+    for (int mi = 0; mi < MT; ++mi)
+#pragma unroll
+      for (int rg = 0; rg < 4; ++rg) asm volatile("" : "+a"(acc[mi][rg]));
+  };
+  for (int c = 0; c < nst; ++c) {
+    step(c, W0, W1, W2);
+    W0 = W1;
+    W1 = W2;
+  }
+  __builtin_amdgcn_s_waitcnt(0);
+  mfma_drain();
+  // act = fp16(fp16(silu(fp16(g))) * fp16(u)) for (token, row): C lane (n, q)
+  // holds row n of its group for tokens 16 mi + 4 q + r
+#pragma unroll
+  for (int mi = 0; mi < MT; ++mi) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int t = t0 + 16 * mi + 4 * q + r;
+      if (t < M) {
+#pragma unroll
+        for (int rg = 0; rg < 2; ++rg) {
+          const float g16 = h2f(f2h(acc[mi][rg][r]));
+          const float s16 = h2f(f2h(g16 / (1.0f + expf(-g16))));
+          const float u16 = h2f(f2h(acc[mi][rg + 2][r]));
+          g.act[(long long)t * I + 32 * blk + 16 * rg + n] = f2h(s16 * u16);
+        }
+      }
+    }
+  }
+}
+
 // y = fp16(sum_s part[s] + bias) (+ residual: fp16(residual + y))
 __global__ void __launch_bounds__(256) k_dg_fin(DenseGuardArgs g) {
   const long long n = (long long)g.M * g.d.H;
@@ -677,9 +654,10 @@ __global__ void __launch_bounds__(256) k_dg_fin(DenseGuardArgs g) {
 }
 
 using DgFn = void (*)(DenseGuardArgs);
+// [dq][MT / 4 - 1 of the 16 MT-token tile]
+const DgFn kDgGu2[2][4] = {{k_dg_gu2<false, 4>, k_dg_gu2<false, 8>, k_dg_gu2<false, 12>, k_dg_gu2<false, 16>},
+                           {k_dg_gu2<true, 4>, k_dg_gu2<true, 8>, k_dg_gu2<true, 12>, k_dg_gu2<true, 16>}};
 // [dq][MT - 1 of the 64 MT-token tile]
-const DgFn kDgGu[2][4] = {{k_dg_gu<false, 1>, k_dg_gu<false, 2>, k_dg_gu<false, 3>, k_dg_gu<false, 4>},
-                          {k_dg_gu<true, 1>, k_dg_gu<true, 2>, k_dg_gu<true, 3>, k_dg_gu<true, 4>}};
 // [dq][host copies][MT / 4 - 1 of the 16 MT-token tile]
 const DgFn kDgDown[2][2][4] = {
     {{k_dg_down<false, false, 4>, k_dg_down<false, false, 8>, k_dg_down<false, false, 12>, k_dg_down<false, false, 16>},
@@ -687,45 +665,27 @@ const DgFn kDgDown[2][2][4] = {
     {{k_dg_down<true, false, 4>, k_dg_down<true, false, 8>, k_dg_down<true, false, 12>, k_dg_down<true, false, 16>},
      {k_dg_down<true, true, 4>, k_dg_down<true, true, 8>, k_dg_down<true, true, 12>, k_dg_down<true, true, 16>}}};
 
-// Token tiles: whole 256-token tiles, then the rest of the prompt in the
-// smallest tile of 64, 128 or 192 tokens that holds it (a 256-token tile would
-// spend its MFMAs and token-row staging on padding): one launch per tile size.
-template <typename Launch>
-void dg_token_tiles(const DenseGuardArgs& g, Launch launch) {
-  const int full = g.M / kDgTok, rest = g.M - full * kDgTok;
-  DenseGuardArgs a = g;
-  if (full > 0) {
-    a.t_base = 0;
-    launch(a, 3, full);
-  }
-  if (rest > 0) {
-    a.t_base = full * kDgTok;
-    launch(a, (rest + 63) / 64 - 1, 1);
-  }
-}
-
 void dg_set_lds() {
   static std::once_flag once;
   std::call_once(once, [] {
-    for (int q = 0; q < 2; ++q)
-      for (int m = 0; m < 4; ++m) {
-        (void)hipFuncSetAttribute(reinterpret_cast<const void*>(kDgGu[q][m]),
-                                  hipFuncAttributeMaxDynamicSharedMemorySize, (int)kDgLds);
-      }
     for (int q = 0; q < 2; ++q)
       for (int h = 0; h < 2; ++h)
         for (int m = 0; m < 4; ++m)
           (void)hipFuncSetAttribute(reinterpret_cast<const void*>(kDgDown[q][h][m]),
                                     hipFuncAttributeMaxDynamicSharedMemorySize, (int)kDnLdsMax);
+    for (int q = 0; q < 2; ++q)
+      for (int m = 0; m < 4; ++m)
+        (void)hipFuncSetAttribute(reinterpret_cast<const void*>(kDgGu2[q][m]),
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, (int)kGuLds);
   });
 }
 
 }  // namespace
 
-// k_dg_down reads its code-pair table and token stages at fixed LDS
-// addresses (immediate offsets from 0): that holds only while the kernel has
-// no static LDS, so that its dynamic LDS starts at address 0.  Checked once
-// per process on the compiled kernels, before the first launch.
+// k_dg_down and k_dg_gu2 read their code-pair table and token stages at
+// fixed LDS addresses (immediate offsets from 0): that holds only while the
+// kernels have no static LDS, so that their dynamic LDS starts at address 0.
+// Checked once per process on the compiled kernels, before the first launch.
 int dense_down_check() {
   static std::once_flag once;
   static size_t static_lds = 0;
@@ -741,6 +701,15 @@ int dense_down_check() {
           }
           if (attr.sharedSizeBytes > static_lds) static_lds = attr.sharedSizeBytes;
         }
+    for (int q = 0; q < 2; ++q)
+      for (int m = 0; m < 4; ++m) {
+        hipFuncAttributes attr;
+        if (hipFuncGetAttributes(&attr, reinterpret_cast<const void*>(kDgGu2[q][m])) != hipSuccess) {
+          rc_attr = 1;
+          continue;
+        }
+        if (attr.sharedSizeBytes > static_lds) static_lds = attr.sharedSizeBytes;
+      }
   });
   if (rc_attr) {
     (void)hipGetLastError();
@@ -788,9 +757,18 @@ void launch_dense_down(const DenseGuardArgs& g, hipStream_t st) {
 
 void launch_dense_guard(const DenseGuardArgs& g, hipStream_t st) {
   dg_set_lds();
-  dg_token_tiles(g, [&](const DenseGuardArgs& a, int mt_idx, int tiles) {
-    kDgGu[a.d.dq ? 1 : 0][mt_idx]<<<dim3((unsigned)(a.d.NB / 4), (unsigned)tiles), dim3(kDgThreads), kDgLds, st>>>(a);
-  });
+  // whole 256-token tiles, then the rest in the smallest 64-, 128- or
+  // 192-token tile that holds it (per token the same sums, bit for bit)
+  const int full = g.M / kDnTok, rest = g.M - full * kDnTok;
+  DenseGuardArgs a = g;
+  if (full > 0) {
+    a.t_base = 0;
+    kDgGu2[g.d.dq ? 1 : 0][3]<<<dim3((unsigned)(g.d.NB / 4), (unsigned)full), dim3(kDnThreads), kGuLds, st>>>(a);
+  }
+  if (rest > 0) {
+    a.t_base = full * kDnTok;
+    kDgGu2[g.d.dq ? 1 : 0][(rest + 63) / 64 - 1]<<<dim3((unsigned)(g.d.NB / 4)), dim3(kDnThreads), kGuLds, st>>>(a);
+  }
   launch_dense_down(g, st);
 }
 

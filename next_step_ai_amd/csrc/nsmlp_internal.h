@@ -420,6 +420,13 @@ __device__ __forceinline__ uint4 buf_ld16c(rsrc_t r, uint32_t voff, uint32_t sof
   const u32x4_t t = __builtin_amdgcn_raw_buffer_load_b128(r, (int)voff, (int)soff, 0);
   return make_uint4(t.x, t.y, t.z, t.w);
 }
+__device__ __forceinline__ uint2 buf_ld8c(rsrc_t r, uint32_t voff, uint32_t soff) {
+  const u32x2_t t = __builtin_amdgcn_raw_buffer_load_b64(r, (int)voff, (int)soff, 0);
+  return make_uint2(t.x, t.y);
+}
+__device__ __forceinline__ uint32_t buf_ldu8c(rsrc_t r, uint32_t voff, uint32_t soff) {
+  return (uint32_t)__builtin_amdgcn_raw_buffer_load_b8(r, (int)voff, (int)soff, 0);
+}
 __device__ __forceinline__ int buf_ldic(rsrc_t r, uint32_t voff, uint32_t soff) {
   return (int)__builtin_amdgcn_raw_buffer_load_b32(r, (int)voff, (int)soff, 0);
 }
