@@ -236,7 +236,7 @@ DecodeWs decode_ws_layout(int H, int k) {
 }
 
 struct RouteWs {
-  size_t lat16, scores, lat_part, total;
+  size_t lat16, scores, lat_part, lat_p64, lat_p32, lat_und, lat_und_n, total;
 };
 
 RouteWs route_ws_layout(size_t base, int rows, int H, int R, int NB) {
@@ -248,6 +248,18 @@ RouteWs route_ws_layout(size_t base, int rows, int H, int R, int NB) {
   off += align_up((size_t)rows * NB * sizeof(uint16_t));
   w.lat_part = off;
   if (rows < kLatSplitRows) off += align_up((size_t)rows * R * kLatParts * 3 * sizeof(double));
+  w.lat_p64 = w.lat_p32 = w.lat_und = w.lat_und_n = off;
+  if (rows >= kLatSplitRows) {
+    const size_t n = (size_t)rows * R, P = (size_t)latent_mf_parts(rows, R, H);
+    w.lat_p64 = off;
+    off += align_up(P * n * sizeof(double));
+    w.lat_p32 = off;
+    off += align_up(P * n * sizeof(float));
+    w.lat_und = off;
+    off += align_up(n * sizeof(int));
+    w.lat_und_n = off;
+    off += align_up(sizeof(int));
+  }
   w.total = off;
   return w;
 }
@@ -367,6 +379,12 @@ int fill_route(RouteArgs& r, const void* x, int rows, int H, const void* enc_w, 
   r.scores = (uint16_t*)(base + L.scores);
   r.status = (int*)(base + kStatusOff);
   r.lat_part = rows < kLatSplitRows ? (double*)(base + L.lat_part) : nullptr;
+  const bool mf = rows >= kLatSplitRows;
+  r.lat_p64 = mf ? (double*)(base + L.lat_p64) : nullptr;
+  r.lat_p32 = mf ? (float*)(base + L.lat_p32) : nullptr;
+  r.lat_und = mf ? (int*)(base + L.lat_und) : nullptr;
+  r.lat_und_n = mf ? (int*)(base + L.lat_und_n) : nullptr;
+  r.lat_nparts = mf ? latent_mf_parts(rows, R, H) : 0;
   r.clear_words = nullptr;
   return NSMLP_OK;
 }

@@ -883,10 +883,29 @@ struct RouteArgs {
   // the call is written (the per-call status and block counts of a shared
   // scratch); nullptr: none
   int* clear_words;
+  // kLatSplitRows rows or more (16-byte loads): the matrix-core first pass's
+  // fp64 sums in lat_nparts column ranges [nparts][rows][R], their magnitude
+  // sums (fp32, same layout), the outputs left undecided [rows R] and their
+  // count; nullptr otherwise
+  double* lat_p64;
+  float* lat_p32;
+  int* lat_und;
+  int* lat_und_n;
+  int lat_nparts;
 };
 constexpr int kClearWords = 8;
 constexpr int kLatSplitRows = 8;
 constexpr int kLatParts = 4;
+// Column ranges of the matrix-core latent: two 4-wave workgroups per CU over
+// the 16 x 16 (token, latent row) tiles, at most 32 ranges, each wave at
+// least 32 columns.
+__host__ __device__ inline int latent_mf_parts(int rows, int R, int H) {
+  const int tiles = ((rows + 15) / 16) * ((R + 15) / 16);
+  int P = (512 + tiles - 1) / tiles;
+  if (P > 32) P = 32;
+  while (P > 1 && 4 * P * 32 > H) P >>= 1;
+  return P < 1 ? 1 : P;
+}
 
 void launch_route(const RouteArgs& a, hipStream_t s);
 // The latent and score kernels only (the top-k runs inside the decode).

@@ -6,8 +6,9 @@
 //                        for fewer than 8 tokens one workgroup per 1/4 of a
 //                        row (k_latent_part), the parts added and rounded by
 //                        the scores kernel;
-//                        from 8 tokens on, one workgroup per 8 x 8 tile of
-//                        latent rows and tokens (k_latent_tiled).
+//                        from 8 tokens on, the sums on the matrix cores in
+//                        fp64 with an error bound (k_latent_mf), exact
+//                        sums only where the bound leaves the rounding open.
 //   2. scores          : fp16 latent (+ the basis_top_k mask) -> exact score
 //                        dots (8 lanes per block) -> fp16, clamp, optional
 //                        down_block_norm scaling.
@@ -78,106 +79,164 @@ __global__ void __launch_bounds__(kLatThreads) k_latent(RouteArgs a) {
   }
 }
 
-// Many tokens: one workgroup per tile of 8 latent rows x 8 tokens; its 16
-// waves each sum a sixteenth of the hidden size.  Lane l takes latent row
-// l / 8 and token l % 8 of the tile and reads 8 columns of both per step
-// (16-byte loads; the 8 lanes of one row or token read the same bytes), so
-// each x and enc_w byte is read once per tile instead of once per output.
-// The first pass sums in plain fp64 (one add per term) with a bound on the
-// rounding error; an output whose bounded interval rounds to one fp16 value
-// has that value as the exact sum's rounding (the common case).  Any other
-// output of the tile is summed again in three parts (Exact3, exact for any
-// fp16 inputs) by the whole workgroup, so the fp16 latent equals k_latent's.
-constexpr int kLtRows = 8, kLtTok = 8, kLtThreads = 1024;
+// Many tokens (kLatSplitRows or more): the sums on the matrix cores.  A
+// workgroup of 4 waves takes a 16-token x 16-latent-row tile and a range of
+// the hidden size, a quarter of it per wave.  Per 32 columns lane l (i =
+// l % 16, g = l / 16) loads columns 8 g .. 8 g + 7 of token t0 + i's x row
+// and of latent row r0 + i's enc_w row and runs 8 steps of
+// v_mfma_f64_16x16x4_f64 (every product of two fp16 values is exact in
+// fp64; K slot g of step s is column 8 g + s) and the same steps on |x|, |w|
+// in fp32 (v_mfma_f32_16x16x4_f32) for the error bound.  The waves' tiles
+// meet in LDS in wave order and the workgroup writes range p of the sums.
+// k_latent_mfin adds the ranges in order and the bias: a sum of n exact terms
+// with any order of fp64 additions lies within n 2^-53 sum|t| of the exact
+// sum, so where that interval (with a 2x margin on the fp32 magnitude sum,
+// and 2^-49 for the bias add and the interval ends' own rounding) rounds to
+// one fp16 value, that value is the exact sum's rounding (the common case).
+// The other outputs (an exact sum near an fp16 rounding boundary, large
+// cancelling terms, inf or nan) go to a list that k_latent_fix sums again in
+// three parts (Exact3, exact for any fp16 inputs), one output per workgroup
+// at a time, so the fp16 latent equals k_latent's.
+typedef double mf_d4 __attribute__((ext_vector_type(4)));
+typedef float mf_f4 __attribute__((ext_vector_type(4)));
+constexpr int kMfThreads = 256;
+constexpr int kFixThreads = 1024, kFixGroups = 64;
 
-__global__ void __launch_bounds__(kLtThreads) k_latent_tiled(RouteArgs a) {
+__global__ void __launch_bounds__(kMfThreads) k_latent_mf(RouteArgs a) {
   const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
-  const int r = (int)blockIdx.x * kLtRows + (lane >> 3);
-  const int t = (int)blockIdx.y * kLtTok + (lane & 7);
-  const int rc = r < a.R ? r : a.R - 1, tc = t < a.rows ? t : a.rows - 1;  // clamped: every load is in range
-  const uint16_t* __restrict__ x = a.x + (long long)tc * a.H;
-  const uint16_t* __restrict__ w = a.enc_w + (long long)rc * a.H;
-  const int span = (a.H + 8 * kLtThreads / kWave - 1) / (8 * kLtThreads / kWave) * 8;  // columns per wave
-  const int c_lo = wave * span, c_hi = min(a.H, c_lo + span);
-  __shared__ double red[kLtThreads / kWave][kWave];
-  __shared__ float bred[kLtThreads / kWave][kWave];
-  __shared__ double xred[kLtThreads / kWave][3];
-  __shared__ unsigned long long undecided;
-  // First pass: plain fp64 sums and the sum of |term| (fp32, relative error
-  // below 2^-13 here).  Each product of two fp16 values is exact in fp32 and
-  // fp64, so a sum of n of them in any order is within (n - 1) 2^-53 sum|t|
-  // of the exact sum; where that interval (with the bias and a margin)
-  // rounds to one fp16 value, that value is the exact sum's.  4 fp64 and 4
-  // fp32 accumulators: independent add chains (the bound holds for any
-  // order of the adds).
-  double acc[4] = {0.0, 0.0, 0.0, 0.0};
-  float bnd[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll 4
-  for (int c = c_lo; c < c_hi; c += 8) {
-    const uint4 xv = *reinterpret_cast<const uint4*>(x + c);
-    const uint4 wv = *reinterpret_cast<const uint4*>(w + c);
-    const uint32_t xs[4] = {xv.x, xv.y, xv.z, xv.w};
-    const uint32_t ws[4] = {wv.x, wv.y, wv.z, wv.w};
+  const int RT = (a.R + 15) / 16;
+  const int tile = (int)blockIdx.x, p = (int)blockIdx.y, P = (int)gridDim.y;
+  const int r0 = (tile % RT) * 16, t0 = (tile / RT) * 16;
+  if (tile == 0 && p == 0 && tid == 0) *a.lat_und_n = 0;  // k_latent_mfin appends after this kernel
+  const int i = lane & 15, g = lane >> 4;
+  const int nt = min(16, a.rows - t0), nr = min(16, a.R - r0);
+  // descriptors over the tile's rows only (every offset below fits 32 bits)
+  const rsrc_t rx = make_rsrc(a.x + (long long)t0 * a.H, nt * a.H * 2);
+  const rsrc_t rw = make_rsrc(a.enc_w + (long long)r0 * a.H, nr * a.H * 2);
+  const uint32_t xo = i < nt ? ((uint32_t)i * (uint32_t)a.H + 8u * (uint32_t)g) * 2u : kOffNone;
+  const uint32_t wo = i < nr ? ((uint32_t)i * (uint32_t)a.H + 8u * (uint32_t)g) * 2u : kOffNone;
+  const int per = (a.H + 4 * P * 32 - 1) / (4 * P * 32) * 32;  // columns per wave
+  const int k0 = (4 * p + wave) * per, k1 = min(a.H, k0 + per);
+  // two fp64 accumulators (even and odd steps): two independent chains of
+  // dependent MFMAs; added at the end (one more rounding per output)
+  mf_d4 acc = {0.0, 0.0, 0.0, 0.0}, acc1 = {0.0, 0.0, 0.0, 0.0};
+  mf_f4 mag = {0.0f, 0.0f, 0.0f, 0.0f};
+  // groups of 4 chunks of 32 columns, double-buffered in registers: a
+  // group's loads are issued while the previous group is multiplied
+  // (columns past the wave's range or H load zeros: H % 8 == 0, so a lane's
+  // 8 columns are all inside or all past it)
+  auto load = [&](uint4 (&xv)[4], uint4 (&wv)[4], int c0) {
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const float p0 = h2f((uint16_t)(xs[q] & 0xFFFFu)) * h2f((uint16_t)(ws[q] & 0xFFFFu));
-      const float p1 = h2f((uint16_t)(xs[q] >> 16)) * h2f((uint16_t)(ws[q] >> 16));
-      bnd[q] += fabsf(p0) + fabsf(p1);
-      acc[q] += (double)p0 + (double)p1;
+    for (int u = 0; u < 4; ++u) {
+      const int c = c0 + 32 * u;
+      const bool in = c < k1 && c + 8 * g < a.H;
+      xv[u] = buf_ld16c(rx, in ? xo : kOffNone, (uint32_t)c * 2u);
+      wv[u] = buf_ld16c(rw, in ? wo : kOffNone, (uint32_t)c * 2u);
     }
-  }
-  red[wave][lane] = (acc[0] + acc[1]) + (acc[2] + acc[3]);
-  bred[wave][lane] = (bnd[0] + bnd[1]) + (bnd[2] + bnd[3]);
-  __syncthreads();
-  const bool real = r < a.R && t < a.rows;
-  if (wave == 0) {
-    double sum1 = 0.0;
-    float b = 0.0f;
+  };
+  auto mul = [&](const uint4 (&xv)[4], const uint4 (&wv)[4]) {
 #pragma unroll
-    for (int v = 0; v < kLtThreads / kWave; ++v) {
-      sum1 += red[v][lane];
-      b += bred[v][lane];
+    for (int u = 0; u < 4; ++u) {
+      const uint32_t xs[4] = {xv[u].x, xv[u].y, xv[u].z, xv[u].w};
+      const uint32_t ws[4] = {wv[u].x, wv[u].y, wv[u].z, wv[u].w};
+#pragma unroll
+      for (int s2 = 0; s2 < 8; ++s2) {
+        const float xf = h2f((uint16_t)(xs[s2 >> 1] >> (16 * (s2 & 1))));
+        const float wf = h2f((uint16_t)(ws[s2 >> 1] >> (16 * (s2 & 1))));
+        if (s2 & 1)
+          acc1 = __builtin_amdgcn_mfma_f64_16x16x4f64((double)xf, (double)wf, acc1, 0, 0, 0);
+        else
+          acc = __builtin_amdgcn_mfma_f64_16x16x4f64((double)xf, (double)wf, acc, 0, 0, 0);
+        mag = __builtin_amdgcn_mfma_f32_16x16x4f32(fabsf(xf), fabsf(wf), mag, 0, 0, 0);
+      }
     }
-    const double bias = a.enc_b != nullptr ? (double)h2f(a.enc_b[rc]) : 0.0;
-    const double sb = sum1 + bias;
-    // (H + 64) 2^-53 (2 b): the sums' rounding (2 b > sum|t|); 2^-49 (|sb| +
-    // |bias|): the bias add and the two interval ends' own rounding
-    const double B = (double)(a.H + 64) * 1.1102230246251565e-16 * (2.0 * (double)b) +
-                     1.7763568394002505e-15 * (fabs(sb) + fabs(bias));
-    const uint16_t lo = exact_to_f16(Exact3{sb - B, 0.0, 0.0});
-    const uint16_t hi = exact_to_f16(Exact3{sb + B, 0.0, 0.0});
-    const bool ok = b < 3.0e38f && fabs(sb) < 1.0e300 && lo == hi;  // false for inf and nan
-    if (ok && real) a.lat16[(long long)t * a.R + r] = lo;
-    const unsigned long long m = __ballot(!ok);
-    if (lane == 0) undecided = m;
+  };
+  uint4 xa[4], wa[4], xb[4], wb[4];
+  load(xa, wa, k0);
+  for (int c = k0; c < k1; c += 256) {
+    load(xb, wb, c + 128);
+    mul(xa, wa);
+    load(xa, wa, c + 256);
+    if (c + 128 < k1) mul(xb, wb);  // uniform
+  }
+  mfma_drain();
+  acc += acc1;
+  // C layouts (measured): f64 lane L element q = (token 4 q + L / 16, row
+  // L % 16); f32 lane L element q = (token 4 (L / 16) + q, row L % 16)
+  __shared__ double r64[4][256];
+  __shared__ float r32[4][256];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    r64[wave][(4 * q + g) * 16 + i] = acc[q];
+    r32[wave][(4 * g + q) * 16 + i] = mag[q];
   }
   __syncthreads();
-  // The outputs the fp64 sums leave undecided (an exact sum within the
-  // bound of an fp16 rounding boundary, large cancelling terms, inf or nan),
-  // one at a time over the whole workgroup: the three-part sums (exact for
-  // any fp16 inputs, in any split of the terms) and one rounding.
-  unsigned long long m = undecided;
-  while (m != 0ull) {
-    const int l = __builtin_ctzll(m);
-    m &= m - 1ull;
-    const int ur = (int)blockIdx.x * kLtRows + (l >> 3), ut = (int)blockIdx.y * kLtTok + (l & 7);
-    const uint16_t* __restrict__ ux = a.x + (long long)min(ut, a.rows - 1) * a.H;
-    const uint16_t* __restrict__ uw = a.enc_w + (long long)min(ur, a.R - 1) * a.H;
-    Exact3 e = exact_zero();
-    for (int c = tid; c < a.H; c += kLtThreads) exact_add(e, (double)(h2f(ux[c]) * h2f(uw[c])));
-    e = wave_sum_exact(e);
+  const int ot = tid >> 4, orr = tid & 15;  // thread tid: token t0 + ot, latent row r0 + orr
+  if (ot < nt && orr < nr) {
+    const double sv = ((r64[0][tid] + r64[1][tid]) + r64[2][tid]) + r64[3][tid];
+    const float bv = ((r32[0][tid] + r32[1][tid]) + r32[2][tid]) + r32[3][tid];
+    const long long o = ((long long)p * a.rows + (t0 + ot)) * a.R + (r0 + orr);
+    a.lat_p64[o] = sv;
+    a.lat_p32[o] = bv;
+  }
+}
+
+// One thread per output: the ranges added in order, the bound, the write or
+// the list of undecided outputs.
+__global__ void __launch_bounds__(256) k_latent_mfin(RouteArgs a) {
+  const long long n = (long long)a.rows * a.R;
+  const long long o = (long long)blockIdx.x * 256 + threadIdx.x;
+  if (o >= n) return;
+  const int r = (int)(o % a.R);
+  double sum1 = 0.0;
+  float b = 0.0f;
+  for (int p = 0; p < a.lat_nparts; ++p) {
+    sum1 += a.lat_p64[p * n + o];
+    b += a.lat_p32[p * n + o];
+  }
+  const double bias = a.enc_b != nullptr ? (double)h2f(a.enc_b[r]) : 0.0;
+  const double sb = sum1 + bias;
+  // (H + 64) 2^-53 (2 b): the sums' roundings (at most one per term, the
+  // ranges' and the waves' additions; 2 b > sum|t|); 2^-49 (|sb| + |bias|):
+  // the bias add and the interval ends' own rounding
+  const double B = (double)(a.H + 64) * 1.1102230246251565e-16 * (2.0 * (double)b) +
+                   1.7763568394002505e-15 * (fabs(sb) + fabs(bias));
+  const uint16_t lo = exact_to_f16(Exact3{sb - B, 0.0, 0.0});
+  const uint16_t hi = exact_to_f16(Exact3{sb + B, 0.0, 0.0});
+  const bool ok = b < 3.0e38f && fabs(sb) < 1.0e300 && lo == hi;  // false for inf and nan
+  if (ok) {
+    a.lat16[o] = lo;
+  } else {
+    const int slot = atomicAdd(a.lat_und_n, 1);
+    a.lat_und[slot] = (int)o;
+  }
+}
+
+// The undecided outputs, exactly: workgroup w takes list entries w, w + G, ...
+__global__ void __launch_bounds__(kFixThreads) k_latent_fix(RouteArgs a) {
+  const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
+  __shared__ double xred[kFixThreads / kWave][3];
+  const int cnt = *a.lat_und_n;
+  for (int e = (int)blockIdx.x; e < cnt; e += (int)gridDim.x) {
+    const int o = a.lat_und[e];
+    const int t = o / a.R, r = o % a.R;
+    const uint16_t* __restrict__ ux = a.x + (long long)t * a.H;
+    const uint16_t* __restrict__ uw = a.enc_w + (long long)r * a.H;
+    Exact3 ex = exact_zero();
+    for (int c = tid; c < a.H; c += kFixThreads) exact_add(ex, (double)(h2f(ux[c]) * h2f(uw[c])));
+    ex = wave_sum_exact(ex);
     if (lane == 0) {
-      xred[wave][0] = e.a0;
-      xred[wave][1] = e.a1;
-      xred[wave][2] = e.a2;
+      xred[wave][0] = ex.a0;
+      xred[wave][1] = ex.a1;
+      xred[wave][2] = ex.a2;
     }
     __syncthreads();
-    if (tid == 0 && ur < a.R && ut < a.rows) {
+    if (tid == 0) {
       Exact3 sum = exact_zero();
 #pragma unroll
-      for (int v = 0; v < kLtThreads / kWave; ++v) exact_merge(sum, Exact3{xred[v][0], xred[v][1], xred[v][2]});
-      if (a.enc_b != nullptr) exact_add(sum, (double)h2f(a.enc_b[ur]));
-      a.lat16[(long long)ut * a.R + ur] = exact_to_f16(sum);
+      for (int v = 0; v < kFixThreads / kWave; ++v) exact_merge(sum, Exact3{xred[v][0], xred[v][1], xred[v][2]});
+      if (a.enc_b != nullptr) exact_add(sum, (double)h2f(a.enc_b[r]));
+      a.lat16[o] = exact_to_f16(sum);
     }
     __syncthreads();
   }
@@ -189,7 +248,6 @@ __global__ void __launch_bounds__(kLtThreads) k_latent_tiled(RouteArgs a) {
 // (Exact3 parts; the bias goes into range 0); k_scores adds the parts (exact
 // in any grouping) and rounds once, so the fp16 latent equals k_latent's.
 constexpr int kLpThreads = 256;
-static_assert(kLtTok == kLatSplitRows, "the tiled latent takes the rows the split latent does not");
 
 template <bool kVec>
 __global__ void __launch_bounds__(kLpThreads) k_latent_part(RouteArgs a) {
@@ -240,9 +298,12 @@ __global__ void __launch_bounds__(kLpThreads) k_latent_part(RouteArgs a) {
 }
 
 void launch_latent(const RouteArgs& a, hipStream_t s) {
-  if (a.vec && a.rows >= kLtTok) {
-    const dim3 g((a.R + kLtRows - 1) / kLtRows, (a.rows + kLtTok - 1) / kLtTok);
-    hipLaunchKernelGGL(k_latent_tiled, g, dim3(kLtThreads), 0, s, a);
+  if (a.vec && a.lat_p64 != nullptr) {
+    const int tiles = ((a.rows + 15) / 16) * ((a.R + 15) / 16);
+    hipLaunchKernelGGL(k_latent_mf, dim3(tiles, a.lat_nparts), dim3(kMfThreads), 0, s, a);
+    const long long n = (long long)a.rows * a.R;
+    hipLaunchKernelGGL(k_latent_mfin, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, a);
+    hipLaunchKernelGGL(k_latent_fix, dim3(kFixGroups), dim3(kFixThreads), 0, s, a);
     return;
   }
   if (a.lat_part != nullptr) {
