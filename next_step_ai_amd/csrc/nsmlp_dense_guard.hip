@@ -43,29 +43,31 @@ typedef float float2_t __attribute__((ext_vector_type(2)));
 // ------------------------------------------------------------- down GEMM --
 // part[s][t][o] = sum over the blocks of range s of act[t][i] * Wd[o][i],
 // Wd = fp16(code * absmax).  A workgroup of 4 waves takes 256 output rows,
-// 256 tokens and one block range; wave w owns rows 64 w .. + 63 and keeps
-// all 256 tokens x 64 rows in 256 fp32 accumulators (AGPRs), so each decoded
-// weight feeds 16 MFMAs and every weight is read from HBM once.  A step
-// covers 2 blocks (64 columns):
-//   - lane (n = l % 16, q = l / 16) loads, for each of its 4 16-row groups,
-//     8 packed bytes of row n: bytes 8 (q / 2) .. + 7 of block 2 c + q % 2.
-//     Dword j of them is the lane's B fragment for MFMA step j, so K slots
-//     8 q .. 8 q + 7 of step j are columns 16 (q / 2) + 8 j .. + 7 of block
-//     2 c + q % 2.  The weights are decoded in registers (each row by one
-//     wave, no LDS staging) through a lane-replicated fp32 code-pair table:
-//     two fp32 products rounded to fp16 by one v_cvt_pk_f16_f32;
+// 256 tokens and one block range; wave w owns rows 64 w .. + 63 as two
+// 32-row tiles and keeps all 256 tokens x 64 rows in 256 fp32 accumulators
+// (AGPRs: 8 token tiles x 2 row tiles of v_mfma_f32_32x32x16_f16), so each
+// decoded weight feeds the MFMAs of all 256 tokens and every weight is read
+// from HBM once.  A step covers 2 blocks (64 columns), 4 MFMA steps of 16:
+//   - lane (j = l % 32, kh = l / 32) loads, for each row tile, the 16 packed
+//     bytes of its row j of block 2 c + kh (the block's 32 columns); dword s
+//     is its B fragment of MFMA step s: K slots 8 kh .. + 7 are columns
+//     8 s .. + 7 of block 2 c + kh, i.e. columns 32 kh + 8 s .. + 7 of the
+//     step.  The weights are decoded in registers (each row by one wave, no
+//     LDS staging) through a lane-replicated fp32 code-pair table: two fp32
+//     products rounded to fp16 by one v_cvt_pk_f16_f32;
 //   - the 256 token rows of the 64 columns (128 bytes each) go into an LDS
 //     stage by loads straight into LDS; row r's 16-byte piece p lands in
-//     slot p ^ ((r / 2) % 8), so 16 rows read at one piece hit 16 different
-//     16-byte bank groups;
-//   - every wave runs 2 MFMA steps x 4 row groups x 16 token groups.
-// One wave per SIMD: 256 accumulators leave no room for a second.  A wave
-// does not overlap its own VALU work with its MFMAs (measured on this GPU:
-// one wave reaches 72% of the MFMA peak with no other work, 49% with two
-// VALU ops per MFMA), so the decode is kept to about one VALU op per MFMA
-// (each decoded weight feeds 16 MFMAs) and issued between the MFMAs, and
-// every LDS read is issued a unit of MFMAs before its use (see the step
-// schedule below).
+//     slot p ^ ((r / 2) % 8); the A fragment of token tile mi and MFMA step s
+//     is piece 4 kh + s of row 32 mi + j, and the 16 rows a group of 16 lanes
+//     reads at one piece hit 16 different 16-byte bank groups;
+//   - every wave runs 4 MFMA steps x 2 row tiles x 8 token tiles.
+// One wave per SIMD: 256 accumulators leave no room for a second.  The
+// 32-cycle 32x32x16 MFMA leaves issue room for the decode between MFMAs
+// (measured on this GPU at one wave per SIMD with independent MFMAs: 94% of
+// the MFMA cycles busy with two VALU ops per MFMA and 91% with four, against
+// 43-81% for the 16-cycle 16x16x32 shape with one or two; the decode here is
+// about two VALU ops per MFMA), and every LDS read is issued a unit of MFMAs
+// before its use (see the step schedule below).
 constexpr int kDnThreads = 256;
 constexpr int kDnTok = 256;                            // tokens per tile
 constexpr int kDnRows = 256;                           // output rows per workgroup (64 per wave)
@@ -112,6 +114,11 @@ __device__ __forceinline__ half8_t dn_finish8(const DnPairs& pr, float am) {
   }
   return as_h8(make_uint4(o[0], o[1], o[2], o[3]));
 }
+// dword s (a constant) of a 16-byte weight load
+template <int s>
+__device__ __forceinline__ uint32_t dn_word(const uint4& w) {
+  return s == 0 ? w.x : s == 1 ? w.y : s == 2 ? w.z : w.w;
+}
 
 // Bytes spanned by the packed rows (abs = false, 16 bytes per row and block)
 // or the absmax entries (elem bytes each) of `blocks` slots of a down view.
@@ -121,20 +128,139 @@ __host__ __device__ inline long long dn_extent(const ProjView& v, int blocks, in
   return abs ? ((blocks - 1) * bs + (long long)(H - 1) * rs + 1) * elem : (blocks - 1) * bs + (long long)(H - 1) * rs + elem;
 }
 
-// One step's weight loads: 8 packed bytes per 16-row group and their absmax
+// One step's weight loads: 16 packed bytes per 32-row tile and their absmax
 // (u8 code + second-level scale, or fp32).
 struct DnW {
-  uint2 w[4];
-  uint32_t qa[4];
-  float a[4];
+  uint4 w[2];
+  uint32_t qa[2];
+  float a[2];
   int ok;  // the lane's block is valid (its absmax is forced to zero otherwise)
 };
 
+// The step schedule both GEMMs share: 4 units (MFMA step s = 0..3) of 16
+// MFMAs (8 token tiles x 2 row tiles); unit s runs MFMA step s while it reads
+// the A fragments of step s + 1, finishes the B fragments of step s + 1
+// (looked up in unit s - 1) and looks up those of step s + 2.  Before the
+// last unit the wave waits for step c + 1's loads and meets the others at the
+// barrier (every wave has read its last A fragments of stage c & 1), sends
+// step c + 2's token rows into that stage and reads step c + 1's first A
+// fragments.  Three weight register sets: decoded, arrived, in flight, moved
+// down one set at the end of a step; step c + 2's weights go out in unit 0,
+// as soon as their set is free, so that they have landed when the move at the
+// end of the step copies them.
+template <int NT, typename IssueW, typename IssueX, typename AmOf>
+__device__ __forceinline__ void dn_gemm(float16_t (&acc)[NT][2], int nst, uint32_t abase, IssueW&& issue_w,
+                                        IssueX&& issue_x, AmOf&& am_of) {
+  const int lane = threadIdx.x & (kWave - 1);
+  uint32_t ad[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) ad[i] = (uint32_t)(lane & (kDnCopies - 1)) * 8u;
+  // A fragment (token tile mi, MFMA step s) of step c: abase holds the
+  // lane's row and swizzled piece 4 kh; step s is piece 4 kh + s, whose slot
+  // is the lane's slot with s XORed in
+  auto read_a = [&](half8_t (&a)[NT], int c, int s) {
+    const uint32_t base = (abase ^ ((uint32_t)s << 4)) + (uint32_t)(c & 1) * kDnStage;
+#pragma unroll
+    for (int mi = 0; mi < NT; ++mi) a[mi] = lds_ld_h8(base + (uint32_t)mi * 4096u);
+  };
+  auto lookup2 = [&](DnPairs (&pr)[2], const DnW& W, auto s) {
+#pragma unroll
+    for (int u = 0; u < 2; ++u) pr[u] = dn_lookup4(dn_word<decltype(s)::value>(W.w[u]), ad);
+  };
+  auto finish2 = [&](half8_t (&b)[2], const DnPairs (&pr)[2], const float (&am)[2]) {
+#pragma unroll
+    for (int u = 0; u < 2; ++u) b[u] = dn_finish8(pr[u], am[u]);
+  };
+  // 2 NT MFMAs, each followed by an LDS read and two VALU ops of the work
+  // ahead
+  auto mfma_unit = [&](const half8_t (&a)[NT], const half8_t (&b)[2]) {
+#pragma unroll
+    for (int u = 0; u < 2; ++u)
+#pragma unroll
+      for (int mi = 0; mi < NT; ++mi) acc[mi][u] = mfma32(a[mi], b[u], acc[mi][u]);
+#pragma unroll
+    for (int i = 0; i < 2 * NT; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  auto step_sync = [] {
+    __builtin_amdgcn_s_waitcnt(0);  // vmcnt(0) expcnt(0) lgkmcnt(0)
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+  };
+  using S0 = std::integral_constant<int, 0>;
+  using S1 = std::integral_constant<int, 1>;
+  using S2 = std::integral_constant<int, 2>;
+  using S3 = std::integral_constant<int, 3>;
+
+  DnW W0, W1, W2;
+  half8_t a0[NT], a1[NT], b0[2], b1[2];
+  DnPairs p0[2], p1[2];
+  float am_c[2], am_n[2];
+  issue_w(W0, 0);
+  issue_x(0);
+  issue_w(W1, 1);
+  issue_x(1);
+  __builtin_amdgcn_s_waitcnt(0);
+  __builtin_amdgcn_s_barrier();  // step 0's token rows are in LDS (and step 1's)
+  asm volatile("" ::: "memory");
+  am_of(W0, am_c);
+  read_a(a0, 0, 0);
+  lookup2(p0, W0, S0{});
+  finish2(b0, p0, am_c);
+  lookup2(p1, W0, S1{});
+  __builtin_amdgcn_sched_barrier(0);
+
+  auto step = [&](int c, const DnW& Wc, const DnW& Wn, DnW& Wf) {
+    // unit 0: B of MFMA step 1 finished, step 2's looked up
+    issue_w(Wf, c + 2);
+    read_a(a1, c, 1);
+    finish2(b1, p1, am_c);
+    lookup2(p0, Wc, S2{});
+    mfma_unit(a0, b0);
+    // unit 1
+    read_a(a0, c, 2);
+    finish2(b0, p0, am_c);
+    lookup2(p1, Wc, S3{});
+    mfma_unit(a1, b1);
+    // unit 2: the next step's absmax and its MFMA step 0 looked up
+    read_a(a1, c, 3);
+    finish2(b1, p1, am_c);
+    am_of(Wn, am_n);
+    lookup2(p0, Wn, S0{});
+    mfma_unit(a0, b0);
+    // unit 3
+    step_sync();
+    issue_x(c + 2);
+    read_a(a0, c + 1, 0);
+    finish2(b0, p0, am_n);
+    lookup2(p1, Wn, S1{});
+    mfma_unit(a1, b1);
+#pragma unroll
+    for (int u = 0; u < 2; ++u) am_c[u] = am_n[u];
+#pragma unroll
+    for (int mi = 0; mi < NT; ++mi)
+#pragma unroll
+      for (int u = 0; u < 2; ++u) asm volatile("" : "+a"(acc[mi][u]));
+  };
+  for (int c = 0; c < nst; ++c) {
+    step(c, W0, W1, W2);
+    W0 = W1;
+    W1 = W2;
+  }
+  __builtin_amdgcn_s_waitcnt(0);
+  mfma_drain();
+}
+
 // MT token groups of 16 per tile (16: 256 tokens; 4, 8 or 12 for the tokens
-// past the last whole 256-token tile).
+// past the last whole 256-token tile), i.e. MT / 2 tiles of 32.
 template <bool DQ, bool HOST, int MT>
 __global__ void __launch_bounds__(kDnThreads, 1) k_dg_down(DenseGuardArgs g) {
   extern __shared__ __attribute__((aligned(16))) uint8_t dn_lds[];  // no static LDS: dn_lds is LDS address 0
+  constexpr int NT = MT / 2;
   const DecodeArgs& d = g.d;
   const int tid = threadIdx.x, lane = tid & (kWave - 1);
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -177,8 +303,8 @@ __global__ void __launch_bounds__(kDnThreads, 1) k_dg_down(DenseGuardArgs g) {
   }
   __syncthreads();
 
-  const int n = lane & 15, q = lane >> 4, qb = q & 1, qh = q >> 1;
-  const uint32_t o0 = (uint32_t)(rt * kDnRows + wave * 64 + n);  // row of group 0; group rg: o0 + 16 rg
+  const int j = lane & 31, kh = lane >> 5;
+  const uint32_t o0 = (uint32_t)(rt * kDnRows + wave * 64 + j);  // row of tile 0; tile u: o0 + 32 u
   const uint32_t rs = (uint32_t)d.down.row_stride, bs = (uint32_t)d.down.blk_stride;
   const uint32_t ars = (uint32_t)d.down.abs_row_stride, abs_ = (uint32_t)d.down.abs_blk_stride;
   const uint32_t Ad = (uint32_t)I >> d.qbs_shift;
@@ -193,45 +319,45 @@ __global__ void __launch_bounds__(kDnThreads, 1) k_dg_down(DenseGuardArgs g) {
                        : ra;
   const rsrc_t rx = make_rsrc(g.act, (int)((long long)M * I * 2));
 
-  // Offsets: a lane's row in 16-row group rg is o0 + 16 rg, so the group's
-  // part of every weight and absmax offset is a uniform constant that goes
-  // into the load's scalar offset; the rows of a wave (64, H % 256 == 0) are
-  // all inside H or all outside.  Every offset is computed, then selected:
-  // a select between two registers (an arm with arithmetic becomes a
-  // branch, which splits the step into blocks the scheduler and the register
-  // allocator see separately).
+  // Offsets: a lane's row in tile u is o0 + 32 u, so the tile's part of every
+  // weight and absmax offset is a uniform constant that goes into the load's
+  // scalar offset; the rows of a wave (64, H % 256 == 0) are all inside H or
+  // all outside.  Every offset is computed, then selected: a select between
+  // two registers (an arm with arithmetic becomes a branch, which splits the
+  // step into blocks the scheduler and the register allocator see
+  // separately).
   const bool wrows = (int)(rt * kDnRows + wave * 64) < H;
   auto issue_w = [&](DnW& W, int c) {
     const int cc = max(0, min(c, nst - 1));  // clamped: the reference read stays in the range
-    const int enc = refs[2 * cc + qb];
+    const int enc = refs[2 * cc + kh];
     const bool ok = (c < nst) & (enc >= 0) & wrows;
     const bool host = HOST & ((enc & kDnRefHost) != 0);
     const uint32_t qq = (uint32_t)(enc & (kDnRefHost - 1));
-    const uint32_t b = (uint32_t)(b_lo + 2 * cc + qb);
+    const uint32_t b = (uint32_t)(b_lo + 2 * cc + kh);
     const bool dv = ok & !host, hv = ok & host;
-    const uint32_t wo_d = qq * bs + o0 * rs + 8u * (uint32_t)qh, ao_d = qq * abs_ + o0 * ars;
-    const uint32_t wo_h = b * bs + o0 * rs + 8u * (uint32_t)qh, ao_h = b * abs_ + o0 * ars;
+    const uint32_t wo_d = qq * bs + o0 * rs, ao_d = qq * abs_ + o0 * ars;
+    const uint32_t wo_h = b * bs + o0 * rs, ao_h = b * abs_ + o0 * ars;
     const uint32_t ab = DQ ? 1u : 4u;
     const uint32_t wo = dv ? wo_d : kOffNone, ao = dv ? ao_d * ab : kOffNone;
     const uint32_t who = hv ? wo_h : kOffNone, aho = hv ? ao_h * ab : kOffNone;
     const uint32_t f0 = o0 * Ad + ((32u * b) >> d.qbs_shift);
     W.ok = ok;
 #pragma unroll
-    for (int rg = 0; rg < 4; ++rg) {
-      const uint32_t so_w = 16u * (uint32_t)rg * rs, so_a = 16u * (uint32_t)rg * ars * ab;
-      W.w[rg] = buf_ld8(rw, wo, so_w);
+    for (int u = 0; u < 2; ++u) {
+      const uint32_t so_w = 32u * (uint32_t)u * rs, so_a = 32u * (uint32_t)u * ars * ab;
+      W.w[u] = buf_ld16(rw, wo, so_w);
       if constexpr (HOST) {
-        const uint2 h = buf_ld8(rwh, who, so_w);
-        W.w[rg] = make_uint2(W.w[rg].x | h.x, W.w[rg].y | h.y);
+        const uint4 h = buf_ld16(rwh, who, so_w);
+        W.w[u] = make_uint4(W.w[u].x | h.x, W.w[u].y | h.y, W.w[u].z | h.z, W.w[u].w | h.w);
       }
       if constexpr (DQ) {
-        W.qa[rg] = buf_ldu8(ra, ao, so_a);
-        if constexpr (HOST) W.qa[rg] |= buf_ldu8(rah, aho, so_a);
-        const uint32_t fo = ((f0 + 16u * (uint32_t)rg * Ad) >> d.dq_shift) * 4u;
-        W.a[rg] = buf_ldfc(r2, ok ? fo : kOffNone, 0);
+        W.qa[u] = buf_ldu8(ra, ao, so_a);
+        if constexpr (HOST) W.qa[u] |= buf_ldu8(rah, aho, so_a);
+        const uint32_t fo = ((f0 + 32u * (uint32_t)u * Ad) >> d.dq_shift) * 4u;
+        W.a[u] = buf_ldfc(r2, ok ? fo : kOffNone, 0);
       } else {
-        W.a[rg] = buf_ldf(ra, ao, so_a);
-        if constexpr (HOST) W.a[rg] = __uint_as_float(__float_as_uint(W.a[rg]) | __float_as_uint(buf_ldf(rah, aho, so_a)));
+        W.a[u] = buf_ldf(ra, ao, so_a);
+        if constexpr (HOST) W.a[u] = __uint_as_float(__float_as_uint(W.a[u]) | __float_as_uint(buf_ldf(rah, aho, so_a)));
       }
     }
   };
@@ -251,141 +377,42 @@ __global__ void __launch_bounds__(kDnThreads, 1) k_dg_down(DenseGuardArgs g) {
       ld_lds16s(rx, dn_lds + sb + (32 * i + 8 * wave) * 128, xi, 64u * (uint32_t)i * (uint32_t)I);
     }
   };
+  auto am_of = [&](const DnW& W, float (&am)[2]) {
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      float v = W.a[u];
+      if constexpr (DQ) v = dq_absmax(c2s[W.qa[u]], W.a[u], d.down.offset);
+      am[u] = W.ok ? v : 0.0f;
+    }
+  };
 
   // 256 accumulators, kept in AGPRs: pinned there at the start and after
   // every step (otherwise part of them crosses the loop in VGPRs, which the
   // loads in flight and the decode need)
-  float4_t acc[MT][4];
+  float16_t acc[NT][2];
 #pragma unroll
-  for (int mi = 0; mi < MT; ++mi)
+  for (int mi = 0; mi < NT; ++mi)
 #pragma unroll
-    for (int rg = 0; rg < 4; ++rg) {
-      acc[mi][rg] = float4_t{0.0f, 0.0f, 0.0f, 0.0f};
-      asm volatile("" : "+a"(acc[mi][rg]));
+    for (int u = 0; u < 2; ++u) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[mi][u][r] = 0.0f;
+      asm volatile("" : "+a"(acc[mi][u]));
     }
-  uint32_t ad[4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) ad[i] = (uint32_t)(lane & (kDnCopies - 1)) * 8u;
-  // A fragment (token group mi, MFMA step j) of step c: token row 16 mi + n,
-  // piece 4 (q % 2) + 2 (q / 2) + j, in slot piece ^ ((row / 2) % 8)
-  auto read_a = [&](half8_t (&a)[MT / 2], int c, int j, int h) {
-    const uint32_t piece = (uint32_t)(4 * qb + 2 * qh + j);
-    const uint32_t base = kDnTab + (uint32_t)(c & 1) * kDnStage + (uint32_t)n * 128u +
-                          ((piece ^ (uint32_t)((n >> 1) & 7)) << 4) + (uint32_t)h * 1024u * MT;
-#pragma unroll
-    for (int mi = 0; mi < MT / 2; ++mi) a[mi] = lds_ld_h8(base + (uint32_t)mi * 2048u);
-  };
-  auto am_of = [&](const DnW& W, float (&am)[4]) {
-#pragma unroll
-    for (int rg = 0; rg < 4; ++rg) {
-      float v = W.a[rg];
-      if constexpr (DQ) v = dq_absmax(c2s[W.qa[rg]], W.a[rg], d.down.offset);
-      am[rg] = W.ok ? v : 0.0f;
-    }
-  };
-  auto lookup4 = [&](DnPairs (&pr)[4], const DnW& W, int j) {
-#pragma unroll
-    for (int rg = 0; rg < 4; ++rg) pr[rg] = dn_lookup4(j == 0 ? W.w[rg].x : W.w[rg].y, ad);
-  };
-  auto finish4 = [&](half8_t (&b)[4], const DnPairs (&pr)[4], const float (&am)[4]) {
-#pragma unroll
-    for (int rg = 0; rg < 4; ++rg) b[rg] = dn_finish8(pr[rg], am[rg]);
-  };
-  // 2 MT MFMAs: token groups MT / 2 h .. + MT / 2 - 1 x the 4 row groups
-  auto mfma_unit = [&](const half8_t (&a)[MT / 2], const half8_t (&b)[4], int h) {
-#pragma unroll
-    for (int rg = 0; rg < 4; ++rg)
-#pragma unroll
-      for (int mi = 0; mi < MT / 2; ++mi) acc[MT / 2 * h + mi][rg] = mfma16(a[mi], b[rg], acc[MT / 2 * h + mi][rg]);
-    // each MFMA followed by an LDS read and a VALU op of the work ahead
-#pragma unroll
-    for (int i = 0; i < 2 * MT; ++i) {
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);
-    }
-    __builtin_amdgcn_sched_barrier(0);
-  };
-  auto step_sync = [] {
-    __builtin_amdgcn_s_waitcnt(0);  // vmcnt(0) expcnt(0) lgkmcnt(0)
-    __builtin_amdgcn_s_barrier();
-    asm volatile("" ::: "memory");
-  };
-
-  // A step is 4 units (MFMA step j, token half h) of 32 MFMAs; while unit
-  // (j, h) runs, the A fragments of the next unit are read and the B
-  // fragments of the next MFMA step are looked up (h = 0) or finished
-  // (h = 1).  Before the last unit the wave waits for step c + 1's loads and
-  // meets the others at the barrier (every wave has read its last A
-  // fragments of stage c & 1), sends step c + 2's token rows into that stage
-  // and reads step c + 1's first A fragments.  Three weight register sets:
-  // decoded, arrived, in flight, moved down one set at the end of a step.
-  // Step c + 2's weights are issued in unit (0, 1), not after the barrier:
-  // the move at the end of the step copies the set in flight, which waits
-  // for its loads, and issued after the barrier they had not landed by then
-  // (862 -> 797 us for the 405B prefill MLP at 256 tokens).
-  DnW W0, W1, W2;
-  half8_t ax[MT / 2], ay[MT / 2], b0[4], b1[4];
-  DnPairs pr[4];
-  float am_c[4], am_n[4];
-  issue_w(W0, 0);
-  issue_x(0);
-  issue_w(W1, 1);
-  issue_x(1);
-  __builtin_amdgcn_s_waitcnt(0);
-  __builtin_amdgcn_s_barrier();  // step 0's token rows are in LDS (and step 1's)
-  asm volatile("" ::: "memory");
-  am_of(W0, am_c);
-  read_a(ax, 0, 0, 0);
-  lookup4(pr, W0, 0);
-  finish4(b0, pr, am_c);
-  __builtin_amdgcn_sched_barrier(0);
-
-  auto step = [&](int c, const DnW& Wc, const DnW& Wn, DnW& Wf) {
-    // unit (0, 0): B fragments of MFMA step 1 looked up
-    read_a(ay, c, 0, 1);
-    lookup4(pr, Wc, 1);
-    mfma_unit(ax, b0, 0);
-    // unit (0, 1): ... and finished
-    issue_w(Wf, c + 2);
-    read_a(ax, c, 1, 0);
-    finish4(b1, pr, am_c);
-    mfma_unit(ay, b0, 1);
-    // unit (1, 0): the next step's MFMA step 0 looked up (its weights are in)
-    read_a(ay, c, 1, 1);
-    am_of(Wn, am_n);
-    lookup4(pr, Wn, 0);
-    mfma_unit(ax, b1, 0);
-    // unit (1, 1)
-    step_sync();
-    issue_x(c + 2);
-    read_a(ax, c + 1, 0, 0);
-    finish4(b0, pr, am_n);
-    mfma_unit(ay, b1, 1);
-#pragma unroll
-    for (int rg = 0; rg < 4; ++rg) am_c[rg] = am_n[rg];
-#pragma unroll
-    for (int mi = 0; mi < MT; ++mi)
-#pragma unroll
-      for (int rg = 0; rg < 4; ++rg) asm volatile("" : "+a"(acc[mi][rg]));
-  };
-  for (int c = 0; c < nst; ++c) {
-    step(c, W0, W1, W2);
-    W0 = W1;
-    W1 = W2;
-  }
-  __builtin_amdgcn_s_waitcnt(0);
-  mfma_drain();
+  // the lane's A fragment address of MFMA step 0 in stage 0: row j, piece 4 kh
+  const uint32_t abase = kDnTab + (uint32_t)j * 128u + ((4u * (uint32_t)kh ^ (uint32_t)((j >> 1) & 7)) << 4);
+  dn_gemm<NT>(acc, nst, abase, issue_w, issue_x, am_of);
+  // C element r of lane (j, kh), tile (mi, u): token 32 mi + 8 (r / 4) +
+  // 4 kh + r % 4, row o0 + 32 u
   float* part = g.part + (long long)s * M * H;
   if (wrows) {
 #pragma unroll
-    for (int mi = 0; mi < MT; ++mi) {
+    for (int mi = 0; mi < NT; ++mi) {
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int t = t0 + 16 * mi + 4 * q + r;
+      for (int r = 0; r < 16; ++r) {
+        const int t = t0 + 32 * mi + 8 * (r >> 2) + 4 * kh + (r & 3);
         if (t < M) {
 #pragma unroll
-          for (int rg = 0; rg < 4; ++rg) part[(long long)t * H + o0 + 16u * (uint32_t)rg] = acc[mi][rg][r];
+          for (int u = 0; u < 2; ++u) part[(long long)t * H + o0 + 32u * (uint32_t)u] = acc[mi][u][r];
         }
       }
     }
@@ -397,29 +424,31 @@ __global__ void __launch_bounds__(kDnThreads, 1) k_dg_down(DenseGuardArgs g) {
 // W = fp16(code * absmax), then act[t][i] = fp16(fp16(silu(fp16(g))) *
 // fp16(u)).  The down kernel's scheme with the roles of the operands kept: a
 // workgroup of 4 waves takes 4 consecutive blocks and 16 MT tokens, wave w
-// owns block 4 bq + w, i.e. its 32 gate rows (groups rg = 0, 1: rows
-// 16 rg + n) and its 32 up rows (rg = 2, 3) x all the tile's tokens in
-// 16 MT fp32 accumulators per group (AGPRs); each decoded weight feeds MT
-// MFMAs and every weight is read from HBM once.  The 4 waves share the
-// tile's token rows.  A step covers 64 columns:
-//   - lane (n = l % 16, q = l / 16) loads, for each row group, 8 packed
-//     bytes of its row: bytes 8 q .. + 7 of the step's 32.  Dword j is its B
-//     fragment for MFMA step j, so K slots 8 q .. 8 q + 7 of step j are
-//     columns 16 q + 8 j .. + 7 of the step (the A fragments use the same
-//     order); the absmax of those 16 columns is the entry (64 c + 16 q) / qbs;
+// owns block 4 bq + w, i.e. its 32 gate rows (row tile 0) and its 32 up rows
+// (row tile 1) x all the tile's tokens in 8 MT fp32 accumulators per tile
+// (AGPRs); each decoded weight feeds the MFMAs of all the tile's tokens and
+// every weight is read from HBM once.  The 4 waves share the tile's token
+// rows.  A step covers 64 columns:
+//   - lane (j = l % 32, kh = l / 32) loads, for each row tile, 16 packed
+//     bytes of its row j: bytes 16 kh .. + 15 of the step's 32, the step's
+//     columns 32 kh .. + 31.  Dword s is its B fragment for MFMA step s, so K
+//     slots 8 kh .. 8 kh + 7 of step s are columns 32 kh + 8 s .. + 7 of the
+//     step (the A fragments use the same order); their absmax is the entry
+//     (64 c + 32 kh) / qbs (qbs >= 32);
 //   - the tokens' rows of the 64 columns (128 bytes each) go into an LDS
 //     stage by loads straight into LDS (row r's 16-byte piece p in slot
-//     p ^ ((r / 2) % 8)); the A fragment of token group mi and MFMA step j is
-//     piece 2 q + j of token row 16 mi + n.
+//     p ^ ((r / 2) % 8)); the A fragment of token tile mi and MFMA step s is
+//     piece 4 kh + s of token row 32 mi + j.
 // Gate and up accumulators of the same (token, row) sit in the same lane, so
-// act is formed in registers.  The code-pair table, the step schedule (4
-// units of 2 MT MFMAs) and the register pinning are the down kernel's.
+// act is formed in registers.  The code-pair table, the step schedule and the
+// register pinning are the down kernel's.
 constexpr uint32_t kGuC2 = kDnTab + 2u * kDnStage;  // second-level code books [2][256]
 constexpr uint32_t kGuLds = kGuC2 + 2u * 256u * 4u;
 
 template <bool DQ, int MT>
 __global__ void __launch_bounds__(kDnThreads, 1) k_dg_gu2(DenseGuardArgs g) {
   extern __shared__ __attribute__((aligned(16))) uint8_t gu_lds[];  // no static LDS: gu_lds is LDS address 0
+  constexpr int NT = MT / 2;
   const DecodeArgs& d = g.d;
   const int tid = threadIdx.x, lane = tid & (kWave - 1);
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -450,47 +479,49 @@ __global__ void __launch_bounds__(kDnThreads, 1) k_dg_gu2(DenseGuardArgs g) {
   if (!br.ok && lane == 0) atomicOr(d.status, 1);
   __syncthreads();
 
-  const int n = lane & 15, q = lane >> 4;
+  const int j = lane & 31, kh = lane >> 5;
   const uint32_t rs = (uint32_t)d.gate.row_stride, A = (uint32_t)d.gate.abs_row_stride;
   rsrc_t rw[2], ra[2], r2[2];
 #pragma unroll
-  for (int jj = 0; jj < 2; ++jj) {
-    const ProjView& pv = jj ? d.up : d.gate;
-    const ProjView& hv = jj ? d.host_up : d.host_gate;
-    rw[jj] = make_rsrc((br.dev ? pv.packed : hv.packed) + br.q * pv.blk_stride, br.ok ? (int)(32 * rs) : 0);
+  for (int u = 0; u < 2; ++u) {
+    const ProjView& pv = u ? d.up : d.gate;
+    const ProjView& hv = u ? d.host_up : d.host_gate;
+    // the block is the wave's (blk is uniform): scalar descriptors
+    rw[u] = make_rsrc_uniform((br.dev ? pv.packed : hv.packed) + br.q * pv.blk_stride, br.ok ? (int)(32 * rs) : 0);
     if constexpr (DQ) {
-      ra[jj] = make_rsrc((br.dev ? pv.qabsmax : hv.qabsmax) + br.q * pv.abs_blk_stride, br.ok ? (int)(32 * A) : 0);
-      r2[jj] = make_rsrc(pv.absmax2, br.ok ? (int)((((long long)I * A + (1 << d.dq_shift) - 1) >> d.dq_shift) * 4) : 0);
+      ra[u] = make_rsrc_uniform((br.dev ? pv.qabsmax : hv.qabsmax) + br.q * pv.abs_blk_stride,
+                                br.ok ? (int)(32 * A) : 0);
+      r2[u] = make_rsrc_uniform(pv.absmax2,
+                                br.ok ? (int)((((long long)I * A + (1 << d.dq_shift) - 1) >> d.dq_shift) * 4) : 0);
     } else {
-      ra[jj] = make_rsrc((br.dev ? pv.absmax : hv.absmax) + br.q * pv.abs_blk_stride, br.ok ? (int)(32 * A * 4) : 0);
-      r2[jj] = ra[jj];
+      ra[u] = make_rsrc_uniform((br.dev ? pv.absmax : hv.absmax) + br.q * pv.abs_blk_stride,
+                                br.ok ? (int)(32 * A * 4) : 0);
+      r2[u] = ra[u];
     }
   }
   const rsrc_t rx = make_rsrc(g.x, (int)((long long)M * H * 2));
-  // per-lane parts of the weight and absmax offsets (row 16 (rg % 2) + n);
-  // the row group's part is uniform and goes into the scalar offset
-  const uint32_t wv = (uint32_t)n * rs + 8u * (uint32_t)q;
-  const uint32_t qv = DQ ? ((uint32_t)(n >> 1) * A) * 2u + (uint32_t)(n & 1) : (uint32_t)n * A * 4u;
-  const uint32_t fv = (32u * (uint32_t)blk + (uint32_t)n) * A;  // absmax index of row n, entry 0
+  // per-lane parts of the weight and absmax offsets (row j); double-quantised
+  // u8 absmax codes are stored in row pairs ([row / 2][entry][row % 2])
+  const uint32_t wv = (uint32_t)j * rs + 16u * (uint32_t)kh;
+  const uint32_t qv = DQ ? ((uint32_t)(j >> 1) * A) * 2u + (uint32_t)(j & 1) : (uint32_t)j * A * 4u;
+  const uint32_t fv = (32u * (uint32_t)blk + (uint32_t)j) * A;  // absmax index of row j, entry 0
   auto issue_w = [&](DnW& W, int c) {
     const bool live = c < nst;
     c = c + rot < nst ? c + rot : c + rot - nst;
-    const uint32_t ce = ((uint32_t)(64 * c) + 16u * (uint32_t)q) >> d.qbs_shift;  // the lane's absmax entry
+    const uint32_t ce = ((uint32_t)(64 * c) + 32u * (uint32_t)kh) >> d.qbs_shift;  // the lane's absmax entry
     const uint32_t wo = live ? wv : kOffNone, qo = live ? qv + (DQ ? 2u : 4u) * ce : kOffNone;
     W.ok = br.ok;
 #pragma unroll
-    for (int rg = 0; rg < 4; ++rg) {
-      const int jj = rg >> 1;
-      const uint32_t half = (uint32_t)(rg & 1);
+    for (int u = 0; u < 2; ++u) {
       // temporal loads: a row's 128-byte line serves 4 steps (an
       // nontemporal load fetched it again for each)
-      W.w[rg] = buf_ld8c(rw[jj], wo, 16u * half * rs + 32u * (uint32_t)c);
+      W.w[u] = buf_ld16c(rw[u], wo, 32u * (uint32_t)c);
       if constexpr (DQ) {
-        W.qa[rg] = buf_ldu8c(ra[jj], qo, 16u * half * A);
-        const uint32_t fo = ((fv + 16u * half * A + ce) >> d.dq_shift) * 4u;
-        W.a[rg] = buf_ldfc(r2[jj], live ? fo : kOffNone, 0);
+        W.qa[u] = buf_ldu8c(ra[u], qo, 0);
+        const uint32_t fo = ((fv + ce) >> d.dq_shift) * 4u;
+        W.a[u] = buf_ldfc(r2[u], live ? fo : kOffNone, 0);
       } else {
-        W.a[rg] = buf_ldfc(ra[jj], qo, 16u * half * A * 4u);
+        W.a[u] = buf_ldfc(ra[u], qo, 0);
       }
     }
   };
@@ -511,129 +542,39 @@ __global__ void __launch_bounds__(kDnThreads, 1) k_dg_gu2(DenseGuardArgs g) {
       ld_lds16s(rx, gu_lds + sb + (32 * i + 8 * wave) * 128, xi, 64u * (uint32_t)i * (uint32_t)H);
     }
   };
-
-  float4_t acc[MT][4];
+  auto am_of = [&](const DnW& W, float (&am)[2]) {
 #pragma unroll
-  for (int mi = 0; mi < MT; ++mi)
-#pragma unroll
-    for (int rg = 0; rg < 4; ++rg) {
-      acc[mi][rg] = float4_t{0.0f, 0.0f, 0.0f, 0.0f};
-      asm volatile("" : "+a"(acc[mi][rg]));
-    }
-  uint32_t ad[4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) ad[i] = (uint32_t)(lane & (kDnCopies - 1)) * 8u;
-  // A fragment (token group mi, MFMA step j) of step c: token row 16 mi + n,
-  // piece 2 q + j, in slot piece ^ ((row / 2) % 8)
-  auto read_a = [&](half8_t (&a)[MT / 2], int c, int j, int h) {
-    const uint32_t piece = (uint32_t)(2 * q + j);
-    const uint32_t base = kDnTab + (uint32_t)(c & 1) * kDnStage + (uint32_t)n * 128u +
-                          ((piece ^ (uint32_t)((n >> 1) & 7)) << 4) + (uint32_t)h * 1024u * MT;
-#pragma unroll
-    for (int mi = 0; mi < MT / 2; ++mi) a[mi] = lds_ld_h8(base + (uint32_t)mi * 2048u);
-  };
-  auto am_of = [&](const DnW& W, float (&am)[4]) {
-#pragma unroll
-    for (int rg = 0; rg < 4; ++rg) {
-      float v = W.a[rg];
-      if constexpr (DQ) v = dq_absmax(c2s[(rg >> 1) * 256 + W.qa[rg]], W.a[rg], rg >> 1 ? d.up.offset : d.gate.offset);
-      am[rg] = W.ok ? v : 0.0f;
+    for (int u = 0; u < 2; ++u) {
+      float v = W.a[u];
+      if constexpr (DQ) v = dq_absmax(c2s[u * 256 + W.qa[u]], W.a[u], u ? d.up.offset : d.gate.offset);
+      am[u] = W.ok ? v : 0.0f;
     }
   };
-  auto lookup4 = [&](DnPairs (&pr)[4], const DnW& W, int j) {
+
+  float16_t acc[NT][2];
 #pragma unroll
-    for (int rg = 0; rg < 4; ++rg) pr[rg] = dn_lookup4(j == 0 ? W.w[rg].x : W.w[rg].y, ad);
-  };
-  auto finish4 = [&](half8_t (&b)[4], const DnPairs (&pr)[4], const float (&am)[4]) {
+  for (int mi = 0; mi < NT; ++mi)
 #pragma unroll
-    for (int rg = 0; rg < 4; ++rg) b[rg] = dn_finish8(pr[rg], am[rg]);
-  };
-  auto mfma_unit = [&](const half8_t (&a)[MT / 2], const half8_t (&b)[4], int h) {
+    for (int u = 0; u < 2; ++u) {
 #pragma unroll
-    for (int rg = 0; rg < 4; ++rg)
-#pragma unroll
-      for (int mi = 0; mi < MT / 2; ++mi) acc[MT / 2 * h + mi][rg] = mfma16(a[mi], b[rg], acc[MT / 2 * h + mi][rg]);
-#pragma unroll
-    for (int i = 0; i < 2 * MT; ++i) {
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);
+      for (int r = 0; r < 16; ++r) acc[mi][u][r] = 0.0f;
+      asm volatile("" : "+a"(acc[mi][u]));
     }
-    __builtin_amdgcn_sched_barrier(0);
-  };
-  auto step_sync = [] {
-    __builtin_amdgcn_s_waitcnt(0);  // vmcnt(0) expcnt(0) lgkmcnt(0)
-    __builtin_amdgcn_s_barrier();
-    asm volatile("" ::: "memory");
-  };
-
-  // the down kernel's step schedule: 4 units (MFMA step j, token half h) of
-  // 2 MT MFMAs, three weight register sets (decoded, arrived, in flight)
-  // moved down one set at the end of a step, step c + 2's weights issued in
-  // unit (0, 1) and its token rows after the barrier of the last unit
-  DnW W0, W1, W2;
-  half8_t ax[MT / 2], ay[MT / 2], b0[4], b1[4];
-  DnPairs pr[4];
-  float am_c[4], am_n[4];
-  issue_w(W0, 0);
-  issue_x(0);
-  issue_w(W1, 1);
-  issue_x(1);
-  __builtin_amdgcn_s_waitcnt(0);
-  __builtin_amdgcn_s_barrier();  // step 0's token rows are in LDS (and step 1's)
-  asm volatile("" ::: "memory");
-  am_of(W0, am_c);
-  read_a(ax, 0, 0, 0);
-  lookup4(pr, W0, 0);
-  finish4(b0, pr, am_c);
-  __builtin_amdgcn_sched_barrier(0);
-
-  auto step = [&](int c, const DnW& Wc, const DnW& Wn, DnW& Wf) {
-    read_a(ay, c, 0, 1);
-    lookup4(pr, Wc, 1);
-    mfma_unit(ax, b0, 0);
-    issue_w(Wf, c + 2);
-    read_a(ax, c, 1, 0);
-    finish4(b1, pr, am_c);
-    mfma_unit(ay, b0, 1);
-    read_a(ay, c, 1, 1);
-    am_of(Wn, am_n);
-    lookup4(pr, Wn, 0);
-    mfma_unit(ax, b1, 0);
-    step_sync();
-    issue_x(c + 2);
-    read_a(ax, c + 1, 0, 0);
-    finish4(b0, pr, am_n);
-    mfma_unit(ay, b1, 1);
+  const uint32_t abase = kDnTab + (uint32_t)j * 128u + ((4u * (uint32_t)kh ^ (uint32_t)((j >> 1) & 7)) << 4);
+  dn_gemm<NT>(acc, nst, abase, issue_w, issue_x, am_of);
+  // act = fp16(fp16(silu(fp16(g))) * fp16(u)) for (token, row): C element r
+  // of lane (j, kh) is row j of its tile for token 32 mi + 8 (r / 4) + 4 kh +
+  // r % 4
 #pragma unroll
-    for (int rg = 0; rg < 4; ++rg) am_c[rg] = am_n[rg];
+  for (int mi = 0; mi < NT; ++mi) {
 #pragma unroll
-    for (int mi = 0; mi < MT; ++mi)
-#pragma unroll
-      for (int rg = 0; rg < 4; ++rg) asm volatile("" : "+a"(acc[mi][rg]));
-  };
-  for (int c = 0; c < nst; ++c) {
-    step(c, W0, W1, W2);
-    W0 = W1;
-    W1 = W2;
-  }
-  __builtin_amdgcn_s_waitcnt(0);
-  mfma_drain();
-  // act = fp16(fp16(silu(fp16(g))) * fp16(u)) for (token, row): C lane (n, q)
-  // holds row n of its group for tokens 16 mi + 4 q + r
-#pragma unroll
-  for (int mi = 0; mi < MT; ++mi) {
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int t = t0 + 16 * mi + 4 * q + r;
+    for (int r = 0; r < 16; ++r) {
+      const int t = t0 + 32 * mi + 8 * (r >> 2) + 4 * kh + (r & 3);
       if (t < M) {
-#pragma unroll
-        for (int rg = 0; rg < 2; ++rg) {
-          const float g16 = h2f(f2h(acc[mi][rg][r]));
-          const float s16 = h2f(f2h(g16 / (1.0f + expf(-g16))));
-          const float u16 = h2f(f2h(acc[mi][rg + 2][r]));
-          g.act[(long long)t * I + 32 * blk + 16 * rg + n] = f2h(s16 * u16);
-        }
+        const float g16 = h2f(f2h(acc[mi][0][r]));
+        const float s16 = h2f(f2h(g16 / (1.0f + expf(-g16))));
+        const float u16 = h2f(f2h(acc[mi][1][r]));
+        g.act[(long long)t * I + 32 * blk + j] = f2h(s16 * u16);
       }
     }
   }

@@ -342,13 +342,24 @@ __device__ __forceinline__ float4_t mfma16(half8_t a, half8_t b, float4_t c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
 }
 
+// v_mfma_f32_32x32x16_f16 lane layout (measured with one-hot operands):
+// A[i][k] and B[k][j] in lane l hold i (or j) = l % 32, k = 8 (l / 32) +
+// 0..7; C[i][j] in lane l holds j = l % 32, element r = 0..15 holding
+// i = 8 (r / 4) + 4 (l / 32) + r % 4.
+typedef float float16_t __attribute__((ext_vector_type(16)));
+
+__device__ __forceinline__ float16_t mfma32(half8_t a, half8_t b, float16_t c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+}
+
 // Wait states between MFMAs and VALU reads of their results, beyond what the
 // compiler inserts: reads of a 16x16x32 result that follow its MFMA closely
 // have returned values that changed from run to run in the last elements
-// (written last), so MFMA results are read only after this drain.
+// (written last), so MFMA results are read only after this drain (long
+// enough for the 32x32x16 shape's 16 passes too).
 __device__ __forceinline__ void mfma_drain() {
   __builtin_amdgcn_sched_barrier(0);
-  asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory");
+  asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory");
   __builtin_amdgcn_sched_barrier(0);
 }
 
@@ -400,6 +411,17 @@ constexpr int kNontemporal = 2;
 
 __device__ __forceinline__ rsrc_t make_rsrc(const void* base, int bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, bytes, kRsrcWord3);
+}
+// Descriptor of a range that is the same in every lane of the wave, built in
+// scalar registers: the compiler cannot always tell that a value derived
+// from a global load is uniform, and a descriptor in vector registers turns
+// every load through it into a loop over the lanes' values.
+__device__ __forceinline__ rsrc_t make_rsrc_uniform(const void* base, int bytes) {
+  const unsigned long long v = reinterpret_cast<unsigned long long>(base);
+  const unsigned lo = (unsigned)__builtin_amdgcn_readfirstlane((int)(unsigned)v);
+  const unsigned hi = (unsigned)__builtin_amdgcn_readfirstlane((int)(unsigned)(v >> 32));
+  return make_rsrc(reinterpret_cast<const void*>(((unsigned long long)hi << 32) | lo),
+                   __builtin_amdgcn_readfirstlane(bytes));
 }
 __device__ __forceinline__ uint4 buf_ld16(rsrc_t r, uint32_t voff, uint32_t soff) {
   const u32x4_t t = __builtin_amdgcn_raw_buffer_load_b128(r, (int)voff, (int)soff, kNontemporal);
