@@ -1,6 +1,6 @@
 // Dense-guard prefill MLP (RT:5775-5831, _dense_guard_mlp_forward_exact_chunked_4bit):
 // every intermediate block for every token, read from the slot table, as
-// full-width GEMMs on v_mfma_f32_16x16x32_f16 with fp32 accumulation.  The
+// full-width GEMMs on v_mfma_f32_32x32x16_f16 with fp32 accumulation.  The
 // reference dequantises each NF4 projection to an fp16 weight and runs
 // F.linear three times; the rounding points kept here are its own:
 //
@@ -31,14 +31,11 @@
 // to run.
 #include <mutex>
 
-#include "nsmlp_internal.h"
+#include "nsmlp_regdecode.h"
 
 namespace nsmlp {
 
 namespace {
-
-typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
-typedef float float2_t __attribute__((ext_vector_type(2)));
 
 // ------------------------------------------------------------- down GEMM --
 // part[s][t][o] = sum over the blocks of range s of act[t][i] * Wd[o][i],
@@ -65,60 +62,19 @@ typedef float float2_t __attribute__((ext_vector_type(2)));
 // 32-cycle 32x32x16 MFMA leaves issue room for the decode between MFMAs
 // (measured on this GPU at one wave per SIMD with independent MFMAs: 94% of
 // the MFMA cycles busy with two VALU ops per MFMA and 91% with four, against
-// 43-81% for the 16-cycle 16x16x32 shape with one or two; the decode here is
-// about two VALU ops per MFMA), and every LDS read is issued a unit of MFMAs
-// before its use (see the step schedule below).
+// 43-81% for the 16-cycle 16x16x32 shape with one or two; here about three
+// VALU ops per MFMA, address arithmetic included), and every LDS read is
+// issued a unit of MFMAs before its use (see the step schedule below).
 constexpr int kDnThreads = 256;
 constexpr int kDnTok = 256;                            // tokens per tile
 constexpr int kDnRows = 256;                           // output rows per workgroup (64 per wave)
-constexpr int kDnCopies = 32;                          // code-pair table copies (lane % 32)
-constexpr uint32_t kDnTab = 256u * kDnCopies * 8u;     // 64 KB at LDS address 0
+constexpr int kDnCopies = kRdCopies;                   // code-pair table copies (lane % 32)
+constexpr uint32_t kDnTab = kRdTab;                    // 64 KB at LDS address 0
 constexpr uint32_t kDnStage = kDnTok * 128u;           // 256 rows x 64 fp16
 constexpr uint32_t kDnC2 = kDnTab + 2u * kDnStage;     // second-level code book [256]
 constexpr uint32_t kDnRefs = kDnC2 + 256u * 4u;        // block references of the range
 constexpr int kDnRefHost = 1 << 30;                    // reference bit: host copy
 constexpr uint32_t kDnLdsMax = 160u * 1024u;
-
-typedef float dn_f2_t __attribute__((ext_vector_type(2)));
-typedef const __attribute__((address_space(3))) dn_f2_t* lds_f2_ptr;
-typedef const __attribute__((address_space(3))) half8_t* lds_h8_ptr;
-__device__ __forceinline__ dn_f2_t lds_ld_f2(uint32_t byte_addr) {
-  return *reinterpret_cast<lds_f2_ptr>(static_cast<uintptr_t>(byte_addr));
-}
-__device__ __forceinline__ half8_t lds_ld_h8(uint32_t byte_addr) {
-  return *reinterpret_cast<lds_h8_ptr>(static_cast<uintptr_t>(byte_addr));
-}
-
-// 8 NF4 codes (one packed dword, even element in the high nibble) ->
-// 8 fp16(code * am) in element order, in two halves so that the table
-// lookups can go out a unit ahead of their use: dn_lookup4 reads the four
-// code pairs, dn_finish8 scales them and rounds to fp16.  ad[i] holds this
-// lane's copy offset (copy * 8) in its low byte; the packed byte goes into
-// bits 8..15.
-struct DnPairs {
-  dn_f2_t p[4];
-};
-__device__ __forceinline__ DnPairs dn_lookup4(uint32_t v, uint32_t (&ad)[4]) {
-  NSMLP_SET_BYTE1(ad[0], v, "BYTE_0");
-  NSMLP_SET_BYTE1(ad[1], v, "BYTE_1");
-  NSMLP_SET_BYTE1(ad[2], v, "BYTE_2");
-  NSMLP_SET_BYTE1(ad[3], v, "BYTE_3");
-  return DnPairs{{lds_ld_f2(ad[0]), lds_ld_f2(ad[1]), lds_ld_f2(ad[2]), lds_ld_f2(ad[3])}};
-}
-__device__ __forceinline__ half8_t dn_finish8(const DnPairs& pr, float am) {
-  uint32_t o[4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const float2_t w = {pr.p[i].x * am, pr.p[i].y * am};
-    o[i] = __builtin_bit_cast(uint32_t, __builtin_convertvector(w, half2_t));
-  }
-  return as_h8(make_uint4(o[0], o[1], o[2], o[3]));
-}
-// dword s (a constant) of a 16-byte weight load
-template <int s>
-__device__ __forceinline__ uint32_t dn_word(const uint4& w) {
-  return s == 0 ? w.x : s == 1 ? w.y : s == 2 ? w.z : w.w;
-}
 
 // Bytes spanned by the packed rows (abs = false, 16 bytes per row and block)
 // or the absmax entries (elem bytes each) of `blocks` slots of a down view.
@@ -127,15 +83,6 @@ __host__ __device__ inline long long dn_extent(const ProjView& v, int blocks, in
   const long long bs = abs ? v.abs_blk_stride : v.blk_stride, rs = abs ? v.abs_row_stride : v.row_stride;
   return abs ? ((blocks - 1) * bs + (long long)(H - 1) * rs + 1) * elem : (blocks - 1) * bs + (long long)(H - 1) * rs + elem;
 }
-
-// One step's weight loads: 16 packed bytes per 32-row tile and their absmax
-// (u8 code + second-level scale, or fp32).
-struct DnW {
-  uint4 w[2];
-  uint32_t qa[2];
-  float a[2];
-  int ok;  // the lane's block is valid (its absmax is forced to zero otherwise)
-};
 
 // The step schedule both GEMMs share: 4 units (MFMA step s = 0..3) of 16
 // MFMAs (8 token tiles x 2 row tiles); unit s runs MFMA step s while it reads
@@ -163,13 +110,13 @@ __device__ __forceinline__ void dn_gemm(float16_t (&acc)[NT][2], int nst, uint32
 #pragma unroll
     for (int mi = 0; mi < NT; ++mi) a[mi] = lds_ld_h8(base + (uint32_t)mi * 4096u);
   };
-  auto lookup2 = [&](DnPairs (&pr)[2], const DnW& W, auto s) {
+  auto lookup2 = [&](RdPairs (&pr)[2], const RdW& W, auto s) {
 #pragma unroll
-    for (int u = 0; u < 2; ++u) pr[u] = dn_lookup4(dn_word<decltype(s)::value>(W.w[u]), ad);
+    for (int u = 0; u < 2; ++u) pr[u] = rd_lookup4(rd_word<decltype(s)::value>(W.w[u]), ad);
   };
-  auto finish2 = [&](half8_t (&b)[2], const DnPairs (&pr)[2], const float (&am)[2]) {
+  auto finish2 = [&](half8_t (&b)[2], const RdPairs (&pr)[2], const float (&am)[2]) {
 #pragma unroll
-    for (int u = 0; u < 2; ++u) b[u] = dn_finish8(pr[u], am[u]);
+    for (int u = 0; u < 2; ++u) b[u] = rd_finish8(pr[u], am[u]);
   };
   // 2 NT MFMAs, each followed by an LDS read and two VALU ops of the work
   // ahead
@@ -196,9 +143,9 @@ __device__ __forceinline__ void dn_gemm(float16_t (&acc)[NT][2], int nst, uint32
   using S2 = std::integral_constant<int, 2>;
   using S3 = std::integral_constant<int, 3>;
 
-  DnW W0, W1, W2;
+  RdW W0, W1, W2;
   half8_t a0[NT], a1[NT], b0[2], b1[2];
-  DnPairs p0[2], p1[2];
+  RdPairs p0[2], p1[2];
   float am_c[2], am_n[2];
   issue_w(W0, 0);
   issue_x(0);
@@ -214,7 +161,7 @@ __device__ __forceinline__ void dn_gemm(float16_t (&acc)[NT][2], int nst, uint32
   lookup2(p1, W0, S1{});
   __builtin_amdgcn_sched_barrier(0);
 
-  auto step = [&](int c, const DnW& Wc, const DnW& Wn, DnW& Wf) {
+  auto step = [&](int c, const RdW& Wc, const RdW& Wn, RdW& Wf) {
     // unit 0: B of MFMA step 1 finished, step 2's looked up
     issue_w(Wf, c + 2);
     read_a(a1, c, 1);
@@ -280,15 +227,7 @@ __global__ void __launch_bounds__(kDnThreads, 1) k_dg_down(DenseGuardArgs g) {
   float* c2s = reinterpret_cast<float*>(dn_lds + kDnC2);
   int32_t* refs = reinterpret_cast<int32_t*>(dn_lds + kDnRefs);
 
-  // code-pair table: thread e writes the 32 copies of entry e (code[e >> 4],
-  // code[e & 15]), 256 contiguous bytes
-  {
-    const float hi = d.code_down[tid >> 4], lo = d.code_down[tid & 15];
-    uint4* dst = reinterpret_cast<uint4*>(dn_lds + tid * 256);
-    const uint4 v = make_uint4(__float_as_uint(hi), __float_as_uint(lo), __float_as_uint(hi), __float_as_uint(lo));
-#pragma unroll
-    for (int i = 0; i < 16; ++i) dst[i] = v;
-  }
+  rd_table_fill(dn_lds, d.code_down, tid);
   if constexpr (DQ) c2s[tid] = d.down.code2[tid];
   // block references: slot, or the block id with kDnRefHost for a host copy,
   // or -1 (out of the table, or no tokens when the block lists are given)
@@ -327,7 +266,7 @@ __global__ void __launch_bounds__(kDnThreads, 1) k_dg_down(DenseGuardArgs g) {
   // step into blocks the scheduler and the register allocator see
   // separately).
   const bool wrows = (int)(rt * kDnRows + wave * 64) < H;
-  auto issue_w = [&](DnW& W, int c) {
+  auto issue_w = [&](RdW& W, int c) {
     const int cc = max(0, min(c, nst - 1));  // clamped: the reference read stays in the range
     const int enc = refs[2 * cc + kh];
     const bool ok = (c < nst) & (enc >= 0) & wrows;
@@ -377,7 +316,7 @@ __global__ void __launch_bounds__(kDnThreads, 1) k_dg_down(DenseGuardArgs g) {
       ld_lds16s(rx, dn_lds + sb + (32 * i + 8 * wave) * 128, xi, 64u * (uint32_t)i * (uint32_t)I);
     }
   };
-  auto am_of = [&](const DnW& W, float (&am)[2]) {
+  auto am_of = [&](const RdW& W, float (&am)[2]) {
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
       float v = W.a[u];
@@ -462,15 +401,7 @@ __global__ void __launch_bounds__(kDnThreads, 1) k_dg_gu2(DenseGuardArgs g) {
   const int rot = (int)(((long long)((blockIdx.x >> 3) & 15) * nst) >> 4);
   float* c2s = reinterpret_cast<float*>(gu_lds + kGuC2);
 
-  // code-pair table: thread e writes the 32 copies of entry e (code[e >> 4],
-  // code[e & 15]), 256 contiguous bytes
-  {
-    const float hi = d.code[tid >> 4], lo = d.code[tid & 15];
-    uint4* dst = reinterpret_cast<uint4*>(gu_lds + tid * 256);
-    const uint4 v = make_uint4(__float_as_uint(hi), __float_as_uint(lo), __float_as_uint(hi), __float_as_uint(lo));
-#pragma unroll
-    for (int i = 0; i < 16; ++i) dst[i] = v;
-  }
+  rd_table_fill(gu_lds, d.code, tid);
   if constexpr (DQ) {
     c2s[tid] = d.gate.code2[tid];
     c2s[256 + tid] = d.up.code2[tid];
@@ -505,7 +436,7 @@ __global__ void __launch_bounds__(kDnThreads, 1) k_dg_gu2(DenseGuardArgs g) {
   const uint32_t wv = (uint32_t)j * rs + 16u * (uint32_t)kh;
   const uint32_t qv = DQ ? ((uint32_t)(j >> 1) * A) * 2u + (uint32_t)(j & 1) : (uint32_t)j * A * 4u;
   const uint32_t fv = (32u * (uint32_t)blk + (uint32_t)j) * A;  // absmax index of row j, entry 0
-  auto issue_w = [&](DnW& W, int c) {
+  auto issue_w = [&](RdW& W, int c) {
     const bool live = c < nst;
     c = c + rot < nst ? c + rot : c + rot - nst;
     const uint32_t ce = ((uint32_t)(64 * c) + 32u * (uint32_t)kh) >> d.qbs_shift;  // the lane's absmax entry
@@ -542,7 +473,7 @@ __global__ void __launch_bounds__(kDnThreads, 1) k_dg_gu2(DenseGuardArgs g) {
       ld_lds16s(rx, gu_lds + sb + (32 * i + 8 * wave) * 128, xi, 64u * (uint32_t)i * (uint32_t)H);
     }
   };
-  auto am_of = [&](const DnW& W, float (&am)[2]) {
+  auto am_of = [&](const RdW& W, float (&am)[2]) {
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
       float v = W.a[u];

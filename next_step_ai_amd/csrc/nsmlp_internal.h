@@ -786,6 +786,7 @@ struct PrefillArgs {
   int S;
 };
 void launch_prefill(const PrefillArgs& p, hipStream_t s);
+int prefill_gu_check();  // NSMLP_OK, or the error (static LDS in the gate/up kernel)
 
 // Dense-guard prefill MLP: every block for every token (M tokens) over a slot
 // table, as staged GEMMs on MFMA.  H % 256 == 0, NB % 4 == 0.
