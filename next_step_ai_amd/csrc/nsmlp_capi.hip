@@ -236,7 +236,7 @@ DecodeWs decode_ws_layout(int H, int k) {
 }
 
 struct RouteWs {
-  size_t lat16, scores, lat_part, lat_p64, lat_p32, lat_und, lat_und_n, total;
+  size_t lat16, scores, lat_part, lat_p64, lat_p32, lat_und, lat_und_n, lat_m, sc_und, sc_und_n, total;
 };
 
 RouteWs route_ws_layout(size_t base, int rows, int H, int R, int NB) {
@@ -248,7 +248,7 @@ RouteWs route_ws_layout(size_t base, int rows, int H, int R, int NB) {
   off += align_up((size_t)rows * NB * sizeof(uint16_t));
   w.lat_part = off;
   if (rows < kLatSplitRows) off += align_up((size_t)rows * R * kLatParts * 3 * sizeof(double));
-  w.lat_p64 = w.lat_p32 = w.lat_und = w.lat_und_n = off;
+  w.lat_p64 = w.lat_p32 = w.lat_und = w.lat_und_n = w.lat_m = w.sc_und = w.sc_und_n = off;
   if (rows >= kLatSplitRows) {
     const size_t n = (size_t)rows * R, P = (size_t)latent_mf_parts(rows, R, H);
     w.lat_p64 = off;
@@ -258,6 +258,12 @@ RouteWs route_ws_layout(size_t base, int rows, int H, int R, int NB) {
     w.lat_und = off;
     off += align_up(n * sizeof(int));
     w.lat_und_n = off;
+    off += align_up(sizeof(int));
+    w.lat_m = off;
+    off += align_up(n * sizeof(uint16_t));
+    w.sc_und = off;
+    off += align_up((size_t)rows * NB * sizeof(int));
+    w.sc_und_n = off;
     off += align_up(sizeof(int));
   }
   w.total = off;
@@ -385,6 +391,9 @@ int fill_route(RouteArgs& r, const void* x, int rows, int H, const void* enc_w, 
   r.lat_und = mf ? (int*)(base + L.lat_und) : nullptr;
   r.lat_und_n = mf ? (int*)(base + L.lat_und_n) : nullptr;
   r.lat_nparts = mf ? latent_mf_parts(rows, R, H) : 0;
+  r.lat_m = mf ? (uint16_t*)(base + L.lat_m) : nullptr;
+  r.sc_und = mf ? (int*)(base + L.sc_und) : nullptr;
+  r.sc_und_n = mf ? (int*)(base + L.sc_und_n) : nullptr;
   r.clear_words = nullptr;
   return NSMLP_OK;
 }

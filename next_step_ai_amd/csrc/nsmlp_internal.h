@@ -915,6 +915,12 @@ struct RouteArgs {
   int* lat_und;
   int* lat_und_n;
   int lat_nparts;
+  // kLatSplitRows rows or more: the scores on the matrix cores (16-byte
+  // score_w rows): the latent with the basis_top_k mask ([rows][R] fp16),
+  // the undecided scores [rows NB] and their count; nullptr otherwise
+  uint16_t* lat_m;
+  int* sc_und;
+  int* sc_und_n;
 };
 constexpr int kClearWords = 8;
 constexpr int kLatSplitRows = 8;

@@ -35,6 +35,7 @@ __global__ void __launch_bounds__(kLatThreads) k_latent(RouteArgs a) {
   const int r = blockIdx.x;    // latent row
   const int row = blockIdx.y;  // token
   const int tid = threadIdx.x;
+  if (r == 0 && row == 0 && tid == 0 && a.sc_und_n != nullptr) *a.sc_und_n = 0;  // k_scores_mf appends after it
   const uint16_t* __restrict__ x = a.x + (long long)row * a.H;
   const uint16_t* __restrict__ w = a.enc_w + (long long)r * a.H;
   // the bias goes out with the first loads (an unconditional load: x[0]
@@ -107,7 +108,10 @@ __global__ void __launch_bounds__(kMfThreads) k_latent_mf(RouteArgs a) {
   const int RT = (a.R + 15) / 16;
   const int tile = (int)blockIdx.x, p = (int)blockIdx.y, P = (int)gridDim.y;
   const int r0 = (tile % RT) * 16, t0 = (tile / RT) * 16;
-  if (tile == 0 && p == 0 && tid == 0) *a.lat_und_n = 0;  // k_latent_mfin appends after this kernel
+  if (tile == 0 && p == 0 && tid == 0) {
+    *a.lat_und_n = 0;  // k_latent_mfin appends after this kernel
+    if (a.sc_und_n != nullptr) *a.sc_und_n = 0;  // and k_scores_mf after that
+  }
   const int i = lane & 15, g = lane >> 4;
   const int nt = min(16, a.rows - t0), nr = min(16, a.R - r0);
   // descriptors over the tile's rows only (every offset below fits 32 bits)
@@ -452,7 +456,170 @@ __global__ void __launch_bounds__(kScoreThreads) k_scores(RouteArgs a) {
   }
 }
 
+// From kLatSplitRows tokens on (16-byte score_w rows), the scores on the
+// matrix cores, as the latent's first pass: with a basis_top_k mask (or a
+// latent_out to write) k_scores_prep first writes the latent as scored;
+// k_scores_mf sums each 16-token x 16-block tile in fp64
+// (v_mfma_f64_16x16x4_f64, every term exact) with the terms' magnitudes in
+// fp32 beside it, and where the error interval of sum + bias rounds to one
+// fp16 value (the bound of k_latent_mfin, over R terms) that value is the
+// score; the others (one in 425984 at the 405B shape and 256 tokens) go to a
+// list that k_scores_fix sums exactly (Exact3), one output per wave.  Either
+// way the score equals k_scores' bit for bit.  The latent kernels clear the
+// list's count.
+constexpr int kSmThreads = 256;  // 4 waves, one tile each
+constexpr int kSfThreads = 256, kSfGroups = 16;
+
+__device__ __forceinline__ void score_store(const RouteArgs& a, long long o, int j, uint16_t sc) {
+  if (!a.legacy_abs && (sc & 0x8000u)) sc = 0;               // clamp_min(0) (RT:4331)
+  if (a.dbn != nullptr) sc = f2h(h2f(sc) * h2f(a.dbn[j]));  // fp16 x fp16 is exact in fp32
+  a.scores[o] = sc;
+  if (a.scores_out != nullptr) a.scores_out[o] = sc;
+}
+
+// One wave per token: the basis_top_k mask over |latent| (ties keep the lower
+// index, as k_scores), latent_out, and the latent as scored.
+__global__ void __launch_bounds__(kWave) k_scores_prep(RouteArgs a) {
+  const int row = (int)blockIdx.x, lane = threadIdx.x;
+  const uint16_t* lt = a.lat16 + (long long)row * a.R;
+  const int btk = a.basis_top_k < 1 ? 1 : (a.basis_top_k > a.R ? a.R : a.basis_top_k);
+  for (int r = lane; r < a.R; r += kWave) {
+    uint16_t v = lt[r];
+    if (btk < a.R) {
+      const uint32_t kr = f16_order_key((uint16_t)(v & 0x7FFFu));
+      int rank = 0;
+      for (int q = 0; q < a.R; ++q) {
+        const uint32_t kq = f16_order_key((uint16_t)(lt[q] & 0x7FFFu));
+        rank += (kq > kr) || (kq == kr && q < r);
+      }
+      if (rank >= btk) v = (uint16_t)(v & 0x8000u);
+    }
+    if (a.latent_out != nullptr) a.latent_out[(long long)row * a.R + r] = v;
+    a.lat_m[(long long)row * a.R + r] = v;
+  }
+}
+
+// Wave w of workgroup g takes tile 4 g + w (16 tokens x 16 blocks), reading
+// the latent as scored from a.lat_m (the prepared copy, or the latent itself
+// when nothing is masked; |latent| is taken here for legacy_abs).  Lane l
+// (i = l % 16, g4 = l / 16) holds, per 64 basis terms, terms 16 g4 .. + 15 of
+// token t0 + i's scored latent and of block b0 + i's score_w row (two
+// 16-byte loads each; R % 8 == 0, so a load's 8 terms are all inside R or all
+// past it); K slot g4 of MFMA step s is term 16 g4 + s.
+__global__ void __launch_bounds__(kSmThreads) k_scores_mf(RouteArgs a) {
+  const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
+  const int BT = (a.NB + 15) / 16, TT = (a.rows + 15) / 16;
+  const int tile = 4 * (int)blockIdx.x + wave;
+  if (tile >= BT * TT) return;  // whole waves; no barrier below
+  const int t0 = (tile / BT) * 16, b0 = (tile % BT) * 16;
+  const int i = lane & 15, g4 = lane >> 4;
+  const int nt = min(16, a.rows - t0), nb = min(16, a.NB - b0);
+  const rsrc_t rx = make_rsrc(a.lat_m + (long long)t0 * a.R, nt * a.R * 2);
+  const rsrc_t rw = make_rsrc(a.score_w + (long long)b0 * a.R, nb * a.R * 2);
+  const uint32_t xo = i < nt ? (uint32_t)(i * a.R) * 2u : kOffNone;
+  const uint32_t wo = i < nb ? (uint32_t)(i * a.R) * 2u : kOffNone;
+  typedef double d4 __attribute__((ext_vector_type(4)));
+  typedef float f4 __attribute__((ext_vector_type(4)));
+  d4 acc = {0.0, 0.0, 0.0, 0.0}, acc1 = {0.0, 0.0, 0.0, 0.0};
+  f4 mag = {0.0f, 0.0f, 0.0f, 0.0f};
+  for (int c0 = 0; c0 < a.R; c0 += 64) {
+    uint4 xv[2], wv[2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int c = c0 + 16 * g4 + 8 * h;
+      const bool in = c < a.R;
+      xv[h] = buf_ld16c(rx, in ? xo : kOffNone, (uint32_t)c * 2u);
+      wv[h] = buf_ld16c(rw, in ? wo : kOffNone, (uint32_t)c * 2u);
+      if (a.legacy_abs) xv[h] = make_uint4(xv[h].x & 0x7FFF7FFFu, xv[h].y & 0x7FFF7FFFu, xv[h].z & 0x7FFF7FFFu,
+                                           xv[h].w & 0x7FFF7FFFu);
+    }
+#pragma unroll
+    for (int s = 0; s < 16; ++s) {
+      const uint32_t xw = s < 8 ? (&xv[0].x)[s >> 1] : (&xv[1].x)[(s - 8) >> 1];
+      const uint32_t ww = s < 8 ? (&wv[0].x)[s >> 1] : (&wv[1].x)[(s - 8) >> 1];
+      const float xf = h2f((uint16_t)(xw >> (16 * (s & 1))));
+      const float wf = h2f((uint16_t)(ww >> (16 * (s & 1))));
+      if (s & 1)
+        acc1 = __builtin_amdgcn_mfma_f64_16x16x4f64((double)xf, (double)wf, acc1, 0, 0, 0);
+      else
+        acc = __builtin_amdgcn_mfma_f64_16x16x4f64((double)xf, (double)wf, acc, 0, 0, 0);
+      mag = __builtin_amdgcn_mfma_f32_16x16x4f32(fabsf(xf), fabsf(wf), mag, 0, 0, 0);
+    }
+  }
+  mfma_drain();
+  acc += acc1;
+  // C layouts (measured): f64 lane L element q = (token 4 q + L / 16, block
+  // L % 16); f32 lane L element q = (token 4 (L / 16) + q, block L % 16): the
+  // magnitudes go through LDS into the f64 layout
+  __shared__ float mg[4][256];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) mg[wave][(4 * g4 + q) * 16 + i] = mag[q];
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+  const bool has_b = !a.legacy_abs && a.score_b != nullptr;
+  const int j = b0 + i;
+  const double bias = has_b && i < nb ? (double)h2f(a.score_b[j]) : 0.0;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const int tt = 4 * q + g4;
+    if (tt < nt && i < nb) {
+      const float b = mg[wave][tt * 16 + i];
+      const double sb = acc[q] + bias;
+      // (R + 64) 2^-53 (2 b): the sums' roundings (at most one per term, the
+      // two chains' addition; 2 b > sum|t|); 2^-49 (|sb| + |bias|): the bias
+      // add and the interval ends' own rounding
+      const double B = (double)(a.R + 64) * 1.1102230246251565e-16 * (2.0 * (double)b) +
+                       1.7763568394002505e-15 * (fabs(sb) + fabs(bias));
+      const uint16_t lo = exact_to_f16(Exact3{sb - B, 0.0, 0.0});
+      const uint16_t hi = exact_to_f16(Exact3{sb + B, 0.0, 0.0});
+      const long long o = (long long)(t0 + tt) * a.NB + j;
+      if (b < 3.0e38f && fabs(sb) < 1.0e300 && lo == hi) {  // false for inf and nan
+        score_store(a, o, j, lo);
+      } else {
+        const int slot = atomicAdd(a.sc_und_n, 1);
+        a.sc_und[slot] = (int)o;
+      }
+    }
+  }
+}
+
+// The undecided scores, exactly: wave g of the grid takes list entries g,
+// g + G, ...; lane l sums terms l, l + 64, ... of its entry (Exact3 parts add
+// exactly across lanes).
+__global__ void __launch_bounds__(kSfThreads) k_scores_fix(RouteArgs a) {
+  const int cnt = *a.sc_und_n;
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wv = (int)(blockIdx.x * (kSfThreads / kWave) + threadIdx.x / kWave), nw = (int)gridDim.x * (kSfThreads / kWave);
+  const bool has_b = !a.legacy_abs && a.score_b != nullptr;
+  const uint16_t amask = a.legacy_abs ? 0x7FFFu : 0xFFFFu;
+  for (int e = wv; e < cnt; e += nw) {
+    const int o = a.sc_und[e];
+    const int t = o / a.NB, j = o % a.NB;
+    const uint16_t* lt = a.lat_m + (long long)t * a.R;
+    const uint16_t* w = a.score_w + (long long)j * a.R;
+    Exact3 acc = exact_zero();
+    for (int r = lane; r < a.R; r += kWave) exact_add(acc, (double)(h2f((uint16_t)(lt[r] & amask)) * h2f(w[r])));
+    acc = wave_sum_exact(acc);
+    if (lane == 0) {
+      if (has_b) exact_add(acc, (double)h2f(a.score_b[j]));
+      score_store(a, o, j, exact_to_f16(acc));
+    }
+  }
+}
+
 void launch_scores(const RouteArgs& a, hipStream_t s) {
+  if (a.sc_und != nullptr && a.svec) {
+    RouteArgs b = a;
+    if (a.basis_top_k < a.R || a.latent_out != nullptr)
+      hipLaunchKernelGGL(k_scores_prep, dim3(a.rows), dim3(kWave), 0, s, a);
+    else
+      b.lat_m = a.lat16;  // nothing masked: the scores read the latent itself
+    const long long tiles = (long long)((a.NB + 15) / 16) * ((a.rows + 15) / 16);
+    hipLaunchKernelGGL(k_scores_mf, dim3((unsigned)((tiles + 3) / 4)), dim3(kSmThreads), 0, s, b);
+    hipLaunchKernelGGL(k_scores_fix, dim3(kSfGroups), dim3(kSfThreads), 0, s, b);
+    return;
+  }
   const int tpw = scores_tokens_per_wg(a.rows, a.R);
   const dim3 g((a.NB + kScoresPerWg - 1) / kScoresPerWg, (a.rows + tpw - 1) / tpw);
   const size_t lds = (size_t)a.R * tpw * sizeof(uint16_t);

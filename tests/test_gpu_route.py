@@ -250,3 +250,41 @@ def test_route_tiled_latent_fp16_ties_exact(gpu, orc):
         lat_o, sc_o, sel_o = orc.route(x16[t], w16, enc_b, swt, sb, k)
         assert np.array_equal(lat[t], lat_o), f"latent of row {t}"
         assert np.array_equal(sc[t], sc_o) and np.array_equal(sel[t], sel_o)
+
+
+def test_route_many_rows_scores_ties_and_cancellation_exact(gpu, orc):
+    """Scores of 8 tokens or more on the matrix cores: outputs that are exact
+    fp16 ties (1 + 2^-11 -> 1, 3 + 2^-10 -> 3) and one whose terms of 65504^2
+    cancel to 0.5 + 2^-11 must leave the fp64 pass to the exact sums.  The
+    latent is x's first R columns exactly (enc_w is the identity, no bias),
+    so the score terms are set directly."""
+    H, R, N, NB, k = 256, 64, 16, 40, 5
+    rng = np.random.default_rng(41)
+    x = (rng.standard_normal((N, H)) * 0.5).astype(np.float16)
+    enc_w = np.zeros((R, H), dtype=np.float16)
+    enc_w[np.arange(R), np.arange(R)] = np.float16(1.0)
+    sw = (rng.standard_normal((NB, R)) * 0.02).astype(np.float16)
+    one, big = np.float16(1.0), np.float16(65504.0)
+    x[3, :R] = 0                     # token 3 x block 7: 1 * 1 + 1 * 2^-11
+    x[3, 0] = x[3, 1] = one
+    sw[7, :] = 0
+    sw[7, 0], sw[7, 1] = one, np.float16(2.0 ** -11)
+    x[9, :R] = 0                     # token 9 x block 11: 1 * 3 + 1 * 2^-10
+    x[9, 0] = x[9, 1] = one
+    sw[11, :] = 0
+    sw[11, 0], sw[11, 1] = np.float16(3.0), np.float16(2.0 ** -10)
+    x[12, :R] = 0                    # token 12 x block 20: 65504^2 - 65504^2 + (0.5 + 2^-11)
+    x[12, 0], x[12, 1], x[12, 2] = big, big, one
+    sw[20, :] = 0
+    sw[20, 0], sw[20, 1], sw[20, 2] = big, -big, np.float16(0.5 + 2.0 ** -11)
+    x16, w16, s16 = x.view(np.uint16), enc_w.view(np.uint16), sw.view(np.uint16)
+    enc_b = np.zeros(R, dtype=np.uint16)
+    sb = np.zeros(NB, dtype=np.uint16)
+    sel, lat, sc = _route_gpu(gpu, x16, w16, enc_b, s16, sb, k)
+    scf = sc.view(np.float16)
+    assert scf[3, 7] == one and scf[9, 11] == np.float16(3.0) and scf[12, 20] == np.float16(0.5 + 2.0 ** -11)
+    for t in range(N):
+        lat_o, sc_o, sel_o = orc.route(x16[t], w16, enc_b, s16, sb, k)
+        assert np.array_equal(lat[t], lat_o), f"latent of row {t}"
+        assert np.array_equal(sc[t], sc_o), f"scores of row {t}"
+        assert np.array_equal(sel[t], sel_o), f"selection of row {t}"
