@@ -95,7 +95,8 @@ __host__ __device__ inline long long dn_extent(const ProjView& v, int blocks, in
 // down one set at the end of a step; step c + 2's weights go out in unit 0,
 // as soon as their set is free, so that they have landed when the move at the
 // end of the step copies them.
-template <int NT, typename IssueW, typename IssueX, typename AmOf>
+// NW: the vector memory instructions of one issue_w.
+template <int NT, int NW, typename IssueW, typename IssueX, typename AmOf>
 __device__ __forceinline__ void dn_gemm(float16_t (&acc)[NT][2], int nst, uint32_t abase, IssueW&& issue_w,
                                         IssueX&& issue_x, AmOf&& am_of) {
   const int lane = threadIdx.x & (kWave - 1);
@@ -133,8 +134,17 @@ __device__ __forceinline__ void dn_gemm(float16_t (&acc)[NT][2], int nst, uint32
     }
     __builtin_amdgcn_sched_barrier(0);
   };
-  auto step_sync = [] {
-    __builtin_amdgcn_s_waitcnt(0);  // vmcnt(0) expcnt(0) lgkmcnt(0)
+  // this wave's token rows of the next step have landed (loads complete in
+  // issue order: only the NW weight loads of step c + 2, issued since, may
+  // still be in flight) and its LDS reads are done; then every wave's.  The
+  // last two steps wait for everything: their weight loads feed no later
+  // step, so the compiler drops them and fewer than NW follow the rows.
+  static_assert(NW >= 1 && NW <= 15, "vmcnt field");
+  auto step_sync = [](bool tail) {
+    if (tail)
+      __builtin_amdgcn_s_waitcnt(0);
+    else
+      __builtin_amdgcn_s_waitcnt(NW | (7 << 4));  // vmcnt(NW) expcnt(7: none) lgkmcnt(0)
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
   };
@@ -161,7 +171,7 @@ __device__ __forceinline__ void dn_gemm(float16_t (&acc)[NT][2], int nst, uint32
   lookup2(p1, W0, S1{});
   __builtin_amdgcn_sched_barrier(0);
 
-  auto step = [&](int c, const RdW& Wc, const RdW& Wn, RdW& Wf) {
+  auto step = [&](int c, const RdW& Wc, const RdW& Wn, RdW& Wf, bool tail) {
     // unit 0: B of MFMA step 1 finished, step 2's looked up
     issue_w(Wf, c + 2);
     read_a(a1, c, 1);
@@ -180,7 +190,7 @@ __device__ __forceinline__ void dn_gemm(float16_t (&acc)[NT][2], int nst, uint32
     lookup2(p0, Wn, S0{});
     mfma_unit(a0, b0);
     // unit 3
-    step_sync();
+    step_sync(tail);
     issue_x(c + 2);
     read_a(a0, c + 1, 0);
     finish2(b0, p0, am_n);
@@ -193,11 +203,17 @@ __device__ __forceinline__ void dn_gemm(float16_t (&acc)[NT][2], int nst, uint32
 #pragma unroll
       for (int u = 0; u < 2; ++u) asm volatile("" : "+a"(acc[mi][u]));
   };
-  for (int c = 0; c < nst; ++c) {
-    step(c, W0, W1, W2);
-    W0 = W1;
-    W1 = W2;
+  // unrolled by the three register sets, whose roles rotate: no set is
+  // copied, so step c + 2's weights only have to land by step c + 1's third
+  // unit (a copy at the end of the step waited for them there)
+  int c = 0;
+  for (; c + 3 <= nst; c += 3) {
+    step(c, W0, W1, W2, false);
+    step(c + 1, W1, W2, W0, false);
+    step(c + 2, W2, W0, W1, false);
   }
+  if (c < nst) step(c, W0, W1, W2, true);
+  if (c + 1 < nst) step(c + 1, W1, W2, W0, true);
   __builtin_amdgcn_s_waitcnt(0);
   mfma_drain();
 }
@@ -339,7 +355,7 @@ __global__ void __launch_bounds__(kDnThreads, 1) k_dg_down(DenseGuardArgs g) {
     }
   // the lane's A fragment address of MFMA step 0 in stage 0: row j, piece 4 kh
   const uint32_t abase = kDnTab + (uint32_t)j * 128u + ((4u * (uint32_t)kh ^ (uint32_t)((j >> 1) & 7)) << 4);
-  dn_gemm<NT>(acc, nst, abase, issue_w, issue_x, am_of);
+  dn_gemm<NT, (DQ ? 3 : 2) * (HOST ? 2 : 1) * 2 - (DQ && HOST ? 2 : 0)>(acc, nst, abase, issue_w, issue_x, am_of);
   // C element r of lane (j, kh), tile (mi, u): token 32 mi + 8 (r / 4) +
   // 4 kh + r % 4, row o0 + 32 u
   float* part = g.part + (long long)s * M * H;
@@ -492,7 +508,7 @@ __global__ void __launch_bounds__(kDnThreads, 1) k_dg_gu2(DenseGuardArgs g) {
       asm volatile("" : "+a"(acc[mi][u]));
     }
   const uint32_t abase = kDnTab + (uint32_t)j * 128u + ((4u * (uint32_t)kh ^ (uint32_t)((j >> 1) & 7)) << 4);
-  dn_gemm<NT>(acc, nst, abase, issue_w, issue_x, am_of);
+  dn_gemm<NT, DQ ? 6 : 4>(acc, nst, abase, issue_w, issue_x, am_of);
   // act = fp16(fp16(silu(fp16(g))) * fp16(u)) for (token, row): C element r
   // of lane (j, kh) is row j of its tile for token 32 mi + 8 (r / 4) + 4 kh +
   // r % 4
