@@ -411,10 +411,12 @@ __global__ void __launch_bounds__(kDnThreads, 1) k_dg_gu2(DenseGuardArgs g) {
   const int t0 = g.t_base + (int)blockIdx.y * 16 * MT;
   const int blk = 4 * (int)blockIdx.x + wave;
   const int nst = H / 64;
-  // the K loop starts at a step that depends on the workgroup (16 starting
-  // points), so that the many rows that share a cache set are not read at
-  // the same columns at the same time
-  const int rot = (int)(((long long)((blockIdx.x >> 3) & 15) * nst) >> 4);
+  // the K loop starts at a step that depends on the workgroup's index within
+  // its XCD (8 starting points), so that the many rows that share a cache
+  // set are not read at the same columns at the same time; the workgroups of
+  // one starting point share their token columns in L2 (16 points and 32
+  // were slower: more token columns fetched per XCD)
+  const int rot = (int)(((long long)((blockIdx.x >> 3) & 7) * nst) >> 3);
   float* c2s = reinterpret_cast<float*>(gu_lds + kGuC2);
 
   rd_table_fill(gu_lds, d.code, tid);
