@@ -905,7 +905,9 @@ size_t nsmlp_dense_mlp_workspace_bytes(int H, int I, int M) {
   if (H <= 0 || I <= 0 || M <= 0) return 0;
   const size_t S = (size_t)dense_guard_splits(H, I / 32, M);
   const size_t Mc = (size_t)(M < kDenseChunk ? M : kDenseChunk);
-  return align_up(kCounterBytes) + align_up(Mc * I * 2) + align_up(S * Mc * H * 4);
+  // the down partials; the gate/up tail's partials use the same space first
+  const size_t part = S * Mc * H * 4, tail = dense_gu_tail_bytes((int)Mc);
+  return align_up(kCounterBytes) + align_up(Mc * I * 2) + align_up(part > tail ? part : tail);
 }
 
 int nsmlp_dense_mlp_slots_f16(const nsmlp_slot_table* table, const void* x, int M, const void* residual, void* out,

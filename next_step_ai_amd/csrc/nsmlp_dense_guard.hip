@@ -14,7 +14,10 @@
 //              tile's tokens in 256 fp32 accumulators; the weights are
 //              decoded to fp16(code * absmax) in registers (each fed to 16
 //              MFMAs), the token rows staged in LDS for the 4 waves; g and u
-//              of a (token, row) meet in one lane, so act is formed there;
+//              of a (token, row) meet in one lane, so act is formed there.
+//              The blocks past the last whole round of the CUs are split in
+//              K over all CUs (fp32 partial sums);
+//   k_dg_gu_fix  adds a split block group's partial sums in K order, act;
 //   k_dg_down  one workgroup per 256 output rows, 256 tokens and one of S
 //              ranges of the intermediate blocks: the same register-decode
 //              GEMM over act and the down columns (two blocks per step);
@@ -91,10 +94,9 @@ __host__ __device__ inline long long dn_extent(const ProjView& v, int blocks, in
 // last unit the wave waits for step c + 1's loads and meets the others at the
 // barrier (every wave has read its last A fragments of stage c & 1), sends
 // step c + 2's token rows into that stage and reads step c + 1's first A
-// fragments.  Three weight register sets: decoded, arrived, in flight, moved
-// down one set at the end of a step; step c + 2's weights go out in unit 0,
-// as soon as their set is free, so that they have landed when the move at the
-// end of the step copies them.
+// fragments.  Three weight register sets (decoded, arrived, in flight) whose
+// roles rotate from step to step; step c + 2's weights go out in unit 0, as
+// soon as their set is free.
 // NW: the vector memory instructions of one issue_w.
 template <int NT, int NW, typename IssueW, typename IssueX, typename AmOf>
 __device__ __forceinline__ void dn_gemm(float16_t (&acc)[NT][2], int nst, uint32_t abase, IssueW&& issue_w,
@@ -400,6 +402,25 @@ __global__ void __launch_bounds__(kDnThreads, 1) k_dg_down(DenseGuardArgs g) {
 constexpr uint32_t kGuC2 = kDnTab + 2u * kDnStage;  // second-level code books [2][256]
 constexpr uint32_t kGuLds = kGuC2 + 2u * 256u * 4u;
 
+// A launch covers one token tile (from t_base); its work is items, item q
+// the 4 consecutive blocks 4 q .. 4 q + 3 (nq = NB / 4 items).  One workgroup
+// per CU: the first gu_full items (whole rounds of the CUs) run one per
+// workgroup over all of K; the rest (gu_tail < CUs items) would leave most CUs
+// idle for a whole K loop, so their K steps are laid end to end and cut into
+// ranges of gu_per steps, one per workgroup (tail workgroup i: steps
+// i gu_per .. + gu_per - 1).  gu_per <= nst, so a range holds at most two
+// segments, each within one item.  A segment that is a whole item forms act;
+// any other writes its fp32 accumulators to slot 2 i + (second segment) of
+// gu_part, and k_dg_gu_fix adds an item's segments in K order and forms act.
+// The split depends on the layer shape and the CU count only, so a token's
+// sums do not depend on how many tokens share the call.
+__device__ __forceinline__ float dg_act(float gsum, float usum) {
+  const float g16 = h2f(f2h(gsum));
+  const float s16 = h2f(f2h(g16 / (1.0f + expf(-g16))));
+  const float u16 = h2f(f2h(usum));
+  return s16 * u16;
+}
+
 template <bool DQ, int MT>
 __global__ void __launch_bounds__(kDnThreads, 1) k_dg_gu2(DenseGuardArgs g) {
   extern __shared__ __attribute__((aligned(16))) uint8_t gu_lds[];  // no static LDS: gu_lds is LDS address 0
@@ -408,15 +429,7 @@ __global__ void __launch_bounds__(kDnThreads, 1) k_dg_gu2(DenseGuardArgs g) {
   const int tid = threadIdx.x, lane = tid & (kWave - 1);
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int H = d.H, I = d.NB * 32, M = g.M;
-  const int t0 = g.t_base + (int)blockIdx.y * 16 * MT;
-  const int blk = 4 * (int)blockIdx.x + wave;
   const int nst = H / 64;
-  // the K loop starts at a step that depends on the workgroup's index within
-  // its XCD (8 starting points), so that the many rows that share a cache
-  // set are not read at the same columns at the same time; the workgroups of
-  // one starting point share their token columns in L2 (16 points and 32
-  // were slower: more token columns fetched per XCD)
-  const int rot = (int)(((long long)((blockIdx.x >> 3) & 7) * nst) >> 3);
   float* c2s = reinterpret_cast<float*>(gu_lds + kGuC2);
 
   rd_table_fill(gu_lds, d.code, tid);
@@ -424,108 +437,185 @@ __global__ void __launch_bounds__(kDnThreads, 1) k_dg_gu2(DenseGuardArgs g) {
     c2s[tid] = d.gate.code2[tid];
     c2s[256 + tid] = d.up.code2[tid];
   }
-  const BlockRef br = resolve_id(d, blk);
-  if (!br.ok && lane == 0) atomicOr(d.status, 1);
+  // this workgroup's item and its virtual steps v0 .. v1 - 1
+  const int wg = (int)blockIdx.x;
+  int item = wg, v0 = 0, v1 = nst, slot = -1, nseg = 1, v1b = 0;
+  if (wg >= g.gu_full) {
+    const int i = wg - g.gu_full, per = g.gu_per;
+    const long long s0 = (long long)i * per, s1 = min(s0 + per, (long long)g.gu_tail * nst);
+    const int a = (int)(s0 / nst);
+    item = g.gu_full + a;
+    v0 = (int)(s0 - (long long)a * nst);
+    v1 = (int)min((long long)nst, s1 - (long long)a * nst);
+    slot = 2 * i;
+    if (s1 > (long long)(a + 1) * nst) {  // the range runs into the next item
+      nseg = 2;
+      v1b = (int)(s1 - (long long)(a + 1) * nst);
+    }
+  }
   __syncthreads();
 
   const int j = lane & 31, kh = lane >> 5;
   const uint32_t rs = (uint32_t)d.gate.row_stride, A = (uint32_t)d.gate.abs_row_stride;
-  rsrc_t rw[2], ra[2], r2[2];
-#pragma unroll
-  for (int u = 0; u < 2; ++u) {
-    const ProjView& pv = u ? d.up : d.gate;
-    const ProjView& hv = u ? d.host_up : d.host_gate;
-    // the block is the wave's (blk is uniform): scalar descriptors
-    rw[u] = make_rsrc_uniform((br.dev ? pv.packed : hv.packed) + br.q * pv.blk_stride, br.ok ? (int)(32 * rs) : 0);
-    if constexpr (DQ) {
-      ra[u] = make_rsrc_uniform((br.dev ? pv.qabsmax : hv.qabsmax) + br.q * pv.abs_blk_stride,
-                                br.ok ? (int)(32 * A) : 0);
-      r2[u] = make_rsrc_uniform(pv.absmax2,
-                                br.ok ? (int)((((long long)I * A + (1 << d.dq_shift) - 1) >> d.dq_shift) * 4) : 0);
-    } else {
-      ra[u] = make_rsrc_uniform((br.dev ? pv.absmax : hv.absmax) + br.q * pv.abs_blk_stride,
-                                br.ok ? (int)(32 * A * 4) : 0);
-      r2[u] = ra[u];
-    }
-  }
   const rsrc_t rx = make_rsrc(g.x, (int)((long long)M * H * 2));
-  // per-lane parts of the weight and absmax offsets (row j); double-quantised
-  // u8 absmax codes are stored in row pairs ([row / 2][entry][row % 2])
-  const uint32_t wv = (uint32_t)j * rs + 16u * (uint32_t)kh;
-  const uint32_t qv = DQ ? ((uint32_t)(j >> 1) * A) * 2u + (uint32_t)(j & 1) : (uint32_t)j * A * 4u;
-  const uint32_t fv = (32u * (uint32_t)blk + (uint32_t)j) * A;  // absmax index of row j, entry 0
-  auto issue_w = [&](RdW& W, int c) {
-    const bool live = c < nst;
-    c = c + rot < nst ? c + rot : c + rot - nst;
-    const uint32_t ce = ((uint32_t)(64 * c) + 32u * (uint32_t)kh) >> d.qbs_shift;  // the lane's absmax entry
-    const uint32_t wo = live ? wv : kOffNone, qo = live ? qv + (DQ ? 2u : 4u) * ce : kOffNone;
-    W.ok = br.ok;
+  const int t0 = g.t_base;
+  auto run = [&](const int quad, const int v0, const int v1, const int slot) {
+    const int blk = 4 * quad + wave;
+    const int len = v1 - v0;
+    // the K loop of an item starts at a step that depends on its quad's index
+    // within its XCD (8 starting points), so that the many rows that share a
+    // cache set are not read at the same columns at the same time; the
+    // workgroups of one starting point share their token columns in L2 (16
+    // points and 32 were slower: more token columns fetched per XCD).  A
+    // segment's virtual step c is the item's step (v0 + c + rot) mod nst.
+    const int rot = (int)(((long long)((quad >> 3) & 7) * nst) >> 3);
+    const int pbase = (v0 + rot) % nst;
+    const BlockRef br = resolve_id(d, blk);
+    if (!br.ok && lane == 0) atomicOr(d.status, 1);
+
+    rsrc_t rw[2], ra[2], r2[2];
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
-      // temporal loads: a row's 128-byte line serves 4 steps (an
-      // nontemporal load fetched it again for each)
-      W.w[u] = buf_ld16c(rw[u], wo, 32u * (uint32_t)c);
+      const ProjView& pv = u ? d.up : d.gate;
+      const ProjView& hv = u ? d.host_up : d.host_gate;
+      // the block is the wave's (blk is uniform): scalar descriptors
+      rw[u] = make_rsrc_uniform((br.dev ? pv.packed : hv.packed) + br.q * pv.blk_stride, br.ok ? (int)(32 * rs) : 0);
       if constexpr (DQ) {
-        W.qa[u] = buf_ldu8c(ra[u], qo, 0);
-        const uint32_t fo = ((fv + ce) >> d.dq_shift) * 4u;
-        W.a[u] = buf_ldfc(r2[u], live ? fo : kOffNone, 0);
+        ra[u] = make_rsrc_uniform((br.dev ? pv.qabsmax : hv.qabsmax) + br.q * pv.abs_blk_stride,
+                                  br.ok ? (int)(32 * A) : 0);
+        r2[u] = make_rsrc_uniform(pv.absmax2,
+                                  br.ok ? (int)((((long long)I * A + (1 << d.dq_shift) - 1) >> d.dq_shift) * 4) : 0);
       } else {
-        W.a[u] = buf_ldfc(ra[u], qo, 0);
+        ra[u] = make_rsrc_uniform((br.dev ? pv.absmax : hv.absmax) + br.q * pv.abs_blk_stride,
+                                  br.ok ? (int)(32 * A * 4) : 0);
+        r2[u] = ra[u];
       }
     }
-  };
-  // token rows of step c into stage c & 1: load i of wave w fills rows
-  // 32 i + 8 w .. + 7 (lane l: row + l / 8, slot l % 8); row i's offset is
-  // load 0's plus 32 i rows (a scalar offset)
-  const int arow = 8 * wave + (lane >> 3);
-  const uint32_t apiece = (uint32_t)((lane & 7) ^ ((arow >> 1) & 7));
-  const uint32_t xrow = ((uint32_t)(t0 + arow) * (uint32_t)H + 8u * apiece) * 2u;
-  auto issue_x = [&](int c) {
-    const int tlim = c < nst ? M - t0 - arow : 0;  // rows 32 i with 32 i < tlim are tokens of this call
-    const int cp = c + rot < nst ? c + rot : c + rot - nst;
-    const uint32_t xo = xrow + 128u * (uint32_t)cp;
-    const uint32_t sb = kDnTab + (uint32_t)(c & 1) * kDnStage;
+    // per-lane parts of the weight and absmax offsets (row j); double-quantised
+    // u8 absmax codes are stored in row pairs ([row / 2][entry][row % 2])
+    const uint32_t wv = (uint32_t)j * rs + 16u * (uint32_t)kh;
+    const uint32_t qv = DQ ? ((uint32_t)(j >> 1) * A) * 2u + (uint32_t)(j & 1) : (uint32_t)j * A * 4u;
+    const uint32_t fv = (32u * (uint32_t)blk + (uint32_t)j) * A;  // absmax index of row j, entry 0
+    auto issue_w = [&](RdW& W, int c) {
+      const bool live = c < len;
+      c = pbase + c < nst ? pbase + c : pbase + c - nst;
+      const uint32_t ce = ((uint32_t)(64 * c) + 32u * (uint32_t)kh) >> d.qbs_shift;  // the lane's absmax entry
+      const uint32_t wo = live ? wv : kOffNone, qo = live ? qv + (DQ ? 2u : 4u) * ce : kOffNone;
+      W.ok = br.ok;
 #pragma unroll
-    for (int i = 0; i < MT / 2; ++i) {
-      const uint32_t xi = 32 * i < tlim ? xo : kOffNone;
-      ld_lds16s(rx, gu_lds + sb + (32 * i + 8 * wave) * 128, xi, 64u * (uint32_t)i * (uint32_t)H);
-    }
-  };
-  auto am_of = [&](const RdW& W, float (&am)[2]) {
+      for (int u = 0; u < 2; ++u) {
+        // temporal loads: a row's 128-byte line serves 4 steps (an
+        // nontemporal load fetched it again for each)
+        W.w[u] = buf_ld16c(rw[u], wo, 32u * (uint32_t)c);
+        if constexpr (DQ) {
+          W.qa[u] = buf_ldu8c(ra[u], qo, 0);
+          const uint32_t fo = ((fv + ce) >> d.dq_shift) * 4u;
+          W.a[u] = buf_ldfc(r2[u], live ? fo : kOffNone, 0);
+        } else {
+          W.a[u] = buf_ldfc(ra[u], qo, 0);
+        }
+      }
+    };
+    // token rows of step c into stage c & 1: load i of wave w fills rows
+    // 32 i + 8 w .. + 7 (lane l: row + l / 8, slot l % 8); row i's offset is
+    // load 0's plus 32 i rows (a scalar offset)
+    const int arow = 8 * wave + (lane >> 3);
+    const uint32_t apiece = (uint32_t)((lane & 7) ^ ((arow >> 1) & 7));
+    const uint32_t xrow = ((uint32_t)(t0 + arow) * (uint32_t)H + 8u * apiece) * 2u;
+    auto issue_x = [&](int c) {
+      const int tlim = c < len ? M - t0 - arow : 0;  // rows 32 i with 32 i < tlim are tokens of this call
+      const int cp = pbase + c < nst ? pbase + c : pbase + c - nst;
+      const uint32_t xo = xrow + 128u * (uint32_t)cp;
+      const uint32_t sb = kDnTab + (uint32_t)(c & 1) * kDnStage;
 #pragma unroll
-    for (int u = 0; u < 2; ++u) {
-      float v = W.a[u];
-      if constexpr (DQ) v = dq_absmax(c2s[u * 256 + W.qa[u]], W.a[u], u ? d.up.offset : d.gate.offset);
-      am[u] = W.ok ? v : 0.0f;
-    }
-  };
+      for (int i = 0; i < MT / 2; ++i) {
+        const uint32_t xi = 32 * i < tlim ? xo : kOffNone;
+        ld_lds16s(rx, gu_lds + sb + (32 * i + 8 * wave) * 128, xi, 64u * (uint32_t)i * (uint32_t)H);
+      }
+    };
+    auto am_of = [&](const RdW& W, float (&am)[2]) {
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        float v = W.a[u];
+        if constexpr (DQ) v = dq_absmax(c2s[u * 256 + W.qa[u]], W.a[u], u ? d.up.offset : d.gate.offset);
+        am[u] = W.ok ? v : 0.0f;
+      }
+    };
 
-  float16_t acc[NT][2];
+    float16_t acc[NT][2];
 #pragma unroll
-  for (int mi = 0; mi < NT; ++mi)
+    for (int mi = 0; mi < NT; ++mi)
 #pragma unroll
-    for (int u = 0; u < 2; ++u) {
+      for (int u = 0; u < 2; ++u) {
 #pragma unroll
-      for (int r = 0; r < 16; ++r) acc[mi][u][r] = 0.0f;
-      asm volatile("" : "+a"(acc[mi][u]));
+        for (int r = 0; r < 16; ++r) acc[mi][u][r] = 0.0f;
+        asm volatile("" : "+a"(acc[mi][u]));
+      }
+    const uint32_t abase = kDnTab + (uint32_t)j * 128u + ((4u * (uint32_t)kh ^ (uint32_t)((j >> 1) & 7)) << 4);
+    dn_gemm<NT, DQ ? 6 : 4>(acc, len, abase, issue_w, issue_x, am_of);
+    if (slot < 0 || len == nst) {
+      // act = fp16(fp16(silu(fp16(g))) * fp16(u)) for (token, row): C element
+      // r of lane (j, kh) is row j of its tile for token 32 mi + 8 (r / 4) +
+      // 4 kh + r % 4
+#pragma unroll
+      for (int mi = 0; mi < NT; ++mi) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int t = t0 + 32 * mi + 8 * (r >> 2) + 4 * kh + (r & 3);
+          if (t < M) g.act[(long long)t * I + 32 * blk + j] = f2h(dg_act(acc[mi][0][r], acc[mi][1][r]));
+        }
+      }
+    } else {
+      // the piece's sums in fragment order: [slot][wave][mi][u][r][lane]
+      float* pp = g.gu_part + ((size_t)slot * 4 + (size_t)wave) * (size_t)(NT * 2 * 16 * 64) + lane;
+#pragma unroll
+      for (int mi = 0; mi < NT; ++mi)
+#pragma unroll
+        for (int u = 0; u < 2; ++u)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) pp[((mi * 2 + u) * 16 + r) * 64] = acc[mi][u][r];
     }
-  const uint32_t abase = kDnTab + (uint32_t)j * 128u + ((4u * (uint32_t)kh ^ (uint32_t)((j >> 1) & 7)) << 4);
-  dn_gemm<NT, DQ ? 6 : 4>(acc, nst, abase, issue_w, issue_x, am_of);
-  // act = fp16(fp16(silu(fp16(g))) * fp16(u)) for (token, row): C element r
-  // of lane (j, kh) is row j of its tile for token 32 mi + 8 (r / 4) + 4 kh +
-  // r % 4
+  };
+  run(item, v0, v1, slot);
+  if (nseg > 1) {
+    __syncthreads();  // every wave is done with the token stages before the next loads refill them
+    run(item + 1, 0, v1b, slot + 1);
+  }
+}
+
+// act of the split tail items: workgroup (tail item a, wave w, 4 token tiles
+// from 4 mg); a thread adds its (tile, lane) sums over the item's segments in
+// K order (tail workgroups i_lo .. i_hi, the segment of workgroup i being its
+// first or its second) and forms act as k_dg_gu2.
+template <int MT>
+__global__ void __launch_bounds__(256) k_dg_gu_fix(DenseGuardArgs g) {
+  constexpr int NT = MT / 2, MG = (NT + 3) / 4;
+  const int nst = g.d.H / 64, I = g.d.NB * 32;
+  const int b = (int)blockIdx.x;
+  const int a = b / (4 * MG), wave = (b / MG) & 3, mi = (b % MG) * 4 + (int)(threadIdx.x >> 6);
+  const int lane = (int)threadIdx.x & 63;
+  if (mi >= NT) return;
+  const long long per = g.gu_per, s0 = (long long)a * nst;
+  const int i_lo = (int)(s0 / per), i_hi = (int)((s0 + nst - 1) / per);
+  float gs[16], us[16];
 #pragma unroll
-  for (int mi = 0; mi < NT; ++mi) {
+  for (int r = 0; r < 16; ++r) gs[r] = us[r] = 0.0f;
+  for (int i = i_lo; i <= i_hi; ++i) {
+    const int slot = 2 * i + ((long long)i * per / nst == a ? 0 : 1);
+    const float* pp = g.gu_part + (((size_t)slot * 4 + (size_t)wave) * NT + (size_t)mi) * (size_t)(2 * 16 * 64) + lane;
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
-      const int t = t0 + 32 * mi + 8 * (r >> 2) + 4 * kh + (r & 3);
-      if (t < M) {
-        const float g16 = h2f(f2h(acc[mi][0][r]));
-        const float s16 = h2f(f2h(g16 / (1.0f + expf(-g16))));
-        const float u16 = h2f(f2h(acc[mi][1][r]));
-        g.act[(long long)t * I + 32 * blk + j] = f2h(s16 * u16);
-      }
+      gs[r] += pp[r * 64];
+      us[r] += pp[(16 + r) * 64];
     }
+  }
+  const int quad = g.gu_full + a;
+  const int t0 = g.t_base, blk = 4 * quad + wave;
+  const int j = lane & 31, kh = lane >> 5;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    const int t = t0 + 32 * mi + 8 * (r >> 2) + 4 * kh + (r & 3);
+    if (t < g.M) g.act[(long long)t * I + 32 * blk + j] = f2h(dg_act(gs[r], us[r]));
   }
 }
 
@@ -547,6 +637,39 @@ using DgFn = void (*)(DenseGuardArgs);
 // [dq][MT / 4 - 1 of the 16 MT-token tile]
 const DgFn kDgGu2[2][4] = {{k_dg_gu2<false, 4>, k_dg_gu2<false, 8>, k_dg_gu2<false, 12>, k_dg_gu2<false, 16>},
                            {k_dg_gu2<true, 4>, k_dg_gu2<true, 8>, k_dg_gu2<true, 12>, k_dg_gu2<true, 16>}};
+const DgFn kDgGuFix[4] = {k_dg_gu_fix<4>, k_dg_gu_fix<8>, k_dg_gu_fix<12>, k_dg_gu_fix<16>};
+constexpr int kGuTailWgs = 256;  // CUs counted at most (the partial slots, 2 per tail workgroup, are sized for it)
+
+// CUs of the current device (one gate/up workgroup each), at most kGuTailWgs
+int dg_tail_wgs() {
+  static int cus[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return kGuTailWgs;
+  if (cus[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = kGuTailWgs;
+    cus[dev] = n < kGuTailWgs ? n : kGuTailWgs;
+  }
+  return cus[dev];
+}
+
+// gate/up of one MT-token tile (from g.t_base): whole rounds of the CUs
+// first, then the rest's K steps in equal ranges over the CUs (see k_dg_gu2);
+// the fix-up runs before the next launch reuses the partial slots
+void launch_gu2(const DenseGuardArgs& g, int MT, hipStream_t st) {
+  const int items = g.d.NB / 4;
+  const int W = dg_tail_wgs(), nst = g.d.H / 64;
+  DenseGuardArgs a = g;
+  a.gu_full = items / W * W;
+  a.gu_tail = items - a.gu_full;
+  a.gu_per = a.gu_tail > 0 ? (int)(((long long)a.gu_tail * nst + W - 1) / W) : nst;  // <= nst: gu_tail < W
+  const int wt = a.gu_tail > 0 ? (int)(((long long)a.gu_tail * nst + a.gu_per - 1) / a.gu_per) : 0;
+  kDgGu2[g.d.dq ? 1 : 0][MT / 4 - 1]<<<dim3((unsigned)(a.gu_full + wt)), dim3(kDnThreads), kGuLds, st>>>(a);
+  if (a.gu_tail > 0 && a.gu_per < nst) {  // every tail item is split
+    const int mg = (MT / 2 + 3) / 4;
+    kDgGuFix[MT / 4 - 1]<<<dim3((unsigned)(a.gu_tail * 4 * mg)), dim3(256), 0, st>>>(a);
+  }
+}
 // [dq][MT - 1 of the 64 MT-token tile]
 // [dq][host copies][MT / 4 - 1 of the 16 MT-token tile]
 const DgFn kDgDown[2][2][4] = {
@@ -571,6 +694,12 @@ void dg_set_lds() {
 }
 
 }  // namespace
+
+size_t dense_gu_tail_bytes(int M) {
+  const int mc = M < kDnTok ? M : kDnTok;
+  const int nt = 2 * ((mc + 63) / 64);  // accumulator tiles of the widest token tile of the call
+  return (size_t)2 * kGuTailWgs * 4 * nt * 2 * 16 * 64 * 4;
+}
 
 // k_dg_down and k_dg_gu2 read their code-pair table and token stages at
 // fixed LDS addresses (immediate offsets from 0): that holds only while the
@@ -651,13 +780,14 @@ void launch_dense_guard(const DenseGuardArgs& g, hipStream_t st) {
   // 192-token tile that holds it (per token the same sums, bit for bit)
   const int full = g.M / kDnTok, rest = g.M - full * kDnTok;
   DenseGuardArgs a = g;
-  if (full > 0) {
-    a.t_base = 0;
-    kDgGu2[g.d.dq ? 1 : 0][3]<<<dim3((unsigned)(g.d.NB / 4), (unsigned)full), dim3(kDnThreads), kGuLds, st>>>(a);
+  a.gu_part = g.part;  // free until the down GEMM writes its partials there
+  for (int ty = 0; ty < full; ++ty) {
+    a.t_base = ty * kDnTok;
+    launch_gu2(a, 16, st);
   }
   if (rest > 0) {
     a.t_base = full * kDnTok;
-    kDgGu2[g.d.dq ? 1 : 0][(rest + 63) / 64 - 1]<<<dim3((unsigned)(g.d.NB / 4)), dim3(kDnThreads), kGuLds, st>>>(a);
+    launch_gu2(a, 4 * ((rest + 63) / 64), st);
   }
   launch_dense_down(g, st);
 }

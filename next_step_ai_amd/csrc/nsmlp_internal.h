@@ -804,8 +804,17 @@ struct DenseGuardArgs {
   // a block with no tokens has an all-zero act column and its down weights
   // are not read (nullptr: every block is read)
   const int32_t* offsets;
+  // gate/up work split (set by the launcher): gu_full whole items first,
+  // then the K steps of gu_tail items in ranges of gu_per steps; the split
+  // items' fp32 sums in gu_part (the down partials' space, free until the
+  // down GEMM)
+  int gu_full, gu_tail, gu_per;
+  float* gu_part;
 };
 void launch_dense_guard(const DenseGuardArgs& g, hipStream_t s);
+// Bytes of the gate/up tail's partial sums for a dense call of M tokens per
+// chunk (g.part must hold at least this many).
+size_t dense_gu_tail_bytes(int M);
 // The down GEMM and the final sum alone, over g.act (the prefill's dense path).
 void launch_dense_down(const DenseGuardArgs& g, hipStream_t s);
 // Whether the down GEMM takes this table with S block ranges: every slot and

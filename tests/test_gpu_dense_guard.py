@@ -99,6 +99,38 @@ def test_dense_mlp_matches_torch_restatement_two_token_tiles(gpu, orc):
     assert worst <= 1.0
 
 
+def test_dense_mlp_split_block_groups_and_batch_invariance(gpu, orc):
+    """1664 blocks = 416 groups of 4: on 256 CUs, 256 groups run whole over K
+    and the other 160 are split in K over all the CUs (their fp32 partial sums
+    added in K order by a second kernel).  Three token tiles (600 tokens)
+    against the float64 torch restatement, and each tile's rows bit-identical
+    to a call over that tile alone: the split depends on the layer shape, not
+    on how many tokens share the call."""
+    from next_step_ai_amd.synth import make_synthetic_layer, synth_normal_f16
+
+    H, I, R, M = 1024, 53248, 16, 600
+    print(f"dense guard split groups H={H} I={I} M={M}", flush=True)
+    L = make_synthetic_layer(H=H, I=I, R=R, seed=161, device=gpu)
+    table = L.slot_table()
+    x = synth_normal_f16(162, (M, H), 1.0, gpu)
+    y = table.dense_mlp(x)
+    tiles = ((0, 256), (256, 512), (512, 600))
+    ys = [table.dense_mlp(x[a:b].contiguous()) for a, b in tiles]
+    code = torch.tensor(orc.nf4_code(), device=gpu)
+    ref = _torch_dense_guard(L, x, code)
+    torch.cuda.synchronize()
+    got = y.double()
+    e = float(torch.linalg.norm(got - ref) / torch.linalg.norm(ref))
+    ulp = torch.abs(ref.half().double()).clamp_min(2.0 ** -14) * 2.0 ** -10
+    tol = 4 * ulp + 1e-3 * ref.abs().amax(dim=1, keepdim=True)
+    worst = float(((got - ref).abs() / tol).max())
+    print(f"  relL2(gpu, torch fp64 restatement)={e:.3e} worst |err|/tol={worst:.3f}", flush=True)
+    assert e <= 1e-3
+    assert worst <= 1.0
+    for (a, b), yt in zip(tiles, ys):
+        assert torch.equal(y[a:b], yt), f"tokens {a}..{b} differ from a call over them alone"
+
+
 def test_dense_mlp_formats_residency_and_residual(gpu):
     from next_step_ai_amd.synth import make_synthetic_layer, synth_normal_f16
 
