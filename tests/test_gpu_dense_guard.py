@@ -131,6 +131,34 @@ def test_dense_mlp_split_block_groups_and_batch_invariance(gpu, orc):
         assert torch.equal(y[a:b], yt), f"tokens {a}..{b} differ from a call over them alone"
 
 
+def test_dense_mlp_405b_shape_matches_torch_restatement(gpu, orc):
+    """The dense-guard workload itself (hidden 16384, intermediate 53248, 256
+    tokens): 256 block groups run whole and 160 are split in K over the CUs.
+    Every output against the float64 torch restatement, and a second call
+    bit-identical."""
+    from next_step_ai_amd.synth import make_synthetic_layer, synth_normal_f16
+
+    H, I, R, M = 16384, 53248, 64, 256
+    print(f"dense guard 405B shape H={H} I={I} M={M}", flush=True)
+    L = make_synthetic_layer(H=H, I=I, R=R, seed=171, device=gpu, double_quant=True)
+    table = L.slot_table()
+    x = synth_normal_f16(172, (M, H), 1.0, gpu)
+    y = table.dense_mlp(x)
+    y2 = table.dense_mlp(x)
+    torch.cuda.synchronize()
+    assert torch.equal(y, y2), "dense MLP is not deterministic"
+    code = torch.tensor(orc.nf4_code(), device=gpu)
+    ref = _torch_dense_guard(L, x, code)
+    got = y.double()
+    e = float(torch.linalg.norm(got - ref) / torch.linalg.norm(ref))
+    ulp = torch.abs(ref.half().double()).clamp_min(2.0 ** -14) * 2.0 ** -10
+    tol = 4 * ulp + 1e-3 * ref.abs().amax(dim=1, keepdim=True)
+    worst = float(((got - ref).abs() / tol).max())
+    print(f"  relL2(gpu, torch fp64 restatement)={e:.3e} worst |err|/tol={worst:.3f}", flush=True)
+    assert e <= 1e-3
+    assert worst <= 1.0
+
+
 def test_dense_mlp_formats_residency_and_residual(gpu):
     from next_step_ai_amd.synth import make_synthetic_layer, synth_normal_f16
 
