@@ -437,7 +437,9 @@ __global__ void __launch_bounds__(kDnThreads, 1) k_dg_gu2(DenseGuardArgs g) {
     c2s[tid] = d.gate.code2[tid];
     c2s[256 + tid] = d.up.code2[tid];
   }
-  // this workgroup's item and its virtual steps v0 .. v1 - 1
+  // this workgroup's first segment: item, virtual steps v0 .. v1 - 1, its
+  // partial slot (-1: a whole item); with nseg = 2 also steps 0 .. v1b - 1 of
+  // the next item (slot + 1)
   const int wg = (int)blockIdx.x;
   int item = wg, v0 = 0, v1 = nst, slot = -1, nseg = 1, v1b = 0;
   if (wg >= g.gu_full) {
@@ -566,7 +568,7 @@ __global__ void __launch_bounds__(kDnThreads, 1) k_dg_gu2(DenseGuardArgs g) {
         }
       }
     } else {
-      // the piece's sums in fragment order: [slot][wave][mi][u][r][lane]
+      // the segment's sums in fragment order: [slot][wave][mi][u][r][lane]
       float* pp = g.gu_part + ((size_t)slot * 4 + (size_t)wave) * (size_t)(NT * 2 * 16 * 64) + lane;
 #pragma unroll
       for (int mi = 0; mi < NT; ++mi)
