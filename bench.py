@@ -531,7 +531,7 @@ def run_dense_guard(args) -> int:
         "dense_mlp_us": round(us, 3),
         "roofline": {"bound": "mfma", "achieved": round(flop / (us * 1e-6) / 1e12, 2), "peak": PEAK_F16_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(flop / (us * 1e-6) / 1e12 / PEAK_F16_TFLOPS, 4),
-                     "traffic": None, "flop": flop, "kernels": "k_dg_gu2 + k_dg_down + k_dg_fin"},
+                     "traffic": None, "flop": flop, "kernels": "k_dg_gu2 + k_dg_gu_fix + k_dg_down + k_dg_fin"},
     })
     print(json.dumps(res), flush=True)
     return 0
