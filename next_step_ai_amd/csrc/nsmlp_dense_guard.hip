@@ -465,12 +465,13 @@ __global__ void __launch_bounds__(kDnThreads, 1) k_dg_gu2(DenseGuardArgs g) {
     const int blk = 4 * quad + wave;
     const int len = v1 - v0;
     // the K loop of an item starts at a step that depends on its quad's index
-    // within its XCD (8 starting points), so that the many rows that share a
+    // within its XCD (4 starting points), so that the many rows that share a
     // cache set are not read at the same columns at the same time; the
-    // workgroups of one starting point share their token columns in L2 (16
-    // points and 32 were slower: more token columns fetched per XCD).  A
-    // segment's virtual step c is the item's step (v0 + c + rot) mod nst.
-    const int rot = (int)(((long long)((quad >> 3) & 7) * nst) >> 3);
+    // workgroups of one starting point share their token columns in L2 (8,
+    // 16 and 32 points were slower: more token columns fetched per XCD; 1 and
+    // 2 too).  A segment's virtual step c is the item's step (v0 + c + rot)
+    // mod nst.
+    const int rot = (int)(((long long)((quad >> 3) & 3) * nst) >> 2);
     const int pbase = (v0 + rot) % nst;
     const BlockRef br = resolve_id(d, blk);
     if (!br.ok && lane == 0) atomicOr(d.status, 1);
